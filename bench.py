@@ -1,0 +1,240 @@
+#!/usr/bin/env python3
+"""Benchmark of neso's hot path on one MI355X: prints ONE JSON line.
+
+A "step" is one FA2 forward launch over BASELINE's headline workload
+(B=1, H=16, N=2048, d=64, non-causal, fp16 in / fp32 out), inputs resident
+in HBM.  ``value`` = 4*B*H*N^2*d / (ms_per_step) in TFLOP/s.  The same line
+carries:
+
+* ``roofline`` for that kernel against dense-fp16 MFMA peak (2516.6 TFLOP/s
+  = 256 CU x 2.4 GHz x 4096 FLOP/clk), from HIP events recorded on the
+  stream the kernel runs on;
+* ``cpu_baseline``: the CPU oracle (torch fp32, all host threads) on the
+  same workload, rank 0 only;
+* ``qmatmul``: the int4 qmatmul at M=1, K=4096, N=11008 in HBM GB/s
+  (algorithmic bytes K*N/2 + (K/32)*N*2 + M*K*2 + M*N*2), timed over 16
+  rotated weight copies (> 256 MiB, so the Infinity Cache cannot hold them)
+  with its own roofline against 8 TB/s and its CPU baseline;
+* ``sweep``: the other BASELINE configs (FA2 N sweep, d=128 causal, rel-pos
+  N=1500, qmatmul M=16/256), one entry each.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+MFMA_F16_PEAK_TFLOPS = 2516.6  # 256 CUs * 2.4 GHz * 4096 dense fp16 FLOP/clk/CU
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
+METRIC = "FA2 fwd TFLOP/s (d64,N2048) + % MFMA peak; int4 qmatmul HBM GB/s"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def time_launches(launch, steps, warmup, torch):
+    """Run ``launch(i)`` warmup + steps times; return ms per launch over the timed steps.
+
+    Events are recorded on torch's current stream, which is the stream the
+    launchers enqueue on.
+    """
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(steps):
+        launch(i)
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / steps
+
+
+def cpu_time(fn, reps):
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def fa2_case(neso_amd, torch, I, B, H, N, d, causal, steps, warmup, seed=0):
+    from oracle import attention as A  # FLOP formula only
+    q, k, v = (t.cuda() for t in I.fa2_inputs(B, H, N, d, seed=seed))
+    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    ms = time_launches(lambda i: neso_amd.attention(q, k, v, causal=causal, out=out), steps,
+                       warmup, torch)
+    flop = A.flops(B, H, N, d, causal)
+    return ms, flop / (ms * 1e-3) / 1e12, (q, k, v)
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        return 2
+    import torch
+
+    import neso_amd
+    from oracle import inputs as I
+
+    torch.manual_seed(0)
+    dev = torch.cuda.get_device_properties(0)
+    log(f"device {dev.name} {dev.gcnArchName} CUs={dev.multi_processor_count}")
+
+    # ---- headline: FA2 forward, B1 H16 N2048 d64 non-causal ----
+    hb = I.FA2_HEADLINE
+    ms, tflops, (q, k, v) = fa2_case(neso_amd, torch, I, hb["B"], hb["H"], hb["N"], hb["d"],
+                                     False, args.steps, args.warmup)
+    log(f"fa2 headline {ms * 1e3:.2f} us/launch {tflops:.1f} TFLOP/s")
+    flop = 4.0 * hb["B"] * hb["H"] * hb["N"] ** 2 * hb["d"]
+    result = {
+        "metric": METRIC,
+        "value": round(tflops, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "flash_attention_fwd B=1 H=16 N=2048 d=64 non-causal, "
+                               "fp16 Q/K/V ~ N(0,1), fp32 accumulation and output",
+                   "B": 1, "H": 16, "N": 2048, "d": 64, "causal": False},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 3),
+                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "fa2_fwd_kernel<64,false,0,false>",
+                     "algorithmic_flop_per_launch": flop},
+    }
+
+    # ---- int4 qmatmul, M=1 (HBM-bound), rotated weights ----
+    qc = I.QMM_CONFIGS[0]
+    result["qmatmul"] = qmm_case(neso_amd, torch, I, qc, args.steps, args.warmup,
+                                 rotate=16, want_cpu=not args.no_cpu)
+    log(f"qmm M=1 {result['qmatmul']['value']:.1f} GB/s")
+
+    # ---- CPU baseline (rank 0, N=1): the oracle on the same workload ----
+    if not args.no_cpu:
+        from oracle import attention as A
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        qc_, kc_, vc_ = (t.cpu() for t in (q, k, v))
+        sec = cpu_time(lambda: A.attention(qc_, kc_, vc_, 1 / 8), reps=3)
+        result["cpu_baseline"] = {
+            "value": round(flop / sec / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": "oracle.attention (torch fp32 CPU, chunked rows) on the full headline "
+                      "workload B1 H16 N2048 d64, median of 3 after 1 warm-up",
+            "seconds_per_step": round(sec, 4)}
+        log(f"cpu baseline {sec:.3f} s/step")
+
+    if not args.no_sweep:
+        result["sweep"] = sweep(neso_amd, torch, I, max(20, args.steps // 4), 5)
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def qmm_case(neso_amd, torch, I, cfg, steps, warmup, rotate=1, want_cpu=False):
+    from oracle import qmatmul as Q
+    import numpy as np
+    M, K, N = cfg["M"], cfg["K"], cfg["N"]
+    x, codes, scales = I.qmatmul_inputs(M, K, N, seed=0)
+    words = torch.from_numpy(Q.pack_int4(codes.numpy()))
+    xs = x.cuda()
+    ws = [words.cuda() for _ in range(rotate)]
+    ss = [scales.cuda() for _ in range(rotate)]
+    y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    ms = time_launches(
+        lambda i: neso_amd.w4a16_matmul(xs, ws[i % rotate], ss[i % rotate], y, M, N, K, K, N),
+        steps, warmup, torch)
+    nbytes = Q.algorithmic_bytes(M, N, K)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    tflops = Q.flops(M, N, K) / (ms * 1e-3) / 1e12
+    out = {"metric": "int4 qmatmul HBM GB/s", "value": round(gbs, 2), "unit": "GB/s",
+           "ms_per_step": round(ms, 6), "tflops": round(tflops, 3),
+           "config": {"workload": f"w4a16_matmul M={M} K={K} N={N} group=32 zero=8, fp16 "
+                                  f"X, fp16 out, {rotate} rotated weight copies",
+                      "M": M, "K": K, "N": N},
+           "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
+                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "algorithmic_bytes_per_launch": nbytes}}
+    if want_cpu:
+        threads = os.cpu_count() or 1
+        torch.set_num_threads(threads)
+        xc = x.float()
+        wdq = torch.from_numpy(Q.dequant_int4(words.numpy(), scales.numpy(), dtype=np.float32))
+
+        def full():
+            w = torch.from_numpy(Q.dequant_int4(words.numpy(), scales.numpy(), dtype=np.float32))
+            return xc @ w.T
+
+        t_full = cpu_time(full, reps=3)
+        t_mm = cpu_time(lambda: xc @ wdq.T, reps=5)
+        out["cpu_baseline"] = {
+            "value": round(nbytes / t_full / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": "oracle dequant_int4 (numpy) + torch fp32 matmul on the full M=1 "
+                      "workload, median of 3; matmul-only with pre-dequantised weights in "
+                      "matmul_only_gbs",
+            "matmul_only_gbs": round(nbytes / t_mm / 1e9, 3)}
+    return out
+
+
+def sweep(neso_amd, torch, I, steps, warmup):
+    rows = []
+    for cfg in I.FA2_SWEEP:
+        ms, tf, _ = fa2_case(neso_amd, torch, I, cfg["B"], cfg["H"], cfg["N"], cfg["d"],
+                             cfg["causal"], steps, warmup)
+        rows.append({"kernel": "fa2", **cfg, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
+                     "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+    c = I.FA2_D128
+    ms, tf, _ = fa2_case(neso_amd, torch, I, c["B"], c["H"], c["N"], c["d"], c["causal"],
+                         max(5, steps // 4), 2)
+    rows.append({"kernel": "fa2", **c, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
+                 "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+    rc = I.RELPOS_CONFIG
+    q, k, v, table = (t.cuda() for t in I.relpos_inputs(**rc, seed=0))
+    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    ms = time_launches(lambda i: neso_amd.rel_pos_attention(q, k, v, table, out=out), steps,
+                       warmup, torch)
+    flop = 4.0 * rc["H"] * rc["N"] ** 2 * rc["d"]
+    tf = flop / (ms * 1e-3) / 1e12
+    rows.append({"kernel": "rel_pos_fa2", **rc, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
+                 "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+    for cfg in I.QMM_CONFIGS[1:]:
+        r = qmm_case(neso_amd, torch, I, cfg, steps, warmup, rotate=8)
+        rows.append({"kernel": "w4a16", **cfg, "us": round(r["ms_per_step"] * 1e3, 2),
+                     "gbs": r["value"], "tflops": r["tflops"],
+                     "hbm_frac": r["roofline"]["frac"],
+                     "mfma_frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4)})
+    return rows
+
+
+if __name__ == "__main__":
+    sys.exit(main())

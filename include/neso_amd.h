@@ -1,0 +1,138 @@
+/*
+ * neso_amd — C ABI of the MI355X (gfx950) kernels behind neso's hot path.
+ *
+ * Every entry point takes device pointers the caller owns, sizes and element
+ * strides by value, and an optional HIP stream (`void*` = hipStream_t, NULL =
+ * the null stream).  Nothing here allocates, copies or synchronises: a call
+ * validates its arguments on the host, enqueues one kernel on `stream` and
+ * returns.  Validation happens before any HIP call, so argument errors are
+ * reported on hosts without a GPU.
+ *
+ * fp16 buffers are IEEE binary16, passed as `const void*`.
+ *
+ * Status codes: NESO_OK, NESO_EINVAL (bad argument), NESO_EUNSUPPORTED
+ * (valid but not implemented, e.g. head_dim 96), NESO_ELAUNCH (the HIP
+ * launch failed; neso_last_error() carries hipGetErrorString).  Calls are
+ * thread-safe; neso_last_error() is per thread.
+ */
+#ifndef NESO_AMD_H_
+#define NESO_AMD_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NESO_OK 0
+#define NESO_EINVAL 1
+#define NESO_EUNSUPPORTED 2
+#define NESO_ELAUNCH 3
+
+/* rel_pos_fa2_fwd bias_mode */
+#define NESO_BIAS_DENSE_SCALED_F16 0 /* bias f16 [h][T][T], logits = (QK^T + B) * scale */
+#define NESO_BIAS_TABLE_F32 1        /* bias f32 [h][2T-1], logits = QK^T * scale + B[i-j+T-1] */
+
+/* output dtype selector */
+#define NESO_OUT_F16 0
+#define NESO_OUT_F32 1
+
+/* Version of this ABI (bumped on any signature change). */
+int neso_abi_version(void);
+
+/* Text of a status code. */
+const char* neso_status_string(int status);
+
+/* Detail of the last non-OK status returned on this thread ("" if none). */
+const char* neso_last_error(void);
+
+/* JSON manifest of the entry points: name, positional parameters (name,
+ * C type, pointer or scalar), reference kernel they replace, constraints.
+ * Role of the reference's AOT manifest, src/neso/aot_compile.py:108-117. */
+const char* neso_kernel_manifest(void);
+
+/*
+ * Flash-Attention-2 forward.  Replaces the `flash_attention_fwd` kernel of
+ * tests/test_flash_attention.py:149-153 (launched at :287-290 and by
+ * macos/harness.rs:149-169 with buffers 0-3 = Q, K, V, O and scalars 4-7 =
+ * N, stride_qo, stride_kv, scale).  The first eight parameters keep that
+ * order and meaning:
+ *   Q, K, V   fp16 [N][d] rows (row stride stride_qo / stride_kv elements)
+ *   O         fp32 [N][d] rows, row stride stride_qo (as in the reference)
+ *   N         sequence length (queries == keys); no multiple-of-block rule
+ *   scale     softmax scale (1/sqrt(d) in the reference)
+ * Extensions (the reference bakes d into the kernel and launches one head):
+ *   head_dim     32, 64 or 128
+ *   batch_heads  number of independent (batch, head) slices, >= 1
+ *   stride_bh_qo, stride_bh_kv  element distance between slices of Q/O, K/V
+ *   causal       0: full attention; 1: key j visible to query i iff j <= i
+ * Strides and pointers must allow 16-byte loads: strides multiple of 8,
+ * pointers 16-byte aligned.  O = softmax(Q K^T * scale) V, softmax in fp32,
+ * P rounded to fp16 before P V (reference :140-145), fp32 accumulation.
+ */
+int neso_flash_attention_fwd(const void* Q, const void* K, const void* V, float* O, int32_t N,
+                             int32_t stride_qo, int32_t stride_kv, float scale, int32_t head_dim,
+                             int32_t batch_heads, int64_t stride_bh_qo, int64_t stride_bh_kv,
+                             int32_t causal, void* stream);
+
+/*
+ * Relative-position-bias FA2.  Replaces `rel_pos_fa2_fwd` of
+ * tests/test_rel_pos_fa2.py:157-163 (grid (T/BM, nh) at :364-368).  The
+ * first ten parameters keep the reference order and meaning:
+ *   Q, K, V       fp16 [nh][T][d], row stride `stride`, head stride `stride_h`
+ *   bias          per bias_mode (head stride bias_stride_h elements):
+ *                   NESO_BIAS_DENSE_SCALED_F16 - f16 [nh][T][T] (reference
+ *                     kernel: logits = (QK^T + bias) * scale)
+ *                   NESO_BIAS_TABLE_F32 - f32 [nh][2T-1] table, logits =
+ *                     QK^T * scale + bias[i - j + T - 1]
+ *   O             [nh][T][d] (out_dtype NESO_OUT_F16 as the reference, or
+ *                 NESO_OUT_F32), row stride `stride`, head stride `stride_h`
+ *   T, stride, scale, stride_h, bias_stride_h  as in the reference
+ * Extensions: num_heads (the reference's grid y), head_dim (32/64/128),
+ * bias_mode, out_dtype.  T needs no multiple-of-block rule (tails masked).
+ */
+int neso_rel_pos_fa2_fwd(const void* Q, const void* K, const void* V, const void* bias, void* O,
+                         int32_t T, int32_t stride, float scale, int32_t stride_h,
+                         int32_t bias_stride_h, int32_t num_heads, int32_t head_dim,
+                         int32_t bias_mode, int32_t out_dtype, void* stream);
+
+/*
+ * Weight-only int4 matmul, Y[M][N] fp16 = X[M][K] fp16 * dequant(W)^T.
+ * No reference kernel packs int4 (the reference's W4A16 stores one int4
+ * value per int8, tests/test_quantized_matmul.py:170-178); this is the
+ * BASELINE format:
+ *   W       int32 [N][K/8]; code of column k = nibble (k % 8) of word k/8,
+ *           low nibble first
+ *   scales  fp16 [N][K/group_size]
+ *   dequant(c) = (c - zero_point) * scale; fp32 accumulation, fp16 output
+ * K multiple of 32, group_size a multiple of 32 dividing K, 0 <= zero_point
+ * <= 15, X rows 16-byte aligned (stride_xm multiple of 8).
+ */
+int neso_w4a16_matmul(const void* X, const int32_t* W, const void* scales, void* Y, int32_t M,
+                      int32_t N, int32_t K, int32_t stride_xm, int32_t stride_ym,
+                      int32_t group_size, int32_t zero_point, void* stream);
+
+/*
+ * W8A16 matmul, C[M][N] fp32 = A[M][K] fp16 * f16(B[K][N] int8).  Replaces
+ * `w8a16_matmul` of tests/test_quantized_matmul.py:77-80 (positional
+ * A, B, C, K, stride_am, stride_bk, stride_cm).  The reference takes M and
+ * N from the launch grid; here they are explicit trailing parameters.
+ */
+int neso_w8a16_matmul(const void* A, const int8_t* B, float* C, int32_t K, int32_t stride_am,
+                      int32_t stride_bk, int32_t stride_cm, int32_t M, int32_t N, void* stream);
+
+/*
+ * W8A16 with per-output-channel scale applied after accumulation,
+ * C = (A * f16(B)) * scale[n], scale fp16 [N].  Replaces
+ * `w8a16_scaled_matmul` of tests/test_quantized_matmul.py:189-192
+ * (positional A, B, C, scale, K, stride_am, stride_bk, stride_cm).
+ */
+int neso_w8a16_scaled_matmul(const void* A, const int8_t* B, float* C, const void* scale,
+                             int32_t K, int32_t stride_am, int32_t stride_bk, int32_t stride_cm,
+                             int32_t M, int32_t N, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NESO_AMD_H_ */

@@ -1,0 +1,67 @@
+// Shared device-side helpers for the gfx950 (CDNA4) kernels of neso_amd.
+//
+// Everything here is written for one target: 64-lane wavefronts, the
+// v_mfma_f32_{32x32x16,16x16x32}_f16 matrix instructions and the 160 KiB LDS
+// of an MI355X compute unit.  There is no portability layer on purpose.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace neso {
+
+typedef _Float16 half_t;
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef _Float16 half4v __attribute__((ext_vector_type(4)));
+typedef _Float16 half8v __attribute__((ext_vector_type(8)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef int32_t int4v __attribute__((ext_vector_type(4)));
+typedef uint32_t uint4v __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+// D(32x32,f32) += A(32x16,f16) * B(16x32,f16).
+// Lane l supplies A[l%32][8*(l/32) + 0..7] and B[8*(l/32) + 0..7][l%32];
+// accumulator register r of lane l is D[8*(r/4) + 4*(l/32) + r%4][l%32].
+__device__ __forceinline__ float16v mfma32x32x16(half8v a, half8v b, float16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// D(16x16,f32) += A(16x32,f16) * B(32x16,f16).
+// Lane l supplies A[l%16][8*(l/16) + 0..7] and B[8*(l/16) + 0..7][l%16];
+// accumulator register r of lane l is D[4*(l/16) + r][l%16].
+__device__ __forceinline__ float4v mfma16x16x32(half8v a, half8v b, float4v c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 2^x on the transcendental unit (v_exp_f32); exp2(-inf) == 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Value held by lane (l ^ 32): the other half of a 64-lane wavefront.
+__device__ __forceinline__ float swap_halves(float x) {
+  return __shfl_xor(x, 32, kWave);
+}
+
+// Wavefront-wide sum; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) x += __shfl_xor(x, off, kWave);
+  return x;
+}
+
+__device__ __forceinline__ half8v load_half8(const half_t* p) {
+  return *reinterpret_cast<const half8v*>(p);
+}
+
+// Workgroup index remapped so that consecutive logical indices land on the
+// same XCD.  The hardware dispatcher deals workgroups round-robin over the
+// 8 XCDs (workgroup i runs on XCD i % 8); each XCD has its own L2, so
+// workgroups that share K/V (or weight) tiles should share an XCD.
+__device__ __forceinline__ uint32_t xcd_swizzle(uint32_t hw_id, uint32_t total) {
+  constexpr uint32_t kXcds = 8;
+  if (total % kXcds != 0) return hw_id;
+  return (hw_id % kXcds) * (total / kXcds) + hw_id / kXcds;
+}
+
+}  // namespace neso

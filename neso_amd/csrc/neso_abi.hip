@@ -1,0 +1,304 @@
+// C ABI of neso_amd: argument validation, status codes and the kernel
+// manifest.  Every check below runs before the first HIP call, so invalid
+// arguments are reported identically with or without a GPU.
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "../../include/neso_amd.h"
+#include "neso_internal.h"
+
+namespace {
+
+thread_local char g_last_error[512] = "";
+
+int fail(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int ok() {
+  g_last_error[0] = '\0';
+  return NESO_OK;
+}
+
+int launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(NESO_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
+
+int check_head_dim(int32_t d) {
+  if (d == 32 || d == 64 || d == 128) return NESO_OK;
+  return fail(NESO_EUNSUPPORTED, "head_dim %d not supported (32, 64, 128)", d);
+}
+
+const char kManifest[] = R"JSON({
+  "library": "neso_amd",
+  "abi_version": 1,
+  "target": "gfx950",
+  "kernels": [
+    {"name": "neso_flash_attention_fwd", "replaces": "flash_attention_fwd (tests/test_flash_attention.py:149-153)",
+     "params": [
+      {"index": 0, "name": "Q", "type": "const fp16*", "is_pointer": true},
+      {"index": 1, "name": "K", "type": "const fp16*", "is_pointer": true},
+      {"index": 2, "name": "V", "type": "const fp16*", "is_pointer": true},
+      {"index": 3, "name": "O", "type": "fp32*", "is_pointer": true},
+      {"index": 4, "name": "N", "type": "int32", "is_pointer": false},
+      {"index": 5, "name": "stride_qo", "type": "int32", "is_pointer": false},
+      {"index": 6, "name": "stride_kv", "type": "int32", "is_pointer": false},
+      {"index": 7, "name": "scale", "type": "fp32", "is_pointer": false},
+      {"index": 8, "name": "head_dim", "type": "int32", "is_pointer": false},
+      {"index": 9, "name": "batch_heads", "type": "int32", "is_pointer": false},
+      {"index": 10, "name": "stride_bh_qo", "type": "int64", "is_pointer": false},
+      {"index": 11, "name": "stride_bh_kv", "type": "int64", "is_pointer": false},
+      {"index": 12, "name": "causal", "type": "int32", "is_pointer": false},
+      {"index": 13, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
+     "threadgroup_size": 256, "block_m": 128, "block_n": 64, "head_dims": [32, 64, 128],
+     "grid": ["cdiv(N, 128) * batch_heads", "1", "1"]},
+    {"name": "neso_rel_pos_fa2_fwd", "replaces": "rel_pos_fa2_fwd (tests/test_rel_pos_fa2.py:157-163)",
+     "params": [
+      {"index": 0, "name": "Q", "type": "const fp16*", "is_pointer": true},
+      {"index": 1, "name": "K", "type": "const fp16*", "is_pointer": true},
+      {"index": 2, "name": "V", "type": "const fp16*", "is_pointer": true},
+      {"index": 3, "name": "bias", "type": "const fp16*|const fp32*", "is_pointer": true},
+      {"index": 4, "name": "O", "type": "fp16*|fp32*", "is_pointer": true},
+      {"index": 5, "name": "T", "type": "int32", "is_pointer": false},
+      {"index": 6, "name": "stride", "type": "int32", "is_pointer": false},
+      {"index": 7, "name": "scale", "type": "fp32", "is_pointer": false},
+      {"index": 8, "name": "stride_h", "type": "int32", "is_pointer": false},
+      {"index": 9, "name": "bias_stride_h", "type": "int32", "is_pointer": false},
+      {"index": 10, "name": "num_heads", "type": "int32", "is_pointer": false},
+      {"index": 11, "name": "head_dim", "type": "int32", "is_pointer": false},
+      {"index": 12, "name": "bias_mode", "type": "int32", "is_pointer": false},
+      {"index": 13, "name": "out_dtype", "type": "int32", "is_pointer": false},
+      {"index": 14, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
+     "threadgroup_size": 256, "block_m": 128, "block_n": 64,
+     "grid": ["cdiv(T, 128) * num_heads", "1", "1"]},
+    {"name": "neso_w4a16_matmul", "replaces": null,
+     "params": [
+      {"index": 0, "name": "X", "type": "const fp16*", "is_pointer": true},
+      {"index": 1, "name": "W", "type": "const int32*", "is_pointer": true},
+      {"index": 2, "name": "scales", "type": "const fp16*", "is_pointer": true},
+      {"index": 3, "name": "Y", "type": "fp16*", "is_pointer": true},
+      {"index": 4, "name": "M", "type": "int32", "is_pointer": false},
+      {"index": 5, "name": "N", "type": "int32", "is_pointer": false},
+      {"index": 6, "name": "K", "type": "int32", "is_pointer": false},
+      {"index": 7, "name": "stride_xm", "type": "int32", "is_pointer": false},
+      {"index": 8, "name": "stride_ym", "type": "int32", "is_pointer": false},
+      {"index": 9, "name": "group_size", "type": "int32", "is_pointer": false},
+      {"index": 10, "name": "zero_point", "type": "int32", "is_pointer": false},
+      {"index": 11, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
+     "threadgroup_size": 256},
+    {"name": "neso_w8a16_matmul", "replaces": "w8a16_matmul (tests/test_quantized_matmul.py:77-80)",
+     "params": [
+      {"index": 0, "name": "A", "type": "const fp16*", "is_pointer": true},
+      {"index": 1, "name": "B", "type": "const int8*", "is_pointer": true},
+      {"index": 2, "name": "C", "type": "fp32*", "is_pointer": true},
+      {"index": 3, "name": "K", "type": "int32", "is_pointer": false},
+      {"index": 4, "name": "stride_am", "type": "int32", "is_pointer": false},
+      {"index": 5, "name": "stride_bk", "type": "int32", "is_pointer": false},
+      {"index": 6, "name": "stride_cm", "type": "int32", "is_pointer": false},
+      {"index": 7, "name": "M", "type": "int32", "is_pointer": false},
+      {"index": 8, "name": "N", "type": "int32", "is_pointer": false},
+      {"index": 9, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
+     "threadgroup_size": 256},
+    {"name": "neso_w8a16_scaled_matmul", "replaces": "w8a16_scaled_matmul (tests/test_quantized_matmul.py:189-192)",
+     "params": [
+      {"index": 0, "name": "A", "type": "const fp16*", "is_pointer": true},
+      {"index": 1, "name": "B", "type": "const int8*", "is_pointer": true},
+      {"index": 2, "name": "C", "type": "fp32*", "is_pointer": true},
+      {"index": 3, "name": "scale", "type": "const fp16*", "is_pointer": true},
+      {"index": 4, "name": "K", "type": "int32", "is_pointer": false},
+      {"index": 5, "name": "stride_am", "type": "int32", "is_pointer": false},
+      {"index": 6, "name": "stride_bk", "type": "int32", "is_pointer": false},
+      {"index": 7, "name": "stride_cm", "type": "int32", "is_pointer": false},
+      {"index": 8, "name": "M", "type": "int32", "is_pointer": false},
+      {"index": 9, "name": "N", "type": "int32", "is_pointer": false},
+      {"index": 10, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
+     "threadgroup_size": 256}
+  ]
+})JSON";
+
+// Shared by both attention entry points once their layouts are resolved.
+int fa2_common(const void* Q, const void* K, const void* V, void* O, const void* bias, int32_t N,
+               int32_t stride_q, int32_t stride_kv, int32_t stride_o, float scale,
+               int32_t head_dim, int32_t heads, int64_t bh_q, int64_t bh_kv, int64_t bh_o,
+               int64_t bias_stride_h, int causal, int bias_kind, bool out_f16, void* stream,
+               const char* name) {
+  if (!Q || !K || !V || !O) return fail(NESO_EINVAL, "%s: null tensor pointer", name);
+  if (N < 0) return fail(NESO_EINVAL, "%s: N=%d < 0", name, N);
+  if (heads < 0) return fail(NESO_EINVAL, "%s: batch_heads=%d < 0", name, heads);
+  int st = check_head_dim(head_dim);
+  if (st != NESO_OK) return st;
+  if (!isfinite(scale)) return fail(NESO_EINVAL, "%s: scale is not finite", name);
+  if (causal != 0 && causal != 1) return fail(NESO_EINVAL, "%s: causal=%d", name, causal);
+  if (stride_q < head_dim || stride_kv < head_dim || stride_o < head_dim)
+    return fail(NESO_EINVAL, "%s: row stride smaller than head_dim %d", name, head_dim);
+  if (stride_q % 8 || stride_kv % 8 || stride_o % 4)
+    return fail(NESO_EINVAL, "%s: row strides must be multiples of 8 elements", name);
+  if (bh_q % 8 || bh_kv % 8 || bh_o % 4 || bh_q < 0 || bh_kv < 0 || bh_o < 0)
+    return fail(NESO_EINVAL, "%s: head strides must be non-negative multiples of 8", name);
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
+    return fail(NESO_EINVAL, "%s: Q/K/V/O must be 16-byte aligned", name);
+  if (bias_kind != neso::kBiasNone) {
+    if (!bias) return fail(NESO_EINVAL, "%s: null bias pointer", name);
+    if (bias_stride_h < 0) return fail(NESO_EINVAL, "%s: bias_stride_h < 0", name);
+    if (bias_kind == neso::kBiasTableF32 && (reinterpret_cast<uintptr_t>(bias) & 3u))
+      return fail(NESO_EINVAL, "%s: f32 bias table must be 4-byte aligned", name);
+    if (bias_kind == neso::kBiasDenseF16 && !aligned2(bias))
+      return fail(NESO_EINVAL, "%s: f16 bias must be 2-byte aligned", name);
+  }
+  if (N == 0 || heads == 0) return ok();
+  if ((int64_t)(N + neso::fa2_query_block() - 1) / neso::fa2_query_block() * heads > 0x7fffffff)
+    return fail(NESO_EUNSUPPORTED, "%s: grid too large", name);
+
+  neso::Fa2Args a{};
+  a.Q = static_cast<const neso::half_t*>(Q);
+  a.K = static_cast<const neso::half_t*>(K);
+  a.V = static_cast<const neso::half_t*>(V);
+  a.O = O;
+  a.bias = bias;
+  a.N = N;
+  a.stride_q = stride_q;
+  a.stride_kv = stride_kv;
+  a.stride_o = stride_o;
+  a.bh_stride_q = bh_q;
+  a.bh_stride_kv = bh_kv;
+  a.bh_stride_o = bh_o;
+  a.bias_stride_h = bias_stride_h;
+  a.batch_heads = heads;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  return launched(neso::launch_fa2(a, head_dim, causal != 0, bias_kind, out_f16,
+                                   static_cast<hipStream_t>(stream)),
+                  name);
+}
+
+}  // namespace
+
+extern "C" {
+
+int neso_abi_version(void) { return 1; }
+
+const char* neso_status_string(int status) {
+  switch (status) {
+    case NESO_OK: return "NESO_OK";
+    case NESO_EINVAL: return "NESO_EINVAL: invalid argument";
+    case NESO_EUNSUPPORTED: return "NESO_EUNSUPPORTED: unsupported configuration";
+    case NESO_ELAUNCH: return "NESO_ELAUNCH: kernel launch failed";
+    default: return "NESO_UNKNOWN";
+  }
+}
+
+const char* neso_last_error(void) { return g_last_error; }
+
+const char* neso_kernel_manifest(void) { return kManifest; }
+
+int neso_flash_attention_fwd(const void* Q, const void* K, const void* V, float* O, int32_t N,
+                             int32_t stride_qo, int32_t stride_kv, float scale, int32_t head_dim,
+                             int32_t batch_heads, int64_t stride_bh_qo, int64_t stride_bh_kv,
+                             int32_t causal, void* stream) {
+  return fa2_common(Q, K, V, O, nullptr, N, stride_qo, stride_kv, stride_qo, scale, head_dim,
+                    batch_heads, stride_bh_qo, stride_bh_kv, stride_bh_qo, 0, causal,
+                    neso::kBiasNone, false, stream, "flash_attention_fwd");
+}
+
+int neso_rel_pos_fa2_fwd(const void* Q, const void* K, const void* V, const void* bias, void* O,
+                         int32_t T, int32_t stride, float scale, int32_t stride_h,
+                         int32_t bias_stride_h, int32_t num_heads, int32_t head_dim,
+                         int32_t bias_mode, int32_t out_dtype, void* stream) {
+  int kind;
+  if (bias_mode == NESO_BIAS_DENSE_SCALED_F16) {
+    kind = neso::kBiasDenseF16;
+  } else if (bias_mode == NESO_BIAS_TABLE_F32) {
+    kind = neso::kBiasTableF32;
+  } else {
+    return fail(NESO_EINVAL, "rel_pos_fa2_fwd: bias_mode=%d", bias_mode);
+  }
+  if (out_dtype != NESO_OUT_F16 && out_dtype != NESO_OUT_F32)
+    return fail(NESO_EINVAL, "rel_pos_fa2_fwd: out_dtype=%d", out_dtype);
+  return fa2_common(Q, K, V, O, bias, T, stride, stride, stride, scale, head_dim, num_heads,
+                    stride_h, stride_h, stride_h, bias_stride_h, 0, kind,
+                    out_dtype == NESO_OUT_F16, stream, "rel_pos_fa2_fwd");
+}
+
+int neso_w4a16_matmul(const void* X, const int32_t* W, const void* scales, void* Y, int32_t M,
+                      int32_t N, int32_t K, int32_t stride_xm, int32_t stride_ym,
+                      int32_t group_size, int32_t zero_point, void* stream) {
+  const char* name = "w4a16_matmul";
+  if (!X || !W || !scales || !Y) return fail(NESO_EINVAL, "%s: null tensor pointer", name);
+  if (M < 0 || N < 0 || K < 0) return fail(NESO_EINVAL, "%s: negative size", name);
+  if (K % 32) return fail(NESO_EINVAL, "%s: K=%d must be a multiple of 32", name, K);
+  if (group_size <= 0 || group_size % 32 || (K && K % group_size))
+    return fail(NESO_EINVAL, "%s: group_size=%d must be a multiple of 32 dividing K", name,
+                group_size);
+  if (zero_point < 0 || zero_point > 15)
+    return fail(NESO_EINVAL, "%s: zero_point=%d outside [0, 15]", name, zero_point);
+  if (stride_xm < K || stride_xm % 8)
+    return fail(NESO_EINVAL, "%s: stride_xm=%d must be >= K and a multiple of 8", name,
+                stride_xm);
+  if (stride_ym < N) return fail(NESO_EINVAL, "%s: stride_ym=%d < N", name, stride_ym);
+  if (!aligned16(X) || !aligned16(W) || !aligned2(scales) || !aligned2(Y))
+    return fail(NESO_EINVAL, "%s: X/W must be 16-byte aligned, scales/Y 2-byte", name);
+  if (M == 0 || N == 0) return ok();
+  if (K == 0) return fail(NESO_EINVAL, "%s: K=0 with non-empty output", name);
+  neso::W4Args a{};
+  a.X = static_cast<const neso::half_t*>(X);
+  a.W = reinterpret_cast<const uint32_t*>(W);
+  a.S = static_cast<const neso::half_t*>(scales);
+  a.Y = static_cast<neso::half_t*>(Y);
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.ldx = stride_xm;
+  a.ldy = stride_ym;
+  a.group = group_size;
+  a.zero = zero_point;
+  return launched(neso::launch_w4a16(a, static_cast<hipStream_t>(stream)), name);
+}
+
+static int w8a16_common(const void* A, const int8_t* B, float* C, const void* scale, int32_t K,
+                        int32_t stride_am, int32_t stride_bk, int32_t stride_cm, int32_t M,
+                        int32_t N, void* stream, const char* name) {
+  if (!A || !B || !C) return fail(NESO_EINVAL, "%s: null tensor pointer", name);
+  if (M < 0 || N < 0 || K < 0) return fail(NESO_EINVAL, "%s: negative size", name);
+  if (stride_am < K || stride_bk < N || stride_cm < N)
+    return fail(NESO_EINVAL, "%s: stride smaller than the row it spans", name);
+  if (!aligned2(A) || (scale && !aligned2(scale)) || (reinterpret_cast<uintptr_t>(C) & 3u))
+    return fail(NESO_EINVAL, "%s: misaligned A/C/scale", name);
+  if (M == 0 || N == 0) return ok();
+  neso::W8Args a{};
+  a.A = static_cast<const neso::half_t*>(A);
+  a.B = B;
+  a.C = C;
+  a.scale = static_cast<const neso::half_t*>(scale);
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.lda = stride_am;
+  a.ldb = stride_bk;
+  a.ldc = stride_cm;
+  return launched(neso::launch_w8a16(a, static_cast<hipStream_t>(stream)), name);
+}
+
+int neso_w8a16_matmul(const void* A, const int8_t* B, float* C, int32_t K, int32_t stride_am,
+                      int32_t stride_bk, int32_t stride_cm, int32_t M, int32_t N, void* stream) {
+  return w8a16_common(A, B, C, nullptr, K, stride_am, stride_bk, stride_cm, M, N, stream,
+                      "w8a16_matmul");
+}
+
+int neso_w8a16_scaled_matmul(const void* A, const int8_t* B, float* C, const void* scale,
+                             int32_t K, int32_t stride_am, int32_t stride_bk, int32_t stride_cm,
+                             int32_t M, int32_t N, void* stream) {
+  if (!scale) return fail(NESO_EINVAL, "w8a16_scaled_matmul: null scale pointer");
+  return w8a16_common(A, B, C, scale, K, stride_am, stride_bk, stride_cm, M, N, stream,
+                      "w8a16_scaled_matmul");
+}
+
+}  // extern "C"

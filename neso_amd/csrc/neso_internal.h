@@ -1,0 +1,66 @@
+// Internal launch interface between the C-ABI layer (neso_abi.hip) and the
+// kernel translation units.  Argument validation happens in the ABI layer;
+// the launchers below assume their arguments were checked.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "common.h"
+
+namespace neso {
+
+enum BiasKind { kBiasNone = 0, kBiasTableF32 = 1, kBiasDenseF16 = 2 };
+
+struct Fa2Args {
+  const half_t* Q;
+  const half_t* K;
+  const half_t* V;
+  void* O;              // f32 or f16, [batch_heads][N][stride_o]
+  const void* bias;     // table f32 [h][2N-1] or dense f16 [h][N][N]
+  int32_t N;            // queries == keys per (batch, head)
+  int32_t stride_q;     // row stride of Q (elements)
+  int32_t stride_kv;    // row stride of K and V (elements)
+  int32_t stride_o;     // row stride of O (elements)
+  int64_t bh_stride_q;  // (batch, head) strides, elements
+  int64_t bh_stride_kv;
+  int64_t bh_stride_o;
+  int64_t bias_stride_h;
+  int32_t batch_heads;
+  float scale_log2;     // softmax scale * log2(e)
+  int32_t num_qblocks;  // filled in by launch_fa2
+};
+
+int fa2_query_block();
+hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool out_f16,
+                      hipStream_t stream);
+
+// Y[M][N] (f16, row stride ldy) = X[M][K] (f16, row stride ldx) * dequant(W)^T
+// with W packed 8 int4 codes per int32 along K ([N][K/8]), scales f16
+// [N][K/group], code c -> (c - zero) * scale.
+struct W4Args {
+  const half_t* X;
+  const uint32_t* W;
+  const half_t* S;
+  half_t* Y;
+  int32_t M, N, K;
+  int32_t ldx, ldy;
+  int32_t group;
+  int32_t zero;
+};
+
+hipError_t launch_w4a16(const W4Args& a, hipStream_t stream);
+
+// C[M][N] (f32) = A[M][K] (f16) * f16(B[K][N] int8) [* scale[n]].
+struct W8Args {
+  const half_t* A;
+  const int8_t* B;
+  float* C;
+  const half_t* scale;  // nullptr: unscaled
+  int32_t M, N, K;
+  int32_t lda, ldb, ldc;
+};
+
+hipError_t launch_w8a16(const W8Args& a, hipStream_t stream);
+
+}  // namespace neso

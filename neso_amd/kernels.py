@@ -1,0 +1,218 @@
+"""Host-side launchers with the reference kernels' names and positional order.
+
+The reference launches hand-written TTIR kernels by name with positional
+buffers, e.g. ``dispatch(pipe, (N // BM, 1, 1), threads, [Q, K, V, O, N,
+stride_qo, stride_kv, scale])`` (tests/test_flash_attention.py:65-76,
+:283-292).  Here each kernel is a Python function taking the same positional
+arguments - device tensors (or raw device addresses) followed by the
+scalars - that calls the C ABI of ``libneso_amd.so`` on the current HIP
+stream.  The grid is derived by the library, so it is not an argument.
+
+Errors follow the reference: invalid arguments raise
+:class:`~neso_amd._lib.NesoArgumentError` (a ``ValueError`` and a
+``RuntimeError``), launch failures raise :class:`~neso_amd._lib.NesoError`
+(a ``RuntimeError``).  There is no CPU path: without the library, or
+without a GPU, these functions raise.
+"""
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "flash_attention_fwd",
+    "rel_pos_fa2_fwd",
+    "w4a16_matmul",
+    "w8a16_matmul",
+    "w8a16_scaled_matmul",
+    "launch",
+    "KERNELS",
+    "attention",
+    "rel_pos_attention",
+    "w4a16_linear",
+]
+
+
+def _ptr(x: Any, name: str, dtype: torch.dtype | tuple[torch.dtype, ...] | None) -> int:
+    """Device address of a tensor (dtype/device checked) or a raw integer address."""
+    if x is None:
+        return 0
+    if isinstance(x, int):
+        return x
+    if not isinstance(x, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor or a device address, got {type(x)!r}")
+    if x.device.type != "cuda":
+        raise ValueError(f"{name}: tensor must be on the GPU (got {x.device}); there is no CPU path")
+    if dtype is not None:
+        allowed = dtype if isinstance(dtype, tuple) else (dtype,)
+        if x.dtype not in allowed:
+            raise TypeError(f"{name}: dtype {x.dtype} not in {allowed}")
+    return x.data_ptr()
+
+
+def _stream(stream: Any, *tensors: Any) -> int:
+    if stream is not None:
+        return int(stream.cuda_stream) if hasattr(stream, "cuda_stream") else int(stream)
+    for t in tensors:
+        if isinstance(t, torch.Tensor) and t.device.type == "cuda":
+            return int(torch.cuda.current_stream(t.device).cuda_stream)
+    return 0
+
+
+def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scale: float, *,
+                        head_dim: int | None = None, batch_heads: int = 1,
+                        stride_bh_qo: int = 0, stride_bh_kv: int = 0, causal: bool = False,
+                        stream=None) -> None:
+    """FA2 forward, O = softmax(Q K^T * scale) V.
+
+    Positional arguments as the reference kernel (tests/test_flash_attention.py
+    :149-153): Q, K, V fp16 [N, d] rows, O fp32 rows with row stride
+    ``stride_qo``, N, stride_qo, stride_kv (elements), scale.  Keyword
+    extensions: ``head_dim`` (inferred from ``Q.shape[-1]`` for tensors),
+    ``batch_heads`` with ``stride_bh_qo`` / ``stride_bh_kv`` for B*H slices
+    in one launch, and ``causal``.
+    """
+    if head_dim is None:
+        if not isinstance(Q, torch.Tensor):
+            raise ValueError("head_dim is required when Q is a raw address")
+        head_dim = int(Q.shape[-1])
+    lib = _lib.load()
+    st = lib.neso_flash_attention_fwd(
+        _ptr(Q, "Q", torch.float16), _ptr(K, "K", torch.float16), _ptr(V, "V", torch.float16),
+        _ptr(O, "O", torch.float32), int(N), int(stride_qo), int(stride_kv), float(scale),
+        int(head_dim), int(batch_heads), int(stride_bh_qo), int(stride_bh_kv), int(bool(causal)),
+        _stream(stream, Q, O))
+    _lib.check(st)
+
+
+def rel_pos_fa2_fwd(Q, K, V, bias, O, T: int, stride: int, scale: float, stride_h: int,
+                    bias_stride_h: int, *, num_heads: int, head_dim: int | None = None,
+                    bias_mode: int = _lib.NESO_BIAS_DENSE_SCALED_F16, stream=None) -> None:
+    """Relative-position-bias FA2.
+
+    Positional arguments as the reference (tests/test_rel_pos_fa2.py:157-163):
+    Q, K, V fp16 [nh, T, d], bias, O, T, stride, scale, stride_h,
+    bias_stride_h.  ``num_heads`` replaces the reference's grid y.
+    ``bias_mode`` selects NESO_BIAS_DENSE_SCALED_F16 (reference: f16
+    [nh, T, T], logits (QK^T + B) * scale) or NESO_BIAS_TABLE_F32 (f32
+    [nh, 2T-1], logits QK^T * scale + B[i - j + T - 1]).  The output dtype
+    follows O (fp16 as in the reference, or fp32).
+    """
+    if head_dim is None:
+        if not isinstance(Q, torch.Tensor):
+            raise ValueError("head_dim is required when Q is a raw address")
+        head_dim = int(Q.shape[-1])
+    if isinstance(O, torch.Tensor):
+        out_dtype = _lib.NESO_OUT_F32 if O.dtype == torch.float32 else _lib.NESO_OUT_F16
+    else:
+        out_dtype = _lib.NESO_OUT_F16
+    bias_dtype = torch.float16 if bias_mode == _lib.NESO_BIAS_DENSE_SCALED_F16 else torch.float32
+    lib = _lib.load()
+    st = lib.neso_rel_pos_fa2_fwd(
+        _ptr(Q, "Q", torch.float16), _ptr(K, "K", torch.float16), _ptr(V, "V", torch.float16),
+        _ptr(bias, "bias", bias_dtype), _ptr(O, "O", (torch.float16, torch.float32)), int(T),
+        int(stride), float(scale), int(stride_h), int(bias_stride_h), int(num_heads),
+        int(head_dim), int(bias_mode), int(out_dtype), _stream(stream, Q, O))
+    _lib.check(st)
+
+
+def w4a16_matmul(X, W, scales, Y, M: int, N: int, K: int, stride_xm: int, stride_ym: int,
+                 group_size: int = 32, zero_point: int = 8, *, stream=None) -> None:
+    """Y[M, N] fp16 = X[M, K] fp16 @ dequant(W)^T, W int32 [N, K/8] (int4, low nibble first)."""
+    lib = _lib.load()
+    st = lib.neso_w4a16_matmul(
+        _ptr(X, "X", torch.float16), _ptr(W, "W", torch.int32), _ptr(scales, "scales", torch.float16),
+        _ptr(Y, "Y", torch.float16), int(M), int(N), int(K), int(stride_xm), int(stride_ym),
+        int(group_size), int(zero_point), _stream(stream, X, Y))
+    _lib.check(st)
+
+
+def w8a16_matmul(A, B, C, K: int, stride_am: int, stride_bk: int, stride_cm: int, *, M: int,
+                 N: int, stream=None) -> None:
+    """C fp32 = A fp16 @ f16(B int8 [K, N]) (tests/test_quantized_matmul.py:77-80 order)."""
+    lib = _lib.load()
+    st = lib.neso_w8a16_matmul(
+        _ptr(A, "A", torch.float16), _ptr(B, "B", torch.int8), _ptr(C, "C", torch.float32), int(K),
+        int(stride_am), int(stride_bk), int(stride_cm), int(M), int(N), _stream(stream, A, C))
+    _lib.check(st)
+
+
+def w8a16_scaled_matmul(A, B, C, scale, K: int, stride_am: int, stride_bk: int, stride_cm: int,
+                        *, M: int, N: int, stream=None) -> None:
+    """C = (A @ f16(B)) * scale[n] (tests/test_quantized_matmul.py:189-192 order)."""
+    lib = _lib.load()
+    st = lib.neso_w8a16_scaled_matmul(
+        _ptr(A, "A", torch.float16), _ptr(B, "B", torch.int8), _ptr(C, "C", torch.float32),
+        _ptr(scale, "scale", torch.float16), int(K), int(stride_am), int(stride_bk),
+        int(stride_cm), int(M), int(N), _stream(stream, A, C))
+    _lib.check(st)
+
+
+KERNELS = {
+    "flash_attention_fwd": flash_attention_fwd,
+    "rel_pos_fa2_fwd": rel_pos_fa2_fwd,
+    "w4a16_matmul": w4a16_matmul,
+    "w8a16_matmul": w8a16_matmul,
+    "w8a16_scaled_matmul": w8a16_scaled_matmul,
+}
+
+
+def launch(name: str, *args, **kwargs) -> None:
+    """Launch a kernel by its reference name with positional arguments."""
+    try:
+        fn = KERNELS[name]
+    except KeyError:
+        raise ValueError(f"unknown kernel {name!r}; known: {sorted(KERNELS)}") from None
+    fn(*args, **kwargs)
+
+
+# ---------------------------------------------------------------------------
+# Tensor-level conveniences over the launchers above.
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = False,
+              scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """FA2 forward over [..., N, d] fp16 tensors (contiguous); returns fp32 [..., N, d]."""
+    if q.shape != k.shape or q.shape != v.shape:
+        raise ValueError("q, k, v must have the same shape [..., N, d]")
+    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("q, k, v must be contiguous")
+    n, d = int(q.shape[-2]), int(q.shape[-1])
+    bh = q.numel() // max(n * d, 1) if n * d else 0
+    if out is None:
+        out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    flash_attention_fwd(q, k, v, out, n, d, d, scale, head_dim=d, batch_heads=bh,
+                        stride_bh_qo=n * d, stride_bh_kv=n * d, causal=causal)
+    return out
+
+
+def rel_pos_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: torch.Tensor, *,
+                      scale: float | None = None, out_dtype: torch.dtype = torch.float32,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """softmax(Q K^T * scale + table[h, i - j + N - 1]) V for [H, N, d] fp16, table f32 [H, 2N-1]."""
+    h, n, d = (int(s) for s in q.shape)
+    if table.shape != (h, 2 * n - 1):
+        raise ValueError(f"table must be [H, 2N-1] = [{h}, {2 * n - 1}], got {tuple(table.shape)}")
+    if out is None:
+        out = torch.empty((h, n, d), dtype=out_dtype, device=q.device)
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    rel_pos_fa2_fwd(q, k, v, table, out, n, d, scale, n * d, 2 * n - 1, num_heads=h, head_dim=d,
+                    bias_mode=_lib.NESO_BIAS_TABLE_F32)
+    return out
+
+
+def w4a16_linear(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Tensor, *,
+                 group_size: int = 32, zero_point: int = 8,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [M, K] fp16 @ dequant(w_packed [N, K/8] int32, scales [N, K/group])^T -> fp16 [M, N]."""
+    m, k = (int(s) for s in x.shape)
+    n = int(w_packed.shape[0])
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float16, device=x.device)
+    w4a16_matmul(x, w_packed, scales, out, m, n, k, x.stride(0), out.stride(0), group_size,
+                 zero_point)
+    return out

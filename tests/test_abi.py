@@ -1,0 +1,193 @@
+"""C-ABI checks that run without a GPU.
+
+The library must load, export every function include/neso_amd.h declares
+(and nothing the Python binding expects must be missing), publish a
+manifest that agrees with the header, and reject invalid arguments with
+NESO_EINVAL / NESO_EUNSUPPORTED before touching HIP (no compute call is
+made here: each call either fails validation or is an empty no-op).
+"""
+from __future__ import annotations
+
+import ctypes
+import json
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+import torch
+
+import neso_amd
+from neso_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "neso_amd.h"
+A16 = 0x10000  # an aligned fake device address: never dereferenced here
+
+
+def header_functions() -> dict[str, int]:
+    """name -> parameter count for every function declared in the header."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for m in re.finditer(r"^[\w ]+?\*?\s*(neso_\w+)\s*\(([^)]*)\)\s*;", text, flags=re.M):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_and_binding_agree():
+    funcs = header_functions()
+    assert funcs, "no declarations parsed from the header"
+    assert set(funcs) == set(_lib.SIGNATURES)
+    for name, n in funcs.items():
+        assert len(_lib.SIGNATURES[name][1]) == n, name
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+    for name in header_functions():
+        assert name in exported, name
+        assert getattr(lib, name) is not None
+
+
+def test_manifest_matches_header(lib):
+    man = json.loads(lib.neso_kernel_manifest().decode())
+    assert man["abi_version"] == lib.neso_abi_version() == 1
+    funcs = header_functions()
+    for k in man["kernels"]:
+        assert k["name"] in funcs
+        assert len(k["params"]) == funcs[k["name"]], k["name"]
+        assert [p["index"] for p in k["params"]] == list(range(len(k["params"])))
+    kernels = {k["name"] for k in man["kernels"]}
+    assert kernels == {n for n in funcs if n.endswith(("_fwd", "_matmul"))}
+
+
+def test_status_strings(lib):
+    for code in (_lib.NESO_OK, _lib.NESO_EINVAL, _lib.NESO_EUNSUPPORTED, _lib.NESO_ELAUNCH):
+        assert lib.neso_status_string(code).startswith(b"NESO_")
+
+
+def fa2(lib, **kw):
+    args = dict(Q=A16, K=A16, V=A16, O=A16, N=128, stride_qo=64, stride_kv=64, scale=0.125,
+                head_dim=64, batch_heads=1, stride_bh_qo=0, stride_bh_kv=0, causal=0, stream=None)
+    args.update(kw)
+    return lib.neso_flash_attention_fwd(*args.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(Q=None), _lib.NESO_EINVAL),
+    (dict(O=None), _lib.NESO_EINVAL),
+    (dict(N=-1), _lib.NESO_EINVAL),
+    (dict(head_dim=96, stride_qo=96, stride_kv=96), _lib.NESO_EUNSUPPORTED),
+    (dict(stride_qo=32), _lib.NESO_EINVAL),
+    (dict(stride_kv=68), _lib.NESO_EINVAL),
+    (dict(K=A16 + 2), _lib.NESO_EINVAL),
+    (dict(scale=float("nan")), _lib.NESO_EINVAL),
+    (dict(causal=2), _lib.NESO_EINVAL),
+    (dict(stride_bh_kv=12), _lib.NESO_EINVAL),
+    (dict(N=0), _lib.NESO_OK),
+    (dict(batch_heads=0), _lib.NESO_OK),
+])
+def test_fa2_validation(lib, kw, status):
+    assert fa2(lib, **kw) == status
+    if status != _lib.NESO_OK:
+        assert lib.neso_last_error()
+
+
+def relpos(lib, **kw):
+    args = dict(Q=A16, K=A16, V=A16, bias=A16, O=A16, T=0, stride=64, scale=0.125, stride_h=0,
+                bias_stride_h=0, num_heads=1, head_dim=64, bias_mode=1, out_dtype=1, stream=None)
+    args.update(kw)
+    return lib.neso_rel_pos_fa2_fwd(*args.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(bias=None), _lib.NESO_EINVAL),
+    (dict(bias_mode=7), _lib.NESO_EINVAL),
+    (dict(out_dtype=3), _lib.NESO_EINVAL),
+    (dict(bias=A16 + 2), _lib.NESO_EINVAL),  # f32 table must be 4-byte aligned
+    (dict(bias=A16 + 2, bias_mode=0), _lib.NESO_OK),
+    (dict(head_dim=48, stride=48), _lib.NESO_EUNSUPPORTED),
+    (dict(), _lib.NESO_OK),
+])
+def test_relpos_validation(lib, kw, status):
+    assert relpos(lib, **kw) == status
+
+
+def w4(lib, **kw):
+    args = dict(X=A16, W=A16, S=A16, Y=A16, M=0, N=11008, K=4096, ldx=4096, ldy=11008,
+                group=32, zero=8, stream=None)
+    args.update(kw)
+    return lib.neso_w4a16_matmul(*args.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(W=None), _lib.NESO_EINVAL),
+    (dict(K=4100, ldx=4104), _lib.NESO_EINVAL),
+    (dict(group=48), _lib.NESO_EINVAL),
+    (dict(group=96), _lib.NESO_EINVAL),  # does not divide K=4096
+    (dict(zero=16), _lib.NESO_EINVAL),
+    (dict(zero=-1), _lib.NESO_EINVAL),
+    (dict(ldx=4000), _lib.NESO_EINVAL),
+    (dict(ldx=4100), _lib.NESO_EINVAL),
+    (dict(ldy=100), _lib.NESO_EINVAL),
+    (dict(X=A16 + 8), _lib.NESO_EINVAL),
+    (dict(M=-1), _lib.NESO_EINVAL),
+    (dict(), _lib.NESO_OK),
+    (dict(group=128), _lib.NESO_OK),
+])
+def test_w4a16_validation(lib, kw, status):
+    assert w4(lib, **kw) == status
+
+
+@pytest.mark.parametrize("scaled", [False, True])
+def test_w8a16_validation(lib, scaled):
+    fn = lib.neso_w8a16_scaled_matmul if scaled else lib.neso_w8a16_matmul
+    extra = [A16] if scaled else []
+    good = [A16, A16, A16, *extra, 64, 64, 64, 64, 0, 64, None]
+    assert fn(*good) == _lib.NESO_OK
+    bad = list(good)
+    bad[0] = None
+    assert fn(*bad) == _lib.NESO_EINVAL
+    bad = list(good)
+    bad[-5] = 32  # stride_bk < N
+    assert fn(*bad) == _lib.NESO_EINVAL
+    if scaled:
+        bad = list(good)
+        bad[3] = None
+        assert fn(*bad) == _lib.NESO_EINVAL
+
+
+def test_python_wrappers_raise():
+    with pytest.raises(ValueError, match="no CPU path"):
+        neso_amd.attention(*(torch.zeros(1, 1, 8, 64, dtype=torch.float16) for _ in range(3)))
+    with pytest.raises(neso_amd.NesoArgumentError):
+        neso_amd.flash_attention_fwd(A16, A16, A16, A16, 128, 64, 64, 0.125, head_dim=80)
+    with pytest.raises(ValueError):
+        neso_amd.flash_attention_fwd(A16, A16, A16, A16, -5, 64, 64, 0.125, head_dim=64)
+    with pytest.raises(ValueError, match="unknown kernel"):
+        neso_amd.launch("vector_add")
+    with pytest.raises(TypeError):
+        neso_amd.w4a16_matmul("x", A16, A16, A16, 1, 1, 32, 32, 1)
+    err = neso_amd.NesoArgumentError(1, "x")
+    assert isinstance(err, RuntimeError) and isinstance(err, ValueError)
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libneso_amd.so")
+    with pytest.raises(ImportError, match="no CPU fallback"):
+        _lib.load()
+
+
+def test_ctypes_signatures_are_c_types():
+    for name, (res, args) in _lib.SIGNATURES.items():
+        for a in args:
+            assert issubclass(a, ctypes._SimpleCData), (name, a)

@@ -1,0 +1,124 @@
+"""Quantised matmul parity on the GPU.
+
+W4A16: rel error max|Y - ref| / max|ref| <= 1e-2 against
+the float64 oracle at M in {1, 16, 256}, K = 4096, N = 11008, plus the int4
+known-answer fixture (exact), ragged shapes, other group sizes / zero
+points and closed forms.  W8A16 / scaled: the reference tests' inputs and
+tolerance (tests/test_quantized_matmul.py:316-447, :531-580).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import neso_amd
+from oracle import inputs as I
+from oracle import qmatmul as Q
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def gpu_w4(x, words, scales, group=32, zero=8):
+    y = neso_amd.w4a16_linear(x.to(DEV), torch.as_tensor(words).to(DEV), scales.to(DEV),
+                              group_size=group, zero_point=zero)
+    torch.cuda.synchronize()
+    return y.cpu()
+
+
+@pytest.mark.parametrize("cfg", I.QMM_CONFIGS, ids=lambda c: f"M{c['M']}")
+def test_baseline_config5(gpu, cfg):
+    x, codes, scales = I.qmatmul_inputs(**cfg, seed=0)
+    words = Q.pack_int4(codes.numpy())
+    y = gpu_w4(x, words, scales)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy(),
+                         dtype=np.float64 if cfg["M"] <= 16 else np.float32)
+    err = Q.rel_err(y.float().numpy(), ref)
+    assert err <= 1e-2, err
+    assert err <= 2e-3, err  # fp16 output rounding is the only expected error
+
+
+def test_int4_kat_exact(gpu, golden_dir):
+    z = np.load(golden_dir / "qmm_int4_kat.npz")
+    x = torch.from_numpy(z["x"]).half()
+    s = torch.from_numpy(z["scales"]).half()
+    for m in (1, 3, 8):  # GEMV and MFMA regimes
+        y = gpu_w4(x[:m], z["words"], s)
+        assert np.array_equal(y.float().numpy(), z["expected"][:m]), m
+
+
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 17, 33, 64, 100])
+@pytest.mark.parametrize("n,k", [(1, 32), (7, 96), (100, 4096), (129, 256)])
+def test_ragged(gpu, m, n, k):
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m * n + k)
+    words = Q.pack_int4(codes.numpy())
+    y = gpu_w4(x, words, scales)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
+    assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("group,zero", [(64, 8), (128, 7), (32, 0), (4096, 15)])
+@pytest.mark.parametrize("m", [1, 16])
+def test_group_and_zero_point(gpu, group, zero, m):
+    x, codes, scales = I.qmatmul_inputs(m, 4096, 300, group=group, seed=group + zero)
+    words = Q.pack_int4(codes.numpy())
+    y = gpu_w4(x, words, scales, group, zero)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy(), group, zero)
+    assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("m", [1, 16, 256])
+def test_zero_point_codes_give_zero(gpu, m):
+    x, _, scales = I.qmatmul_inputs(m, 4096, 512, seed=1)
+    eights = Q.pack_int4(np.full((512, 4096), 8, np.uint8))
+    y = gpu_w4(x, eights, scales)
+    assert torch.count_nonzero(y).item() == 0
+
+
+def test_strided_output(gpu):
+    m, n, k = 3, 200, 512
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=9)
+    words = torch.from_numpy(Q.pack_int4(codes.numpy())).to(DEV)
+    xp = torch.zeros(m, k + 64, dtype=torch.float16, device=DEV)
+    xp[:, :k] = x.to(DEV)
+    y = torch.full((m, n + 8), 5.0, dtype=torch.float16, device=DEV)
+    neso_amd.w4a16_matmul(xp, words, scales.to(DEV), y, m, n, k, k + 64, n + 8)
+    torch.cuda.synchronize()
+    ref = Q.w4a16_matmul(x.numpy(), words.cpu().numpy(), scales.numpy())
+    assert Q.rel_err(y[:, :n].float().cpu().numpy(), ref) <= 2e-3
+    assert torch.all(y[:, n:].cpu() == 5.0)
+
+
+def _w8(kind, m, n, k):
+    a, b, scale = I.reference_quant_lists(m, n, k, kind)
+    A_ = torch.tensor(a).reshape(m, k).half().to(DEV)
+    B_ = torch.tensor(b, dtype=torch.int8).reshape(k, n).to(DEV)
+    C_ = torch.empty(m, n, dtype=torch.float32, device=DEV)
+    if scale is None:
+        neso_amd.launch("w8a16_matmul", A_, B_, C_, k, k, n, n, M=m, N=n)
+    else:
+        S_ = torch.tensor(scale).half().to(DEV)
+        neso_amd.launch("w8a16_scaled_matmul", A_, B_, C_, S_, k, k, n, n, M=m, N=n)
+    torch.cuda.synchronize()
+    return C_.cpu().numpy(), a, b, scale
+
+
+@pytest.mark.parametrize("kind", ["w8a16", "w4a16", "scaled"])
+@pytest.mark.parametrize("mnk", [(32, 32, 32), (64, 64, 64), (64, 64, 128), (128, 128, 128),
+                                 (128, 128, 256), (256, 256, 256)])
+def test_w8a16_reference_configs(gpu, golden_dir, kind, mnk):
+    m, n, k = mnk
+    c, a, b, scale = _w8(kind, m, n, k)
+    A_ = np.array(a, np.float64).reshape(m, k)
+    B_ = np.array(b, np.float64).reshape(k, n)
+    ref = Q.w8a16_scaled_matmul(A_, B_, scale) if scale else Q.w8a16_matmul(A_, B_)
+    assert Q.rel_err(c, ref) < 1e-2  # reference tolerance (:354-358)
+    # Tighter: against the same product on the fp16-rounded activations.
+    A16 = np.array(a, np.float16).astype(np.float64).reshape(m, k)
+    s16 = np.array(scale, np.float16).astype(np.float64) if scale else None
+    ref16 = Q.w8a16_scaled_matmul(A16, B_, s16) if scale else Q.w8a16_matmul(A16, B_)
+    assert Q.rel_err(c, ref16) < 1e-4  # fp32 accumulation order only
+    fixture = golden_dir / f"qmm_{ {'w4a16': 'w4i8'}.get(kind, kind)}_{m}x{n}x{k}.npz"
+    if fixture.exists():
+        assert Q.rel_err(c.reshape(-1), np.load(fixture)["expected"]) < 1e-2
