@@ -33,6 +33,9 @@ COMMON_FLAGS = [
     # Packed FP32 (v_pk_*_f32) stays off: the compiler would otherwise form
     # it from ordinary float code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the softmax reads S and rescales O with
+    # ordinary VALU ops, so AGPR placement would add v_accvgpr copies.
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
 ]
 
 

@@ -54,6 +54,15 @@ __device__ __forceinline__ half8v load_half8(const half_t* p) {
   return *reinterpret_cast<const half8v*>(p);
 }
 
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also
+// fences global memory, which makes the compiler drain every outstanding
+// global load (s_waitcnt vmcnt(0)) at the barrier and defeats prefetching.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Workgroup index remapped so that consecutive logical indices land on the
 // same XCD.  The hardware dispatcher deals workgroups round-robin over the
 // 8 XCDs (workgroup i runs on XCD i % 8); each XCD has its own L2, so

@@ -11,21 +11,29 @@
 //
 // MI355X mapping
 // --------------
-// * One workgroup = 4 waves = 128 query rows of one (batch, head); each wave
-//   owns 32 queries.  Keys/values stream through LDS in blocks of 64,
-//   double-buffered with one barrier per block.
+// * A key group = 4 waves = 128 query rows of one (batch, head); each wave
+//   owns 32 queries.  Keys/values stream through LDS in blocks of 64.
+//   Global loads run two blocks ahead through registers; the LDS holds two
+//   blocks; one barrier per block.
+// * KSPLIT key groups per workgroup split the key blocks between them
+//   (group g takes blocks g, g+KSPLIT, ...) and merge (m, l, O) through LDS
+//   at the end.  KSPLIT = 2 gives every SIMD two waves when the grid alone
+//   would leave one, so MFMA work of one wave hides the softmax of the other.
 // * The score tile is computed transposed, S^T = K Q^T (A = K rows from LDS,
 //   B = Q^T from registers), so lane l holds 32 scores of ONE query (l % 32)
-//   and the other 32 live in lane l ^ 32: row max / row sum are in-register
-//   plus one half-wave exchange, and alpha is a per-lane scalar.
+//   and the other 32 live in lane l ^ 32: row max is in-register plus one
+//   v_permlane32_swap, and alpha is a per-lane scalar.
 // * The K rows feeding the A operand are permuted (kRowPerm) so that the
 //   S^T accumulator registers of lane group g are exactly 8 consecutive keys
 //   per 16-key chunk.  exp(S^T) converted to f16 is therefore directly the
 //   B operand of O^T = V^T P^T: P never goes through LDS.
 // * V is written to LDS transposed ([d][key]) as 32-bit key pairs, which is
 //   bank-conflict free, so the A operand V^T is one ds_read_b128 per lane.
-// * Softmax runs in the log2 domain: t = s * scale * log2(e), p = 2^(t - m),
-//   one FMA + one v_exp_f32 per score.
+// * Softmax runs in the log2 domain with one FMA + one v_exp_f32 per score:
+//   p = 2^(s*c - m), c = |scale| * log2(e).  The running max m is only
+//   raised (and O, l rescaled) when a row max exceeds it by more than
+//   kLazyLog2, so p <= 2^kLazyLog2 and most blocks skip the O rescale.
+//   Row sums use v_dot2_f32_f16 on the fp16 P actually fed to the MFMA.
 // * Workgroups of one head are placed on one XCD (xcd_swizzle) so K/V of
 //   that head are fetched into a single L2.
 #include "common.h"
@@ -35,10 +43,11 @@ namespace neso {
 
 namespace {
 
-constexpr int kBM = 128;      // queries per workgroup
-constexpr int kKB = 64;       // keys per LDS block
-constexpr int kThreads = 256; // 4 waves
+constexpr int kBM = 128;       // queries per workgroup
+constexpr int kKB = 64;        // keys per LDS block
+constexpr int kGroup = 256;    // threads per key group (4 waves)
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLazyLog2 = 8.f;  // rescale threshold (log2 units)
 
 // Row of the 32-key tile loaded into A-operand row rho (= lane % 32) so that
 // accumulator register r of lane group g holds key 16*(r/8) + 8*g + r%8.
@@ -48,25 +57,50 @@ __device__ __forceinline__ int kRowPerm(int rho) {
   return 16 * (b >> 1) + 8 * g + 4 * (b & 1) + j;
 }
 
-template <int D, bool CAUSAL, int BIAS, bool OUT_F16>
-__global__ __launch_bounds__(kThreads) void fa2_fwd_kernel(Fa2Args p) {
-  constexpr int KS = D / 16;                   // k-steps of S^T = K Q^T
-  constexpr int DT = D / 32;                   // 32-row tiles of O^T
-  constexpr int KLD = D + 8;                   // LDS row stride of K (halves)
-  constexpr int VLD = kKB + 8;                 // LDS row stride of V^T (halves)
-  constexpr int KCH = kKB * D / 8 / kThreads;  // 16-byte K chunks per thread
-  constexpr int VJOBS = kKB * D / 16;          // (key pair, 8 columns) jobs
-  constexpr int VCH = (VJOBS + kThreads - 1) / kThreads;
-  constexpr int BAND = kBM + kKB - 1;          // bias-table entries per block
-  static_assert(KCH >= 1 && kKB * D / 8 % kThreads == 0, "K tile split");
+// max over lanes l and l ^ 32 (v_permlane32_swap returns the lower-half and
+// upper-half values of the lane's position within its half).
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
-  __shared__ __attribute__((aligned(16))) half_t sK[2][kKB * KLD];
-  __shared__ __attribute__((aligned(16))) half_t sV[2][D * VLD];
-  __shared__ float sBias[2][BIAS == kBiasTableF32 ? BAND + 1 : 1];
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int D>
+struct Staging {
+  static constexpr int KCH = kKB * D / 8 / kGroup;   // 16-byte K chunks per thread
+  static constexpr int VJOBS = kKB * D / 16;         // (key pair, 8 columns) jobs
+  static constexpr int VCH = (VJOBS + kGroup - 1) / kGroup;
+  half8v k[KCH];
+  half8v v[VCH][2];
+  float b;
+  int kb0;  // first key of the staged block
+};
+
+template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int KSPLIT>
+__global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
+  constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
+  constexpr int DT = D / 32;   // 32-row tiles of O^T
+  constexpr int KLD = D + 8;   // LDS row stride of K (halves)
+  constexpr int VLD = kKB + 8; // LDS row stride of V^T (halves)
+  constexpr int BAND = kBM + kKB - 1;  // bias-table entries per block
+  using St = Staging<D>;
+  static_assert(St::KCH >= 1 && kKB * D / 8 % kGroup == 0, "K tile split");
+
+  __shared__ __attribute__((aligned(16))) half_t sK[KSPLIT][2][kKB * KLD];
+  __shared__ __attribute__((aligned(16))) half_t sV[KSPLIT][2][D * VLD];
+  __shared__ float sBias[KSPLIT][2][BIAS == kBiasTableF32 ? BAND + 1 : 1];
 
   const int tid = threadIdx.x;
+  const int kg = tid / kGroup;   // key group
+  const int gtid = tid % kGroup; // thread index within the key group
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = gtid >> 6;    // query slice of this wave (0..3)
   const int g = lane >> 5;
   const int ql = lane & 31;
 
@@ -83,191 +117,250 @@ __global__ __launch_bounds__(kThreads) void fa2_fwd_kernel(Fa2Args p) {
   const half_t* Kh = p.K + (int64_t)bh * p.bh_stride_kv;
   const half_t* Vh = p.V + (int64_t)bh * p.bh_stride_kv;
 
+  // Softmax constant c = |scale| log2(e) > 0; a negative scale flips Q.
+  const bool neg = p.scale_log2 < 0.f;
+  const float c = fmaxf(fabsf(p.scale_log2), 1.17549435e-38f);
+
   // Q fragments: B operand of S^T, lane holds Q[q][16*ks + 8*g .. +7].
   half8v qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    qf[ks] = (q < N) ? load_half8(Qh + (int64_t)q * p.stride_q + 16 * ks + 8 * g)
-                     : half8v{};
+    half8v t = (q < N) ? load_half8(Qh + (int64_t)q * p.stride_q + 16 * ks + 8 * g) : half8v{};
+    qf[ks] = neg ? -t : t;
   }
 
-  // Keys this workgroup visits.
+  // Key blocks this workgroup visits; group kg takes blocks kg + KSPLIT*i.
   const int kend = CAUSAL ? min(N, q0 + kBM) : N;
   const int nblk = (kend + kKB - 1) / kKB;
+  const int my_n = nblk > kg ? (nblk - kg + KSPLIT - 1) / KSPLIT : 0;
+  const int iters = (nblk + KSPLIT - 1) / KSPLIT;  // uniform over the workgroup
 
-  // Global -> register staging of the next K/V block.
-  half8v kreg[KCH];
-  half8v vreg[VCH][2];
-  float breg = 0.f;
-
-  auto gload = [&](int kb0) {
+  // Global -> register staging.  Every load is issued unconditionally from a
+  // clamped (in-bounds) address and out-of-range elements are zeroed only
+  // when written to LDS: conditional loads would make the compiler wait for
+  // all outstanding loads (s_waitcnt vmcnt(0)) at every control-flow join.
+  auto gload = [&](St& st, int i) {
+    const int blk = min(kg + KSPLIT * i, nblk - 1);
+    const int kb0 = blk * kKB;
+    st.kb0 = kb0;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + kThreads * i;
-      const int key = kb0 + c / (D / 8);
-      const int col = 8 * (c % (D / 8));
-      kreg[i] = (key < N) ? load_half8(Kh + (int64_t)key * p.stride_kv + col) : half8v{};
+    for (int j = 0; j < St::KCH; ++j) {
+      const int c8 = gtid + kGroup * j;
+      const int key = min(kb0 + c8 / (D / 8), N - 1);
+      st.k[j] = load_half8(Kh + (int64_t)key * p.stride_kv + 8 * (c8 % (D / 8)));
     }
 #pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int j = tid + kThreads * i;
-      if (j < VJOBS) {
-        const int key = kb0 + 2 * (j % (kKB / 2));
-        const int col = 8 * (j / (kKB / 2));
-        vreg[i][0] = (key < N) ? load_half8(Vh + (int64_t)key * p.stride_kv + col) : half8v{};
-        vreg[i][1] = (key + 1 < N) ? load_half8(Vh + (int64_t)(key + 1) * p.stride_kv + col)
-                                   : half8v{};
-      }
+    for (int j = 0; j < St::VCH; ++j) {
+      const int job = min(gtid + kGroup * j, St::VJOBS - 1);
+      const int key = kb0 + 2 * (job % (kKB / 2));
+      const int col = 8 * (job / (kKB / 2));
+      st.v[j][0] = load_half8(Vh + (int64_t)min(key, N - 1) * p.stride_kv + col);
+      st.v[j][1] = load_half8(Vh + (int64_t)min(key + 1, N - 1) * p.stride_kv + col);
     }
     if (BIAS == kBiasTableF32) {
       // Band of table[h][q - key + N - 1] for q in [q0, q0+BM), key in
-      // [kb0, kb0+KB): index base + i with base = q0 - kb0 - (KB-1) + N - 1.
-      const int idx = q0 - kb0 - (kKB - 1) + N - 1 + tid;
+      // [kb0, kb0+KB): entry i is index q0 - kb0 - (KB-1) + N - 1 + i.
+      const int idx = q0 - kb0 - (kKB - 1) + N - 1 + gtid;
       const float* tab = static_cast<const float*>(p.bias) + (int64_t)bh * p.bias_stride_h;
-      breg = (tid < BAND && idx >= 0 && idx <= 2 * N - 2) ? tab[idx] * kLog2e : 0.f;
+      st.b = tab[min(max(idx, 0), 2 * N - 2)];
     }
   };
 
-  auto sstore = [&](int buf) {
+  auto sstore = [&](const St& st, int buf) {
+    half_t* k_l = sK[kg][buf];
+    half_t* v_l = sV[kg][buf];
+    const int kb0 = st.kb0;
+    const bool full = kb0 + kKB <= N;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int c = tid + kThreads * i;
-      *reinterpret_cast<half8v*>(&sK[buf][(c / (D / 8)) * KLD + 8 * (c % (D / 8))]) = kreg[i];
+    for (int j = 0; j < St::KCH; ++j) {
+      const int c8 = gtid + kGroup * j;
+      const int key = kb0 + c8 / (D / 8);
+      const half8v val = (full || key < N) ? st.k[j] : half8v{};
+      *reinterpret_cast<half8v*>(&k_l[(c8 / (D / 8)) * KLD + 8 * (c8 % (D / 8))]) = val;
     }
 #pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int j = tid + kThreads * i;
-      if (j < VJOBS) {
-        const int kp = 2 * (j % (kKB / 2));
-        const int col = 8 * (j / (kKB / 2));
+    for (int j = 0; j < St::VCH; ++j) {
+      const int job = gtid + kGroup * j;
+      if (St::VJOBS % kGroup == 0 || job < St::VJOBS) {
+        const int kp = 2 * (job % (kKB / 2));
+        const int col = 8 * (job / (kKB / 2));
+        const bool ok0 = full || kb0 + kp < N;
+        const bool ok1 = full || kb0 + kp + 1 < N;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          half2v pr = {vreg[i][0][e], vreg[i][1][e]};
-          *reinterpret_cast<half2v*>(&sV[buf][(col + e) * VLD + kp]) = pr;
+          half2v pr = {ok0 ? st.v[j][0][e] : (half_t)0, ok1 ? st.v[j][1][e] : (half_t)0};
+          *reinterpret_cast<half2v*>(&v_l[(col + e) * VLD + kp]) = pr;
         }
       }
     }
     if (BIAS == kBiasTableF32) {
-      if (tid < BAND) sBias[buf][tid] = breg;
+      const int idx = q0 - kb0 - (kKB - 1) + N - 1 + gtid;
+      if (gtid < BAND) sBias[kg][buf][gtid] = (idx >= 0 && idx <= 2 * N - 2) ? st.b * kLog2e : 0.f;
     }
   };
 
-  float m_run = -INFINITY;  // running max (log2 domain), same in lanes l, l^32
+  float m_run = -INFINITY;  // running max (scaled log2 units), same in lanes l, l^32
   float l_run = 0.f;        // this lane's partial row sum
   float16v o[DT];
 #pragma unroll
   for (int u = 0; u < DT; ++u) o[u] = float16v{};
-
   const int krow = kRowPerm(ql);
+  const half2v ones = {(half_t)1.f, (half_t)1.f};
 
-  if (nblk > 0) {
-    gload(0);
-    sstore(0);
-  }
-  __syncthreads();
-
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int buf = blk & 1;
-    const int kb0 = blk * kKB;
-    if (blk + 1 < nblk) gload(kb0 + kKB);
-
+  auto compute = [&](int i, int buf) {
+    const int kb0 = (kg + KSPLIT * i) * kKB;
     // A wave whose queries all precede this key block has nothing to do.
-    const bool active = !CAUSAL || kb0 <= qw0 + 31;
-    if (active) {
-      // ---- S^T = K Q^T for two 32-key tiles ----
-      float16v s[2];
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        s[t] = float16v{};
-        const half_t* kp = &sK[buf][(32 * t + krow) * KLD + 8 * g];
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks) s[t] = mfma32x32x16(load_half8(kp + 16 * ks), qf[ks], s[t]);
-      }
+    if (CAUSAL && kb0 > qw0 + 31) return;
+    const half_t* k_l = sK[kg][buf];
+    const half_t* v_l = sV[kg][buf];
 
-      // ---- logits in the log2 domain, bias, masks ----
-      float x[2][16];
-      const bool tail = kb0 + kKB > N;
-      const bool diag = CAUSAL && kb0 + kKB - 1 > qw0;
+    // ---- S^T = K Q^T for two 32-key tiles ----
+    float16v s[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      s[t] = float16v{};
+      const half_t* kp = &k_l[(32 * t + krow) * KLD + 8 * g];
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) s[t] = mfma32x32x16(load_half8(kp + 16 * ks), qf[ks], s[t]);
+    }
+
+    // ---- logits x (scaled log2 units for bias modes, raw s otherwise) ----
+    const bool masked = (kb0 + kKB > N) || (CAUSAL && kb0 + kKB - 1 > qw0);
+    if (BIAS != kBiasNone) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kr = 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);  // key - kb0
-          float v;
           if (BIAS == kBiasDenseF16) {
             // Reference semantics: (QK^T + B) * scale, B dense [T, T] f16.
             const int key = kb0 + kr;
             const half_t* bp = static_cast<const half_t*>(p.bias) +
                                (int64_t)bh * p.bias_stride_h;
             const float b = (q < N && key < N) ? (float)bp[(int64_t)q * N + key] : 0.f;
-            v = (s[t][r] + b) * p.scale_log2;
-          } else if (BIAS == kBiasTableF32) {
-            // BASELINE semantics: QK^T * scale + table[h][q - key + N - 1].
-            v = s[t][r] * p.scale_log2 + sBias[buf][(q - q0) - kr + (kKB - 1)];
+            s[t][r] = (s[t][r] + (neg ? -b : b)) * c;
           } else {
-            v = s[t][r] * p.scale_log2;
-          }
-          x[t][r] = v;
-        }
-      }
-      if (tail || diag) {
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = kb0 + 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);
-            if (key >= N || (CAUSAL && key > q)) x[t][r] = -INFINITY;
+            // BASELINE semantics: QK^T * scale + table[h][q - key + N - 1].
+            s[t][r] = __builtin_fmaf(s[t][r], c, sBias[kg][buf][(q - q0) - kr + (kKB - 1)]);
           }
         }
       }
-
-      // ---- online softmax ----
-      float mx = -INFINITY;
+    }
+    if (masked) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, x[t][r]);
-      mx = fmaxf(mx, swap_halves(mx));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      m_run = m_new;
-
-      float rs = 0.f;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < 2; ++t) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          x[t][r] = fast_exp2(x[t][r] - m_use);
-          rs += x[t][r];
+          const int key = kb0 + 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);
+          if (key >= N || (CAUSAL && key > q)) s[t][r] = -INFINITY;
         }
-      l_run = l_run * alpha + rs;
+      }
+    }
+
+    // ---- online softmax with lazy rescale ----
+    float mx = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
+    mx = max_halves(mx);
+    // Row max in scaled units (c > 0, so scaling is monotone).
+    const float mx_c = (BIAS != kBiasNone || mx == -INFINITY) ? mx : mx * c;
+    if (__any(mx_c > m_run + kLazyLog2)) {
+      const float m_new = fmaxf(m_run, mx_c);
+      const float alpha = fast_exp2(m_run - m_new);  // 0 on the first block
+      m_run = m_new;
+      l_run *= alpha;
 #pragma unroll
       for (int u = 0; u < DT; ++u)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
 
-      // ---- O^T += V^T P^T, P truncated to f16 (reference :140-145) ----
-      half8v pb[4];
+    half8v pb[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+    for (int t = 0; t < 2; ++t) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) pb[c][e] = (half_t)x[c >> 1][8 * (c & 1) + e];
-#pragma unroll
-      for (int u = 0; u < DT; ++u) {
-        const half_t* vp = &sV[buf][(32 * u + ql) * VLD + 8 * g];
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o[u] = mfma32x32x16(load_half8(vp + 16 * c), pb[c], o[u]);
+      for (int r = 0; r < 16; ++r) {
+        const float e = (BIAS != kBiasNone) ? s[t][r] - m_use : __builtin_fmaf(s[t][r], c, -m_use);
+        pb[2 * t + (r >> 3)][r & 7] = (half_t)fast_exp2(e);
       }
     }
+    // Row sum of the fp16 P that feeds the MFMA (two chains).
+    float ls0 = 0.f, ls1 = 0.f;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const half8v& v8 = pb[cc];
+      ls0 = __builtin_amdgcn_fdot2(half2v{v8[0], v8[1]}, ones, ls0, false);
+      ls1 = __builtin_amdgcn_fdot2(half2v{v8[2], v8[3]}, ones, ls1, false);
+      ls0 = __builtin_amdgcn_fdot2(half2v{v8[4], v8[5]}, ones, ls0, false);
+      ls1 = __builtin_amdgcn_fdot2(half2v{v8[6], v8[7]}, ones, ls1, false);
+    }
+    l_run += ls0 + ls1;
 
-    if (blk + 1 < nblk) sstore(buf ^ 1);
-    __syncthreads();
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int u = 0; u < DT; ++u) {
+      const half_t* vp = &v_l[(32 * u + ql) * VLD + 8 * g];
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) o[u] = mfma32x32x16(load_half8(vp + 16 * cc), pb[cc], o[u]);
+    }
+  };
+
+  // ---- pipelined main loop: loads two blocks ahead, LDS double buffer ----
+  // Loads and LDS stores run unconditionally (blocks past the end are
+  // clamped and never computed) so the load counter stays precise.
+  St stA, stB;
+  gload(stA, 0);
+  gload(stB, 1);
+  sstore(stA, 0);
+  lds_barrier();
+
+  auto step = [&](int i, int buf, St& cur, St& nxt) {
+    gload(cur, i + 2);  // cur's block i is already in LDS
+    if (i < my_n) compute(i, buf);
+    sstore(nxt, buf ^ 1);
+    lds_barrier();
+  };
+  // Always run both halves of the pair (the second may compute nothing) so
+  // every path into the loop header has the same loads outstanding.
+  for (int i = 0; i < iters; i += 2) {
+    step(i, 0, stA, stB);
+    step(i + 1, 1, stB, stA);
+  }
+
+  // ---- merge the key groups ----
+  if constexpr (KSPLIT > 1) {
+    constexpr int SLOTS = 16 * DT + 2;
+    float* red = reinterpret_cast<float*>(&sK[0][0][0]);
+    static_assert(sizeof(sK) >= (size_t)4 * SLOTS * 64 * sizeof(float), "merge buffer");
+    float* mine = red + (size_t)wave * SLOTS * 64 + lane;
+    if (kg == 1) {
+      mine[0] = m_run;
+      mine[64] = l_run;
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mine[(2 + 16 * u + r) * 64] = o[u][r];
+    }
+    lds_barrier();
+    if (kg != 0) return;
+    const float m1 = mine[0];
+    const float l1 = mine[64];
+    const float mm = fmaxf(m_run, m1);
+    const float mu = (mm == -INFINITY) ? 0.f : mm;
+    const float a0 = fast_exp2(m_run - mu);
+    const float a1 = fast_exp2(m1 - mu);
+    l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[u][r] = o[u][r] * a0 + mine[(2 + 16 * u + r) * 64] * a1;
   }
 
   // ---- normalise and store: lane holds O[q][32u + 8b + 4g + 0..3] ----
-  // Lanes l and l^32 hold the same query, so the exchange is uniform.
-  const float l_tot = l_run + swap_halves(l_run);
+  const float l_tot = sum_halves(l_run);
   if (q < N) {
     const float inv = 1.f / fmaxf(l_tot, 1e-6f);
 #pragma unroll
@@ -293,25 +386,34 @@ __global__ __launch_bounds__(kThreads) void fa2_fwd_kernel(Fa2Args p) {
 }
 
 template <int D, bool CAUSAL, int BIAS, bool OUT_F16>
-hipError_t launch_fa2_t(const Fa2Args& a, hipStream_t stream) {
+hipError_t launch_fa2_t(const Fa2Args& a, int ksplit, hipStream_t stream) {
   const int grid = a.num_qblocks * a.batch_heads;
-  hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16>), dim3(grid), dim3(kThreads), 0,
-                     stream, a);
+  if (ksplit == 2) {
+    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 2>), dim3(grid),
+                       dim3(2 * kGroup), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 1>), dim3(grid),
+                       dim3(kGroup), 0, stream, a);
+  }
   return hipGetLastError();
 }
 
 template <int D, int BIAS, bool OUT_F16>
-hipError_t launch_fa2_c(const Fa2Args& a, bool causal, hipStream_t s) {
-  return causal ? launch_fa2_t<D, true, BIAS, OUT_F16>(a, s)
-                : launch_fa2_t<D, false, BIAS, OUT_F16>(a, s);
+hipError_t launch_fa2_c(const Fa2Args& a, bool causal, int ksplit, hipStream_t s) {
+  if constexpr (BIAS == kBiasNone) {
+    if (causal) return launch_fa2_t<D, true, BIAS, OUT_F16>(a, ksplit, s);
+  } else {
+    if (causal) return hipErrorInvalidValue;  // the biased entry point is never causal
+  }
+  return launch_fa2_t<D, false, BIAS, OUT_F16>(a, ksplit, s);
 }
 
 template <int BIAS, bool OUT_F16>
-hipError_t launch_fa2_d(const Fa2Args& a, int d, bool causal, hipStream_t s) {
+hipError_t launch_fa2_d(const Fa2Args& a, int d, bool causal, int ksplit, hipStream_t s) {
   switch (d) {
-    case 32: return launch_fa2_c<32, BIAS, OUT_F16>(a, causal, s);
-    case 64: return launch_fa2_c<64, BIAS, OUT_F16>(a, causal, s);
-    case 128: return launch_fa2_c<128, BIAS, OUT_F16>(a, causal, s);
+    case 32: return launch_fa2_c<32, BIAS, OUT_F16>(a, causal, ksplit, s);
+    case 64: return launch_fa2_c<64, BIAS, OUT_F16>(a, causal, ksplit, s);
+    case 128: return launch_fa2_c<128, BIAS, OUT_F16>(a, causal, ksplit, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -323,16 +425,20 @@ int fa2_query_block() { return kBM; }
 hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool out_f16,
                       hipStream_t stream) {
   a.num_qblocks = (a.N + kBM - 1) / kBM;
+  // Split the keys of a workgroup over two wave groups when the grid alone
+  // gives fewer than two workgroups per compute unit.
+  const int64_t wgs = (int64_t)a.num_qblocks * a.batch_heads;
+  const int ksplit = (a.ksplit > 0) ? a.ksplit : (wgs < 2 * (int64_t)device_cu_count() ? 2 : 1);
   if (bias_kind == kBiasNone) {
-    return out_f16 ? launch_fa2_d<kBiasNone, true>(a, head_dim, causal, stream)
-                   : launch_fa2_d<kBiasNone, false>(a, head_dim, causal, stream);
+    return out_f16 ? launch_fa2_d<kBiasNone, true>(a, head_dim, causal, ksplit, stream)
+                   : launch_fa2_d<kBiasNone, false>(a, head_dim, causal, ksplit, stream);
   }
   if (bias_kind == kBiasTableF32) {
-    return out_f16 ? launch_fa2_d<kBiasTableF32, true>(a, head_dim, causal, stream)
-                   : launch_fa2_d<kBiasTableF32, false>(a, head_dim, causal, stream);
+    return out_f16 ? launch_fa2_d<kBiasTableF32, true>(a, head_dim, causal, ksplit, stream)
+                   : launch_fa2_d<kBiasTableF32, false>(a, head_dim, causal, ksplit, stream);
   }
-  return out_f16 ? launch_fa2_d<kBiasDenseF16, true>(a, head_dim, causal, stream)
-                 : launch_fa2_d<kBiasDenseF16, false>(a, head_dim, causal, stream);
+  return out_f16 ? launch_fa2_d<kBiasDenseF16, true>(a, head_dim, causal, ksplit, stream)
+                 : launch_fa2_d<kBiasDenseF16, false>(a, head_dim, causal, ksplit, stream);
 }
 
 }  // namespace neso

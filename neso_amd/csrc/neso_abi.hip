@@ -4,7 +4,10 @@
 #include <math.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <atomic>
 
 #include "../../include/neso_amd.h"
 #include "neso_internal.h"
@@ -33,6 +36,15 @@ int launched(hipError_t e, const char* what) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
+
+// Optional override of the FA2 key split, for tuning and for tests that
+// exercise both code paths: NESO_AMD_FA2_KSPLIT=1|2.
+int env_ksplit() {
+  const char* v = getenv("NESO_AMD_FA2_KSPLIT");
+  if (!v) return 0;
+  const int k = atoi(v);
+  return (k == 1 || k == 2) ? k : 0;
+}
 
 int check_head_dim(int32_t d) {
   if (d == 32 || d == 64 || d == 128) return NESO_OK;
@@ -175,12 +187,34 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
   a.bias_stride_h = bias_stride_h;
   a.batch_heads = heads;
   a.scale_log2 = scale * 1.4426950408889634f;
+  a.ksplit = env_ksplit();
   return launched(neso::launch_fa2(a, head_dim, causal != 0, bias_kind, out_f16,
                                    static_cast<hipStream_t>(stream)),
                   name);
 }
 
 }  // namespace
+
+namespace neso {
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+  if (dev < kMaxDevices) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  if (dev < kMaxDevices) cache[dev].store(cus, std::memory_order_relaxed);
+  return cus;
+}
+
+}  // namespace neso
 
 extern "C" {
 

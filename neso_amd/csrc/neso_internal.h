@@ -29,7 +29,11 @@ struct Fa2Args {
   int32_t batch_heads;
   float scale_log2;     // softmax scale * log2(e)
   int32_t num_qblocks;  // filled in by launch_fa2
+  int32_t ksplit;       // key groups per workgroup (1, 2); 0 = chosen from the grid size
 };
+
+// Compute units of the current device (cached per device).
+int device_cu_count();
 
 int fa2_query_block();
 hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool out_f16,
