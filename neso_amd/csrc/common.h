@@ -54,6 +54,28 @@ __device__ __forceinline__ half8v load_half8(const half_t* p) {
   return *reinterpret_cast<const half8v*>(p);
 }
 
+// Raw buffer resource over [base, base + bytes).  Buffer loads whose offset
+// lies past `bytes` return zeros and such stores are dropped, which gives
+// tail handling without per-element compares or clamped addresses.
+// dword3 = 0x00020000: 32-bit data format, no swizzle (gfx9 family).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
+}
+__device__ __forceinline__ half8v buf_load_half8(rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(half8v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
+}
+__device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
+}
+__device__ __forceinline__ void buf_store_f32x4(float4v v, rsrc_t r, uint32_t byte_off) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4v, v), r, byte_off, 0, 0);
+}
+__device__ __forceinline__ void buf_store_f16x4(half4v v, rsrc_t r, uint32_t byte_off) {
+  typedef int int2v __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(int2v, v), r, byte_off, 0, 0);
+}
+
 // Workgroup barrier that orders LDS accesses only.  __syncthreads() also
 // fences global memory, which makes the compiler drain every outstanding
 // global load (s_waitcnt vmcnt(0)) at the barrier and defeats prefetching.

@@ -79,7 +79,6 @@ struct Staging {
   half8v k[KCH];
   half8v v[VCH][2];
   float b;
-  int kb0;  // first key of the staged block
 };
 
 template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int KSPLIT>
@@ -122,10 +121,13 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   const float c = fmaxf(fabsf(p.scale_log2), 1.17549435e-38f);
 
   // Q fragments: B operand of S^T, lane holds Q[q][16*ks + 8*g .. +7].
+  // Rows past N read as zeros (buffer bounds check).
+  const int qrows = min(N - q0, kBM);
+  const rsrc_t rsQ = make_rsrc(Qh + (int64_t)q0 * p.stride_q, (uint32_t)qrows * p.stride_q * 2);
   half8v qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    half8v t = (q < N) ? load_half8(Qh + (int64_t)q * p.stride_q + 16 * ks + 8 * g) : half8v{};
+    half8v t = buf_load_half8(rsQ, ((q - q0) * p.stride_q + 16 * ks + 8 * g) * 2);
     qf[ks] = neg ? -t : t;
   }
 
@@ -135,48 +137,56 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   const int my_n = nblk > kg ? (nblk - kg + KSPLIT - 1) / KSPLIT : 0;
   const int iters = (nblk + KSPLIT - 1) / KSPLIT;  // uniform over the workgroup
 
-  // Global -> register staging.  Every load is issued unconditionally from a
-  // clamped (in-bounds) address and out-of-range elements are zeroed only
-  // when written to LDS: conditional loads would make the compiler wait for
-  // all outstanding loads (s_waitcnt vmcnt(0)) at every control-flow join.
-  auto gload = [&](St& st, int i) {
-    const int blk = min(kg + KSPLIT * i, nblk - 1);
-    const int kb0 = blk * kKB;
-    st.kb0 = kb0;
+  // Global -> register staging through per-block buffer resources: the
+  // block's base and extent are scalar, each thread's byte offsets are
+  // constant, and rows past N read as zeros.  The same number of loads is
+  // issued every step (blocks past the end are clamped and never computed)
+  // so the compiler's load counter stays exact across the loop.
+  uint32_t k_off[St::KCH];
 #pragma unroll
-    for (int j = 0; j < St::KCH; ++j) {
-      const int c8 = gtid + kGroup * j;
-      const int key = min(kb0 + c8 / (D / 8), N - 1);
-      st.k[j] = load_half8(Kh + (int64_t)key * p.stride_kv + 8 * (c8 % (D / 8)));
-    }
+  for (int j = 0; j < St::KCH; ++j) {
+    const int c8 = gtid + kGroup * j;
+    k_off[j] = ((c8 / (D / 8)) * p.stride_kv + 8 * (c8 % (D / 8))) * 2;
+  }
+  uint32_t v_off[St::VCH];
+#pragma unroll
+  for (int j = 0; j < St::VCH; ++j) {
+    const int job = min(gtid + kGroup * j, St::VJOBS - 1);
+    v_off[j] = (2 * (job % (kKB / 2)) * p.stride_kv + 8 * (job / (kKB / 2))) * 2;
+  }
+  const int kgu = __builtin_amdgcn_readfirstlane(kg);  // wave-uniform
+
+  auto gload = [&](St& st, int i) {
+    const int blk = min(kgu + KSPLIT * i, nblk - 1);
+    const int kb0 = blk * kKB;
+    const uint32_t bytes = (uint32_t)min(N - kb0, kKB) * p.stride_kv * 2;
+    const rsrc_t rk = make_rsrc(Kh + (int64_t)kb0 * p.stride_kv, bytes);
+    const rsrc_t rv = make_rsrc(Vh + (int64_t)kb0 * p.stride_kv, bytes);
+#pragma unroll
+    for (int j = 0; j < St::KCH; ++j) st.k[j] = buf_load_half8(rk, k_off[j]);
 #pragma unroll
     for (int j = 0; j < St::VCH; ++j) {
-      const int job = min(gtid + kGroup * j, St::VJOBS - 1);
-      const int key = kb0 + 2 * (job % (kKB / 2));
-      const int col = 8 * (job / (kKB / 2));
-      st.v[j][0] = load_half8(Vh + (int64_t)min(key, N - 1) * p.stride_kv + col);
-      st.v[j][1] = load_half8(Vh + (int64_t)min(key + 1, N - 1) * p.stride_kv + col);
+      st.v[j][0] = buf_load_half8(rv, v_off[j]);
+      st.v[j][1] = buf_load_half8(rv, v_off[j] + p.stride_kv * 2);
     }
     if (BIAS == kBiasTableF32) {
       // Band of table[h][q - key + N - 1] for q in [q0, q0+BM), key in
-      // [kb0, kb0+KB): entry i is index q0 - kb0 - (KB-1) + N - 1 + i.
+      // [kb0, kb0+KB): entry i is index q0 - kb0 - (KB-1) + N - 1 + i;
+      // indices outside [0, 2N-2] read as zero.
       const int idx = q0 - kb0 - (kKB - 1) + N - 1 + gtid;
-      const float* tab = static_cast<const float*>(p.bias) + (int64_t)bh * p.bias_stride_h;
-      st.b = tab[min(max(idx, 0), 2 * N - 2)];
+      const rsrc_t rb = make_rsrc(static_cast<const float*>(p.bias) + (int64_t)bh * p.bias_stride_h,
+                                  (uint32_t)(2 * N - 1) * 4);
+      st.b = buf_load_f32(rb, (uint32_t)idx * 4u);
     }
   };
 
   auto sstore = [&](const St& st, int buf) {
     half_t* k_l = sK[kg][buf];
     half_t* v_l = sV[kg][buf];
-    const int kb0 = st.kb0;
-    const bool full = kb0 + kKB <= N;
 #pragma unroll
     for (int j = 0; j < St::KCH; ++j) {
       const int c8 = gtid + kGroup * j;
-      const int key = kb0 + c8 / (D / 8);
-      const half8v val = (full || key < N) ? st.k[j] : half8v{};
-      *reinterpret_cast<half8v*>(&k_l[(c8 / (D / 8)) * KLD + 8 * (c8 % (D / 8))]) = val;
+      *reinterpret_cast<half8v*>(&k_l[(c8 / (D / 8)) * KLD + 8 * (c8 % (D / 8))]) = st.k[j];
     }
 #pragma unroll
     for (int j = 0; j < St::VCH; ++j) {
@@ -184,18 +194,15 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
       if (St::VJOBS % kGroup == 0 || job < St::VJOBS) {
         const int kp = 2 * (job % (kKB / 2));
         const int col = 8 * (job / (kKB / 2));
-        const bool ok0 = full || kb0 + kp < N;
-        const bool ok1 = full || kb0 + kp + 1 < N;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          half2v pr = {ok0 ? st.v[j][0][e] : (half_t)0, ok1 ? st.v[j][1][e] : (half_t)0};
+          half2v pr = {st.v[j][0][e], st.v[j][1][e]};
           *reinterpret_cast<half2v*>(&v_l[(col + e) * VLD + kp]) = pr;
         }
       }
     }
     if (BIAS == kBiasTableF32) {
-      const int idx = q0 - kb0 - (kKB - 1) + N - 1 + gtid;
-      if (gtid < BAND) sBias[kg][buf][gtid] = (idx >= 0 && idx <= 2 * N - 2) ? st.b * kLog2e : 0.f;
+      if (gtid < BAND) sBias[kg][buf][gtid] = st.b * kLog2e;
     }
   };
 
@@ -360,26 +367,25 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   }
 
   // ---- normalise and store: lane holds O[q][32u + 8b + 4g + 0..3] ----
+  // Rows past N fall outside the buffer resource and are dropped.
   const float l_tot = sum_halves(l_run);
-  if (q < N) {
-    const float inv = 1.f / fmaxf(l_tot, 1e-6f);
+  const float inv = 1.f / fmaxf(l_tot, 1e-6f);
+  constexpr int ES = OUT_F16 ? 2 : 4;
+  const rsrc_t rsO = make_rsrc(static_cast<char*>(p.O) +
+                                   ((int64_t)bh * p.bh_stride_o + (int64_t)q0 * p.stride_o) * ES,
+                               (uint32_t)qrows * p.stride_o * ES);
 #pragma unroll
-    for (int u = 0; u < DT; ++u) {
+  for (int u = 0; u < DT; ++u) {
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int col = 32 * u + 8 * b + 4 * g;
-        float4v v = {o[u][4 * b] * inv, o[u][4 * b + 1] * inv, o[u][4 * b + 2] * inv,
-                     o[u][4 * b + 3] * inv};
-        if (OUT_F16) {
-          half_t* op = static_cast<half_t*>(p.O) + (int64_t)bh * p.bh_stride_o +
-                       (int64_t)q * p.stride_o + col;
-          half4v hv = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
-          *reinterpret_cast<half4v*>(op) = hv;
-        } else {
-          float* op = static_cast<float*>(p.O) + (int64_t)bh * p.bh_stride_o +
-                      (int64_t)q * p.stride_o + col;
-          *reinterpret_cast<float4v*>(op) = v;
-        }
+    for (int b = 0; b < 4; ++b) {
+      const int col = 32 * u + 8 * b + 4 * g;
+      const uint32_t off = ((q - q0) * p.stride_o + col) * ES;
+      float4v v = {o[u][4 * b] * inv, o[u][4 * b + 1] * inv, o[u][4 * b + 2] * inv,
+                   o[u][4 * b + 3] * inv};
+      if (OUT_F16) {
+        buf_store_f16x4(half4v{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]}, rsO, off);
+      } else {
+        buf_store_f32x4(v, rsO, off);
       }
     }
   }
