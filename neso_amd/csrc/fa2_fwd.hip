@@ -91,15 +91,20 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   using St = Staging<D>;
   static_assert(St::KCH >= 1 && kKB * D / 8 % kGroup == 0, "K tile split");
 
-  __shared__ __attribute__((aligned(16))) half_t sK[KSPLIT][2][kKB * KLD];
-  __shared__ __attribute__((aligned(16))) half_t sV[KSPLIT][2][D * VLD];
+  // LDS: per key group two block slots, each K [KB][KLD] then V^T [D][VLD]
+  // (halves); reused after the loop for the key-group merge.
+  constexpr int KHALF = kKB * KLD;
+  constexpr int SLOT = KHALF + D * VLD;
+  __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * 2 * SLOT];
   __shared__ float sBias[KSPLIT][2][BIAS == kBiasTableF32 ? BAND + 1 : 1];
 
   const int tid = threadIdx.x;
-  const int kg = tid / kGroup;   // key group
-  const int gtid = tid % kGroup; // thread index within the key group
+  // Key group and wave index are wave-uniform; readfirstlane tells the
+  // compiler so, which keeps branches on them scalar (not if-converted).
+  const int kg = __builtin_amdgcn_readfirstlane(tid / kGroup);  // key group
+  const int gtid = tid % kGroup;  // thread index within the key group
   const int lane = tid & 63;
-  const int wave = gtid >> 6;    // query slice of this wave (0..3)
+  const int wave = __builtin_amdgcn_readfirstlane(gtid >> 6);  // query slice (0..3)
   const int g = lane >> 5;
   const int ql = lane & 31;
 
@@ -154,7 +159,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     const int job = min(gtid + kGroup * j, St::VJOBS - 1);
     v_off[j] = (2 * (job % (kKB / 2)) * p.stride_kv + 8 * (job / (kKB / 2))) * 2;
   }
-  const int kgu = __builtin_amdgcn_readfirstlane(kg);  // wave-uniform
+  const int kgu = kg;
 
   auto gload = [&](St& st, int i) {
     const int blk = min(kgu + KSPLIT * i, nblk - 1);
@@ -181,8 +186,8 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   };
 
   auto sstore = [&](const St& st, int buf) {
-    half_t* k_l = sK[kg][buf];
-    half_t* v_l = sV[kg][buf];
+    half_t* k_l = &smem[(kg * 2 + buf) * SLOT];
+    half_t* v_l = k_l + KHALF;
 #pragma unroll
     for (int j = 0; j < St::KCH; ++j) {
       const int c8 = gtid + kGroup * j;
@@ -218,8 +223,8 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     const int kb0 = (kg + KSPLIT * i) * kKB;
     // A wave whose queries all precede this key block has nothing to do.
     if (CAUSAL && kb0 > qw0 + 31) return;
-    const half_t* k_l = sK[kg][buf];
-    const half_t* v_l = sV[kg][buf];
+    const half_t* k_l = &smem[(kg * 2 + buf) * SLOT];
+    const half_t* v_l = k_l + KHALF;
 
     // ---- S^T = K Q^T for two 32-key tiles ----
     float16v s[2];
@@ -254,14 +259,16 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
       }
     }
     if (masked) {
+      // Keeps this a real (scalar) branch: if-converted, the masking would
+      // cost 64 VALU ops on every block instead of on the few masked ones.
+      asm volatile("");
+      // key >= lim is invisible to this lane's query.
+      const int lim = (CAUSAL ? min(N, q + 1) : N) - kb0 - 8 * g;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int key = kb0 + 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);
-          if (key >= N || (CAUSAL && key > q)) s[t][r] = -INFINITY;
-        }
-      }
+        for (int r = 0; r < 16; ++r)
+          if (32 * t + 16 * (r >> 3) + (r & 7) >= lim) s[t][r] = -INFINITY;
     }
 
     // ---- online softmax with lazy rescale ----
@@ -338,12 +345,15 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   }
 
   // ---- merge the key groups ----
+  // Groups 1..KSPLIT-1 publish (m, l, O) per lane; group 0 folds them in
+  // order.  Lane layout is identical across groups (same query slice).
   if constexpr (KSPLIT > 1) {
     constexpr int SLOTS = 16 * DT + 2;
-    float* red = reinterpret_cast<float*>(&sK[0][0][0]);
-    static_assert(sizeof(sK) >= (size_t)4 * SLOTS * 64 * sizeof(float), "merge buffer");
-    float* mine = red + (size_t)wave * SLOTS * 64 + lane;
-    if (kg == 1) {
+    constexpr int PART = 4 * SLOTS * 64;  // floats per published group
+    static_assert(sizeof(smem) >= (size_t)(KSPLIT - 1) * PART * sizeof(float), "merge buffer");
+    float* red = reinterpret_cast<float*>(smem) + (size_t)wave * SLOTS * 64 + lane;
+    if (kg > 0) {
+      float* mine = red + (size_t)(kg - 1) * PART;
       mine[0] = m_run;
       mine[64] = l_run;
 #pragma unroll
@@ -353,17 +363,22 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     }
     lds_barrier();
     if (kg != 0) return;
-    const float m1 = mine[0];
-    const float l1 = mine[64];
-    const float mm = fmaxf(m_run, m1);
-    const float mu = (mm == -INFINITY) ? 0.f : mm;
-    const float a0 = fast_exp2(m_run - mu);
-    const float a1 = fast_exp2(m1 - mu);
-    l_run = l_run * a0 + l1 * a1;
 #pragma unroll
-    for (int u = 0; u < DT; ++u)
+    for (int j = 0; j < KSPLIT - 1; ++j) {
+      const float* other = red + (size_t)j * PART;
+      const float m1 = other[0];
+      const float l1 = other[64];
+      const float mm = fmaxf(m_run, m1);
+      const float mu = (mm == -INFINITY) ? 0.f : mm;
+      const float a0 = fast_exp2(m_run - mu);
+      const float a1 = fast_exp2(m1 - mu);
+      m_run = mm;
+      l_run = l_run * a0 + l1 * a1;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[u][r] = o[u][r] * a0 + mine[(2 + 16 * u + r) * 64] * a1;
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[u][r] = o[u][r] * a0 + other[(2 + 16 * u + r) * 64] * a1;
+    }
   }
 
   // ---- normalise and store: lane holds O[q][32u + 8b + 4g + 0..3] ----
@@ -394,12 +409,30 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
 template <int D, bool CAUSAL, int BIAS, bool OUT_F16>
 hipError_t launch_fa2_t(const Fa2Args& a, int ksplit, hipStream_t stream) {
   const int grid = a.num_qblocks * a.batch_heads;
-  if (ksplit == 2) {
-    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 2>), dim3(grid),
-                       dim3(2 * kGroup), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 1>), dim3(grid),
-                       dim3(kGroup), 0, stream, a);
+  // More key groups need more LDS slots: 2 groups fit at every head dim,
+  // 3-4 only up to d = 64.
+  switch (ksplit) {
+    case 4:
+      if constexpr (D <= 64) {
+        hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 4>), dim3(grid),
+                           dim3(4 * kGroup), 0, stream, a);
+        break;
+      }
+      [[fallthrough]];
+    case 3:
+      if constexpr (D <= 64) {
+        hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 3>), dim3(grid),
+                           dim3(3 * kGroup), 0, stream, a);
+        break;
+      }
+      [[fallthrough]];
+    case 2:
+      hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 2>), dim3(grid),
+                         dim3(2 * kGroup), 0, stream, a);
+      break;
+    default:
+      hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 1>), dim3(grid),
+                         dim3(kGroup), 0, stream, a);
   }
   return hipGetLastError();
 }

@@ -38,12 +38,12 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 bool aligned2(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 1u) == 0; }
 
 // Optional override of the FA2 key split, for tuning and for tests that
-// exercise both code paths: NESO_AMD_FA2_KSPLIT=1|2.
+// exercise every code path: NESO_AMD_FA2_KSPLIT=1..4.
 int env_ksplit() {
   const char* v = getenv("NESO_AMD_FA2_KSPLIT");
   if (!v) return 0;
   const int k = atoi(v);
-  return (k == 1 || k == 2) ? k : 0;
+  return (k >= 1 && k <= 4) ? k : 0;
 }
 
 int check_head_dim(int32_t d) {
