@@ -44,7 +44,6 @@ namespace neso {
 namespace {
 
 constexpr int kBM = 128;       // queries per workgroup
-constexpr int kKB = 64;        // keys per LDS block
 constexpr int kGroup = 256;    // threads per key group (4 waves)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.f;  // rescale threshold (log2 units)
@@ -71,8 +70,14 @@ __device__ __forceinline__ float sum_halves(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Keys per LDS block.  64 measured faster than 128 at d = 64 on MI355X
+// (fewer live registers; the extra barriers are not the bottleneck).
+template <int D>
+constexpr int key_block() { return 64; }
+
 template <int D>
 struct Staging {
+  static constexpr int kKB = key_block<D>();
   static constexpr int KCH = kKB * D / 8 / kGroup;   // 16-byte K chunks per thread
   static constexpr int VJOBS = kKB * D / 16;         // (key pair, 8 columns) jobs
   static constexpr int VCH = (VJOBS + kGroup - 1) / kGroup;
@@ -83,6 +88,8 @@ struct Staging {
 
 template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int KSPLIT>
 __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
+  constexpr int kKB = key_block<D>();
+  constexpr int NT = kKB / 32; // 32-key tiles per block
   constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;   // 32-row tiles of O^T
   constexpr int KLD = D + 8;   // LDS row stride of K (halves)
@@ -226,10 +233,10 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     const half_t* k_l = &smem[(kg * 2 + buf) * SLOT];
     const half_t* v_l = k_l + KHALF;
 
-    // ---- S^T = K Q^T for two 32-key tiles ----
-    float16v s[2];
+    // ---- S^T = K Q^T for NT 32-key tiles ----
+    float16v s[NT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < NT; ++t) {
       s[t] = float16v{};
       const half_t* kp = &k_l[(32 * t + krow) * KLD + 8 * g];
 #pragma unroll
@@ -240,7 +247,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     const bool masked = (kb0 + kKB > N) || (CAUSAL && kb0 + kKB - 1 > qw0);
     if (BIAS != kBiasNone) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < NT; ++t) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kr = 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);  // key - kb0
@@ -265,19 +272,27 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
       // key >= lim is invisible to this lane's query.
       const int lim = (CAUSAL ? min(N, q + 1) : N) - kb0 - 8 * g;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r)
           if (32 * t + 16 * (r >> 3) + (r & 7) >= lim) s[t][r] = -INFINITY;
     }
 
     // ---- online softmax with lazy rescale ----
-    float mx = -INFINITY;
+    // Tree reduction (independent v_max3 chains per 8 values).
+    float m8[2 * NT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int cc = 0; cc < 2 * NT; ++cc) {
+      const float16v& v = s[cc >> 1];
+      const int o8 = 8 * (cc & 1);
+      m8[cc] = fmaxf(fmaxf(fmaxf(v[o8], v[o8 + 1]), fmaxf(v[o8 + 2], v[o8 + 3])),
+                     fmaxf(fmaxf(v[o8 + 4], v[o8 + 5]), fmaxf(v[o8 + 6], v[o8 + 7])));
+    }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[t][r]);
-    mx = max_halves(mx);
+    for (int w = 1; w < 2 * NT; w *= 2)
+#pragma unroll
+      for (int cc = 0; cc + w < 2 * NT; cc += 2 * w) m8[cc] = fmaxf(m8[cc], m8[cc + w]);
+    const float mx = max_halves(m8[0]);
     // Row max in scaled units (c > 0, so scaling is monotone).
     const float mx_c = (BIAS != kBiasNone || mx == -INFINITY) ? mx : mx * c;
     if (__any(mx_c > m_run + kLazyLog2)) {
@@ -292,33 +307,37 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     }
     const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
 
-    half8v pb[4];
+    half8v pb[2 * NT];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+    for (int t = 0; t < NT; ++t) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float e = (BIAS != kBiasNone) ? s[t][r] - m_use : __builtin_fmaf(s[t][r], c, -m_use);
         pb[2 * t + (r >> 3)][r & 7] = (half_t)fast_exp2(e);
       }
     }
-    // Row sum of the fp16 P that feeds the MFMA (two chains).
-    float ls0 = 0.f, ls1 = 0.f;
+    // Row sum of the fp16 P that feeds the MFMA (one dot2 chain per chunk).
+    float ls[2 * NT];
 #pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
+    for (int cc = 0; cc < 2 * NT; ++cc) {
       const half8v& v8 = pb[cc];
-      ls0 = __builtin_amdgcn_fdot2(half2v{v8[0], v8[1]}, ones, ls0, false);
-      ls1 = __builtin_amdgcn_fdot2(half2v{v8[2], v8[3]}, ones, ls1, false);
-      ls0 = __builtin_amdgcn_fdot2(half2v{v8[4], v8[5]}, ones, ls0, false);
-      ls1 = __builtin_amdgcn_fdot2(half2v{v8[6], v8[7]}, ones, ls1, false);
+      float a = __builtin_amdgcn_fdot2(half2v{v8[0], v8[1]}, ones, 0.f, false);
+      a = __builtin_amdgcn_fdot2(half2v{v8[2], v8[3]}, ones, a, false);
+      a = __builtin_amdgcn_fdot2(half2v{v8[4], v8[5]}, ones, a, false);
+      ls[cc] = __builtin_amdgcn_fdot2(half2v{v8[6], v8[7]}, ones, a, false);
     }
-    l_run += ls0 + ls1;
+#pragma unroll
+    for (int w = 1; w < 2 * NT; w *= 2)
+#pragma unroll
+      for (int cc = 0; cc + w < 2 * NT; cc += 2 * w) ls[cc] += ls[cc + w];
+    l_run += ls[0];
 
     // ---- O^T += V^T P^T ----
 #pragma unroll
     for (int u = 0; u < DT; ++u) {
       const half_t* vp = &v_l[(32 * u + ql) * VLD + 8 * g];
 #pragma unroll
-      for (int cc = 0; cc < 4; ++cc) o[u] = mfma32x32x16(load_half8(vp + 16 * cc), pb[cc], o[u]);
+      for (int cc = 0; cc < 2 * NT; ++cc) o[u] = mfma32x32x16(load_half8(vp + 16 * cc), pb[cc], o[u]);
     }
   };
 
@@ -406,34 +425,33 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   }
 }
 
+// Static LDS of one workgroup with K key groups.
+template <int D, int BIAS>
+constexpr int fa2_lds_bytes(int K) {
+  constexpr int kb = key_block<D>();
+  const int slot = (kb * (D + 8) + D * (kb + 8)) * 2;
+  const int bias = BIAS == kBiasTableF32 ? (kBM + kb) * 4 : 4;
+  return K * 2 * (slot + bias);
+}
+
+template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int K>
+bool launch_fa2_k(const Fa2Args& a, hipStream_t stream) {
+  if constexpr (fa2_lds_bytes<D, BIAS>(K) <= 160 * 1024) {
+    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, K>),
+                       dim3(a.num_qblocks * a.batch_heads), dim3(K * kGroup), 0, stream, a);
+    return true;
+  }
+  return false;
+}
+
 template <int D, bool CAUSAL, int BIAS, bool OUT_F16>
 hipError_t launch_fa2_t(const Fa2Args& a, int ksplit, hipStream_t stream) {
-  const int grid = a.num_qblocks * a.batch_heads;
-  // More key groups need more LDS slots: 2 groups fit at every head dim,
-  // 3-4 only up to d = 64.
-  switch (ksplit) {
-    case 4:
-      if constexpr (D <= 64) {
-        hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 4>), dim3(grid),
-                           dim3(4 * kGroup), 0, stream, a);
-        break;
-      }
-      [[fallthrough]];
-    case 3:
-      if constexpr (D <= 64) {
-        hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 3>), dim3(grid),
-                           dim3(3 * kGroup), 0, stream, a);
-        break;
-      }
-      [[fallthrough]];
-    case 2:
-      hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 2>), dim3(grid),
-                         dim3(2 * kGroup), 0, stream, a);
-      break;
-    default:
-      hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, 1>), dim3(grid),
-                         dim3(kGroup), 0, stream, a);
-  }
+  // Use the requested key split, or the largest smaller one whose LDS fits.
+  bool done = false;
+  if (ksplit >= 4) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 4>(a, stream);
+  if (!done && ksplit >= 3) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 3>(a, stream);
+  if (!done && ksplit >= 2) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 2>(a, stream);
+  if (!done) launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 1>(a, stream);
   return hipGetLastError();
 }
 
