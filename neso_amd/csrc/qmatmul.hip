@@ -15,6 +15,8 @@
 //
 // W8A16 (tests/test_quantized_matmul.py:67-167 and :181-283): C[M][N] f32 =
 // A[M][K] f16 * f16(B[K][N] int8) [* scale[n] after accumulation].
+#include <stdlib.h>
+
 #include "common.h"
 #include "neso_internal.h"
 
@@ -38,89 +40,173 @@ __device__ __forceinline__ void unpack_word(uint32_t w, half2v z1, half2v z16, h
 }
 
 // ---------------------------------------------------------------------------
-// GEMV regime.  MR activation rows, ROWS weight rows per wave, GI 16-byte
-// group loads per lane per row (K <= 2048 * GI).
-template <int MR, int ROWS, int GI>
+// GEMV regime (M <= 4): a persistent stream of weight rows.
+//
+// Wave w handles rows w, w + T, w + 2T, ... (T = waves in the grid), so at
+// any moment the grid streams one contiguous stretch of W.  Lane l owns the
+// 32-code chunks l + 64*gi of a row: one 16-byte load per chunk, a wave
+// reads 1 KiB contiguous per instruction.  The next row's words and scales
+// are loaded while the current row is reduced.  Rows and chunks past the
+// end come back as zeros from the buffer bounds check.
+//
+// Dequantisation without the zero-point subtraction: the exponent trick
+// yields (1024 + c) and (1024 + 16 c) as f16, v_dot2_f32_f16 accumulates
+// them against X pairs, and the per-chunk constant
+//   corr = -(1024 + z) * S_A - (64 + z) * S_B
+// (S_A, S_B = sums of the X elements paired with the two nibble sets)
+// restores sum((c - z) x) = acc1 + acc16 / 16 + corr exactly in real
+// arithmetic.  Per 8 codes: 1 shift, 4 v_and_or_b32, 4 v_dot2.
+
+// 32-bit constants the compiler cannot fold back into literals: gfx9 VOP3
+// encodings take no literal and read at most one SGPR, so v_and_or_b32
+// needs its two constants as one SGPR and one VGPR.
+__device__ __forceinline__ uint32_t sgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
+  return r;
+}
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+  return r;
+}
+
+// Sum over the 64 lanes with DPP row operations; the total lands in lane 63
+// and is returned to every lane.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_add(float v) {
+  const int s = __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false);
+  return v + __int_as_float(s);
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v = dpp_add<0xB1, 0xF>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E, 0xF>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141, 0xF>(v);  // row_half_mirror
+  v = dpp_add<0x140, 0xF>(v);  // row_mirror
+  v = dpp_add<0x142, 0xA>(v);  // row_bcast:15
+  v = dpp_add<0x143, 0xC>(v);  // row_bcast:31
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+template <int GI>
+struct GemvRow {
+  uint4v w[GI];
+  float s[GI];
+};
+
+template <int MR, int GI, int R>
 __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int G = a.K >> 5;        // 32-code chunks per row
+  const int wid = blockIdx.x * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int T = gridDim.x * (kThreads / kWave);
   const int KW = a.K >> 3;       // words per row
   const int SG = a.K / a.group;  // scales per row
-  const int n0 = (blockIdx.x * (kThreads / kWave) + wave) * ROWS;
-  if (n0 >= a.N) return;
+  const uint32_t mlo = sgpr_const(0x000F000Fu);
+  const uint32_t mhi = sgpr_const(0x00F000F0u);
+  const uint32_t mag = vgpr_const(0x64006400u);
 
-  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
-  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  half2v xp[MR][GI][16];  // X pairs (filled after the first weight loads)
+  float corr[MR][GI];
 
-  // Weight words and scales first: the HBM stream is what this kernel waits on.
-  uint4v wv[ROWS][GI];
-  float sc[ROWS][GI];
-#pragma unroll
-  for (int rr = 0; rr < ROWS; ++rr) {
-    const int n = n0 + rr;
+  auto load_row = [&](GemvRow<GI>& r, int n) {
+    // Rows past the end get an empty buffer resource: all loads return 0.
+    const bool ok = n < a.N;
+    const rsrc_t rw = make_rsrc(a.W + (int64_t)(ok ? n : 0) * KW, ok ? (uint32_t)KW * 4 : 0u);
+    const rsrc_t rs = make_rsrc(a.S + (int64_t)(ok ? n : 0) * SG, ok ? (uint32_t)SG * 2 : 0u);
 #pragma unroll
     for (int gi = 0; gi < GI; ++gi) {
       const int gch = lane + 64 * gi;
-      const bool ok = n < a.N && gch < G;
-      wv[rr][gi] = ok ? *reinterpret_cast<const uint4v*>(a.W + (int64_t)n * KW + 4 * gch)
-                      : uint4v{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
-      sc[rr][gi] = ok ? (float)a.S[(int64_t)n * SG + (32 * gch) / a.group] : 0.f;
+      r.w[gi] = __builtin_bit_cast(uint4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rw, (uint32_t)gch * 16u, 0, 0));
+      const uint32_t sidx = (uint32_t)(32 * gch) / (uint32_t)a.group;
+      r.s[gi] = (float)__builtin_bit_cast(
+          half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, sidx * 2u, 0, 0));
     }
-  }
+  };
 
-  // X pairs: for word i of chunk gi, xp[.][gi][4i + e] pairs element e with
-  // element e + 4 of that word's eight columns (the order unpack_word gives).
-  half2v xp[MR][GI][16];
+  auto row_dot = [&](const GemvRow<GI>& r, float (&y)[MR]) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) y[m] = 0.f;
+#pragma unroll
+    for (int gi = 0; gi < GI; ++gi) {
+      float a1[MR][2], a16[MR][2];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) a1[m][0] = a1[m][1] = a16[m][0] = a16[m][1] = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w = r.w[gi][i];
+        const uint32_t w8 = w >> 8;
+        const half2v h0 = as_half2((w & mlo) | mag);    // (1024 + c0, 1024 + c4)
+        const half2v h1 = as_half2((w & mhi) | mag);    // (1024 + 16 c1, 1024 + 16 c5)
+        const half2v h2 = as_half2((w8 & mlo) | mag);   // (1024 + c2, 1024 + c6)
+        const half2v h3 = as_half2((w8 & mhi) | mag);   // (1024 + 16 c3, 1024 + 16 c7)
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          a1[m][i & 1] = __builtin_amdgcn_fdot2(h0, xp[m][gi][4 * i + 0], a1[m][i & 1], false);
+          a16[m][i & 1] = __builtin_amdgcn_fdot2(h1, xp[m][gi][4 * i + 1], a16[m][i & 1], false);
+          a1[m][i & 1] = __builtin_amdgcn_fdot2(h2, xp[m][gi][4 * i + 2], a1[m][i & 1], false);
+          a16[m][i & 1] = __builtin_amdgcn_fdot2(h3, xp[m][gi][4 * i + 3], a16[m][i & 1], false);
+        }
+      }
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float gd = (a1[m][0] + a1[m][1]) + (a16[m][0] + a16[m][1]) * 0.0625f + corr[m][gi];
+        y[m] = __builtin_fmaf(gd, r.s[gi], y[m]);
+      }
+    }
+  };
+
+  // Wave w handles rows w + k*T, k < R, in straight-line code (a loop
+  // back-edge makes the compiler drain every outstanding load).  A ring of
+  // PF rows is in flight; the first PF are requested before X is read.
+  // Rows past N read zeros and their (lane-0) stores fall outside ry.
+  constexpr int PF = R < 4 ? R : 4;
+  GemvRow<GI> ring[PF];
+#pragma unroll
+  for (int k = 0; k < PF; ++k) load_row(ring[k], wid + k * T);
+
+  // X pairs and per-chunk corrections, once per wave.  Buffer loads: rows
+  // m >= M and chunks past K read as zeros, with no branch around them.
+  rsrc_t rx[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+    rx[m] = make_rsrc(a.X + (int64_t)(m < a.M ? m : 0) * a.ldx, m < a.M ? (uint32_t)a.K * 2 : 0u);
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
 #pragma unroll
     for (int gi = 0; gi < GI; ++gi) {
       const int gch = lane + 64 * gi;
+      float sa = 0.f, sb = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const half8v x = (m < a.M && gch < G)
-                             ? load_half8(a.X + (int64_t)m * a.ldx + 32 * gch + 8 * i)
-                             : half8v{};
+        const half8v x = buf_load_half8(rx[m], (uint32_t)(32 * gch + 8 * i) * 2u);
         xp[m][gi][4 * i + 0] = half2v{x[0], x[4]};
         xp[m][gi][4 * i + 1] = half2v{x[1], x[5]};
         xp[m][gi][4 * i + 2] = half2v{x[2], x[6]};
         xp[m][gi][4 * i + 3] = half2v{x[3], x[7]};
+        sa += (float)x[0] + (float)x[4] + (float)x[2] + (float)x[6];
+        sb += (float)x[1] + (float)x[5] + (float)x[3] + (float)x[7];
       }
+      corr[m][gi] = -(1024.f + a.zero) * sa - (64.f + a.zero) * sb;
     }
   }
 
+
+  rsrc_t ry[MR];
 #pragma unroll
-  for (int rr = 0; rr < ROWS; ++rr) {
+  for (int m = 0; m < MR; ++m)
+    ry[m] = make_rsrc(a.Y + (int64_t)(m < a.M ? m : 0) * a.ldy, m < a.M ? (uint32_t)a.N * 2 : 0u);
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int n = wid + k * T;
     float y[MR];
+    row_dot(ring[k % PF], y);
+    if (k + PF < R) load_row(ring[k % PF], n + PF * T);
+    const uint32_t off = lane == 0 ? (uint32_t)n * 2u : 0xFFFFFFF0u;
 #pragma unroll
-    for (int m = 0; m < MR; ++m) y[m] = 0.f;
-#pragma unroll
-    for (int gi = 0; gi < GI; ++gi) {
-      float a1[MR], a16[MR];
-#pragma unroll
-      for (int m = 0; m < MR; ++m) a1[m] = a16[m] = 0.f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        half2v r[4];
-        unpack_word(wv[rr][gi][i], z1, z16, r);
-#pragma unroll
-        for (int m = 0; m < MR; ++m) {
-          a1[m] = __builtin_amdgcn_fdot2(r[0], xp[m][gi][4 * i + 0], a1[m], false);
-          a16[m] = __builtin_amdgcn_fdot2(r[1], xp[m][gi][4 * i + 1], a16[m], false);
-          a1[m] = __builtin_amdgcn_fdot2(r[2], xp[m][gi][4 * i + 2], a1[m], false);
-          a16[m] = __builtin_amdgcn_fdot2(r[3], xp[m][gi][4 * i + 3], a16[m], false);
-        }
-      }
-#pragma unroll
-      for (int m = 0; m < MR; ++m) y[m] += (a1[m] + a16[m] * 0.0625f) * sc[rr][gi];
-    }
-    const int n = n0 + rr;
-#pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      const float t = wave_sum(y[m]);
-      if (lane == 0 && n < a.N && m < a.M) a.Y[(int64_t)m * a.ldy + n] = (half_t)t;
-    }
+    for (int m = 0; m < MR; ++m)
+      __builtin_amdgcn_raw_buffer_store_b16(
+          __builtin_bit_cast(uint16_t, (half_t)wave_sum_dpp(y[m])), ry[m], off, 0, 0);
   }
 }
 
@@ -226,22 +312,38 @@ __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Args a) {
   }
 }
 
-template <int MR>
-hipError_t launch_gemv_mr(const W4Args& a, hipStream_t s) {
-  constexpr int ROWS = 4;
-  const int waves = (a.N + ROWS - 1) / ROWS;
+template <int MR, int R>
+hipError_t launch_gemv_r(const W4Args& a, hipStream_t s) {
+  const int waves = (a.N + R - 1) / R;
   const int blocks = (waves + 3) / 4;
   const int G = a.K / 32;
   if (G <= 64) {
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, ROWS, 1>), dim3(blocks), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 1, R>), dim3(blocks), dim3(kThreads), 0, s, a);
   } else if (G <= 128) {
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, ROWS, 2>), dim3(blocks), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 2, R>), dim3(blocks), dim3(kThreads), 0, s, a);
   } else if (G <= 256) {
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, ROWS, 4>), dim3(blocks), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 4, R>), dim3(blocks), dim3(kThreads), 0, s, a);
   } else {
     return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int MR>
+hipError_t launch_gemv_mr(const W4Args& a, hipStream_t s) {
+  // Rows per wave: the smallest of 2/4/8 that keeps the grid near two waves
+  // per SIMD (NESO_AMD_GEMV_ROWS_PER_WAVE overrides).
+  static const int forced = [] {
+    const char* v = getenv("NESO_AMD_GEMV_ROWS_PER_WAVE");
+    const int k = v ? atoi(v) : 0;
+    return (k == 2 || k == 4 || k == 8) ? k : 0;
+  }();
+  const int simds = 4 * device_cu_count();
+  int r = forced;
+  if (!r) r = a.N <= 2 * 2 * simds ? 2 : (a.N <= 4 * 2 * simds ? 4 : 8);
+  if (r == 2) return launch_gemv_r<MR, 2>(a, s);
+  if (r == 4) return launch_gemv_r<MR, 4>(a, s);
+  return launch_gemv_r<MR, 8>(a, s);
 }
 
 }  // namespace

@@ -70,10 +70,20 @@ def test_group_and_zero_point(gpu, group, zero, m):
 
 @pytest.mark.parametrize("m", [1, 16, 256])
 def test_zero_point_codes_give_zero(gpu, m):
+    """Codes equal to the zero point dequantise to 0, so Y = 0.
+
+    The MFMA regime subtracts the zero point per element (exact zeros).  The
+    GEMV regime (M <= 4) folds it into a per-chunk correction computed from
+    X, so it returns 0 up to fp32 rounding: |Y| <= 1e-3 here, against
+    typical |Y| ~ 4 for these inputs with random codes.
+    """
     x, _, scales = I.qmatmul_inputs(m, 4096, 512, seed=1)
     eights = Q.pack_int4(np.full((512, 4096), 8, np.uint8))
     y = gpu_w4(x, eights, scales)
-    assert torch.count_nonzero(y).item() == 0
+    if m <= 4:
+        assert y.float().abs().max().item() <= 1e-3
+    else:
+        assert torch.count_nonzero(y).item() == 0
 
 
 def test_strided_output(gpu):
