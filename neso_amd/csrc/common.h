@@ -59,6 +59,9 @@ __device__ __forceinline__ half8v load_half8(const half_t* p) {
 // tail handling without per-element compares or clamped addresses.
 // dword3 = 0x00020000: 32-bit data format, no swizzle (gfx9 family).
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+// Cache-policy operand of the buffer intrinsics: the "nt" (non-temporal,
+// streaming) bit of gfx94x/gfx950 memory instructions.
+constexpr int kNonTemporal = 2;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }

@@ -105,11 +105,12 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
   const uint32_t mhi = sgpr_const(0x00F000F0u);
   const uint32_t mag = vgpr_const(0x64006400u);
 
-  half2v xp[MR][GI][16];  // X pairs (filled after the first weight loads)
+  half2v xp[MR][GI][16];  // X pairs, paired like the nibbles of a word
   float corr[MR][GI];
 
   auto load_row = [&](GemvRow<GI>& r, int n) {
     // Rows past the end get an empty buffer resource: all loads return 0.
+    // Weights and scales are read once per call: non-temporal loads.
     const bool ok = n < a.N;
     const rsrc_t rw = make_rsrc(a.W + (int64_t)(ok ? n : 0) * KW, ok ? (uint32_t)KW * 4 : 0u);
     const rsrc_t rs = make_rsrc(a.S + (int64_t)(ok ? n : 0) * SG, ok ? (uint32_t)SG * 2 : 0u);
@@ -117,10 +118,10 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
     for (int gi = 0; gi < GI; ++gi) {
       const int gch = lane + 64 * gi;
       r.w[gi] = __builtin_bit_cast(uint4v, __builtin_amdgcn_raw_buffer_load_b128(
-                                               rw, (uint32_t)gch * 16u, 0, 0));
+                                               rw, (uint32_t)gch * 16u, 0, kNonTemporal));
       const uint32_t sidx = (uint32_t)(32 * gch) / (uint32_t)a.group;
       r.s[gi] = (float)__builtin_bit_cast(
-          half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, sidx * 2u, 0, 0));
+          half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, sidx * 2u, 0, kNonTemporal));
     }
   };
 
@@ -156,36 +157,50 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
     }
   };
 
+  // X is requested first, then the first PF weight rows: loads complete in
+  // issue order, so the X pairs and corrections below are computed while
+  // the weights are still in flight.  Buffer loads: rows m >= M and chunks
+  // past K read as zeros, with no branch around them.
+  rsrc_t rx[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+    rx[m] = make_rsrc(a.X + (int64_t)(m < a.M ? m : 0) * a.ldx, m < a.M ? (uint32_t)a.K * 2 : 0u);
+  half8v xr[MR][GI][4];
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int gi = 0; gi < GI; ++gi)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        xr[m][gi][i] = buf_load_half8(rx[m], (uint32_t)(32 * (lane + 64 * gi) + 8 * i) * 2u);
+
   // Wave w handles rows w + k*T, k < R, in straight-line code (a loop
   // back-edge makes the compiler drain every outstanding load).  A ring of
-  // PF rows is in flight; the first PF are requested before X is read.
-  // Rows past N read zeros and their (lane-0) stores fall outside ry.
+  // PF rows is in flight.  Rows past N read zeros and their (lane-0) stores
+  // fall outside ry.
   constexpr int PF = R < 4 ? R : 4;
   GemvRow<GI> ring[PF];
 #pragma unroll
   for (int k = 0; k < PF; ++k) load_row(ring[k], wid + k * T);
 
-  // X pairs and per-chunk corrections, once per wave.  Buffer loads: rows
-  // m >= M and chunks past K read as zeros, with no branch around them.
-  rsrc_t rx[MR];
-#pragma unroll
-  for (int m = 0; m < MR; ++m)
-    rx[m] = make_rsrc(a.X + (int64_t)(m < a.M ? m : 0) * a.ldx, m < a.M ? (uint32_t)a.K * 2 : 0u);
+  // Chunk sums for the corrections with v_dot2 against (1, 1).
+  const half2v ones = {(half_t)1, (half_t)1};
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
 #pragma unroll
     for (int gi = 0; gi < GI; ++gi) {
-      const int gch = lane + 64 * gi;
       float sa = 0.f, sb = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const half8v x = buf_load_half8(rx[m], (uint32_t)(32 * gch + 8 * i) * 2u);
+        const half8v x = xr[m][gi][i];
         xp[m][gi][4 * i + 0] = half2v{x[0], x[4]};
         xp[m][gi][4 * i + 1] = half2v{x[1], x[5]};
         xp[m][gi][4 * i + 2] = half2v{x[2], x[6]};
         xp[m][gi][4 * i + 3] = half2v{x[3], x[7]};
-        sa += (float)x[0] + (float)x[4] + (float)x[2] + (float)x[6];
-        sb += (float)x[1] + (float)x[5] + (float)x[3] + (float)x[7];
+        sa = __builtin_amdgcn_fdot2(xp[m][gi][4 * i + 0], ones, sa, false);
+        sa = __builtin_amdgcn_fdot2(xp[m][gi][4 * i + 2], ones, sa, false);
+        sb = __builtin_amdgcn_fdot2(xp[m][gi][4 * i + 1], ones, sb, false);
+        sb = __builtin_amdgcn_fdot2(xp[m][gi][4 * i + 3], ones, sb, false);
       }
       corr[m][gi] = -(1024.f + a.zero) * sa - (64.f + a.zero) * sb;
     }
@@ -331,8 +346,9 @@ hipError_t launch_gemv_r(const W4Args& a, hipStream_t s) {
 
 template <int MR>
 hipError_t launch_gemv_mr(const W4Args& a, hipStream_t s) {
-  // Rows per wave: the smallest of 2/4/8 that keeps the grid near two waves
-  // per SIMD (NESO_AMD_GEMV_ROWS_PER_WAVE overrides).
+  // Rows per wave: 4 (all four in flight from the start) unless the grid
+  // would then leave SIMDs without a wave; 8 only for very tall matrices.
+  // NESO_AMD_GEMV_ROWS_PER_WAVE overrides.
   static const int forced = [] {
     const char* v = getenv("NESO_AMD_GEMV_ROWS_PER_WAVE");
     const int k = v ? atoi(v) : 0;
@@ -340,7 +356,7 @@ hipError_t launch_gemv_mr(const W4Args& a, hipStream_t s) {
   }();
   const int simds = 4 * device_cu_count();
   int r = forced;
-  if (!r) r = a.N <= 2 * 2 * simds ? 2 : (a.N <= 4 * 2 * simds ? 4 : 8);
+  if (!r) r = a.N < 4 * simds ? 2 : (a.N <= 16 * simds ? 4 : 8);
   if (r == 2) return launch_gemv_r<MR, 2>(a, s);
   if (r == 4) return launch_gemv_r<MR, 4>(a, s);
   return launch_gemv_r<MR, 8>(a, s);
