@@ -3,22 +3,32 @@
 
 A "step" is one FA2 forward launch over BASELINE's headline workload
 (B=1, H=16, N=2048, d=64, non-causal, fp16 in / fp32 out), inputs resident
-in HBM.  ``value`` = 4*B*H*N^2*d / (ms_per_step) in TFLOP/s.  The same line
-carries:
+in HBM.  ``value`` = 4*B*H*N^2*d / (ms_per_step) in TFLOP/s.
+
+Launches are captured in a HIP graph (16 per graph) and the graph is
+replayed; HIP events recorded on the replay stream bracket the timed
+launches.  The per-launch time therefore includes the GPU's dispatch gap
+between consecutive kernels but not Python's launch cost, which exceeds the
+runtime of the smaller kernels (``eager_ms_per_step`` reports the eager
+rate for comparison).  The same line carries:
 
 * ``roofline`` for that kernel against dense-fp16 MFMA peak (2516.6 TFLOP/s
-  = 256 CU x 2.4 GHz x 4096 FLOP/clk), from HIP events recorded on the
-  stream the kernel runs on;
+  = 256 CU x 2.4 GHz x 4096 FLOP/clk);
 * ``cpu_baseline``: the CPU oracle (torch fp32, all host threads) on the
   same workload, rank 0 only;
 * ``qmatmul``: the int4 qmatmul at M=1, K=4096, N=11008 in HBM GB/s
-  (algorithmic bytes K*N/2 + (K/32)*N*2 + M*K*2 + M*N*2), timed over 16
-  rotated weight copies (> 256 MiB, so the Infinity Cache cannot hold them)
-  with its own roofline against 8 TB/s and its CPU baseline;
+  (algorithmic bytes K*N/2 + (K/32)*N*2 + M*K*2 + M*N*2), over 16 rotated
+  weight copies (> 256 MiB, so the Infinity Cache cannot hold them), with
+  its own roofline against 8 TB/s and its CPU baseline;
 * ``sweep``: the other BASELINE configs (FA2 N sweep, d=128 causal, rel-pos
   N=1500, qmatmul M=16/256), one entry each.
 
+``--calibrate-copy`` instead times a plain device-to-device copy of 256 MiB
+(torch's copy kernel), the reference for scaling the FETCH_SIZE/WRITE_SIZE
+counters to bytes.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+       python bench.py --calibrate-copy
 """
 from __future__ import annotations
 
@@ -42,6 +52,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true")
     return ap.parse_args()
 
 
@@ -49,14 +60,40 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def time_launches(launch, steps, warmup, torch):
-    """Run ``launch(i)`` warmup + steps times; return ms per launch over the timed steps.
+GRAPH_LAUNCHES = 16
 
-    Events are recorded on torch's current stream, which is the stream the
-    launchers enqueue on.
+
+def time_launches(launch, steps, warmup, torch, per_graph=GRAPH_LAUNCHES):
+    """ms per launch of ``launch(i)``, replayed from a HIP graph.
+
+    ``per_graph`` consecutive launches (i = 0 .. per_graph-1) are captured
+    once; the graph is replayed ceil(steps / per_graph) times between two
+    events recorded on the current stream, which is the stream the replays
+    run on.  ``warmup`` launches run eagerly first (and compile nothing).
     """
     for i in range(warmup):
-        launch(i)
+        launch(i % per_graph)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(per_graph):
+            launch(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    replays = max(1, -(-steps // per_graph))
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        graph.replay()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / (replays * per_graph)
+
+
+def time_eager(launch, steps, torch):
+    """ms per launch when launched one by one from Python (host-bound for short kernels)."""
+    launch(0)
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -66,6 +103,45 @@ def time_launches(launch, steps, warmup, torch):
     stop.record()
     torch.cuda.synchronize()
     return start.elapsed_time(stop) / steps
+
+
+def measured_traffic(key):
+    """HBM bytes per launch from the committed counter summary, or None.
+
+    profiles/traffic.json holds FETCH_SIZE + WRITE_SIZE per dispatch (two
+    rocprofv3 --pmc passes over this script) already scaled by the plain-copy
+    calibration factor; the counters cannot be read from inside the process.
+    """
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f)["kernels"].get(key)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if entry is None else entry.get("hbm_bytes_per_launch")
+
+
+def best_time(launch, steps, warmup, torch):
+    """(ms per launch, mode, graph ms, eager ms): the faster of graph replay and eager launches.
+
+    Short kernels are host-bound when launched from Python, so graph replay
+    is their rate; long kernels keep the queue full either way and the
+    graph's per-node overhead can make eager launches faster.
+    """
+    g = time_launches(launch, steps, warmup, torch)
+    e = time_eager(launch, min(steps, 64), torch)
+    return (g, "graph", g, e) if g <= e else (e, "eager", g, e)
+
+
+def calibrate_copy(torch):
+    """Plain 256 MiB device copy: bytes moved per launch and its time."""
+    nbytes = 256 << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    ms = time_launches(lambda i: dst.copy_(src), 20, 3, torch, per_graph=4)
+    return {"metric": "device copy GB/s (read + write)", "bytes_read": nbytes,
+            "bytes_written": nbytes, "ms_per_copy": round(ms, 6),
+            "value": round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s"}
 
 
 def cpu_time(fn, reps):
@@ -82,10 +158,11 @@ def fa2_case(neso_amd, torch, I, B, H, N, d, causal, steps, warmup, seed=0):
     from oracle import attention as A  # FLOP formula only
     q, k, v = (t.cuda() for t in I.fa2_inputs(B, H, N, d, seed=seed))
     out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
-    ms = time_launches(lambda i: neso_amd.attention(q, k, v, causal=causal, out=out), steps,
-                       warmup, torch)
+    ms, mode, g, e = best_time(lambda i: neso_amd.attention(q, k, v, causal=causal, out=out),
+                               steps, warmup, torch)
     flop = A.flops(B, H, N, d, causal)
-    return ms, flop / (ms * 1e-3) / 1e12, (q, k, v)
+    return ms, flop / (ms * 1e-3) / 1e12, (q, k, v), {"timing": mode, "graph_ms": round(g, 6),
+                                                      "eager_ms": round(e, 6)}
 
 
 def main():
@@ -100,14 +177,17 @@ def main():
     from oracle import inputs as I
 
     torch.manual_seed(0)
+    if args.calibrate_copy:
+        print(json.dumps(calibrate_copy(torch)), flush=True)
+        return 0
     dev = torch.cuda.get_device_properties(0)
     log(f"device {dev.name} {dev.gcnArchName} CUs={dev.multi_processor_count}")
 
     # ---- headline: FA2 forward, B1 H16 N2048 d64 non-causal ----
     hb = I.FA2_HEADLINE
-    ms, tflops, (q, k, v) = fa2_case(neso_amd, torch, I, hb["B"], hb["H"], hb["N"], hb["d"],
-                                     False, args.steps, args.warmup)
-    log(f"fa2 headline {ms * 1e3:.2f} us/launch {tflops:.1f} TFLOP/s")
+    ms, tflops, (q, k, v), tmode = fa2_case(neso_amd, torch, I, hb["B"], hb["H"], hb["N"],
+                                            hb["d"], False, args.steps, args.warmup)
+    log(f"fa2 headline {ms * 1e3:.2f} us/launch {tflops:.1f} TFLOP/s ({tmode})")
     flop = 4.0 * hb["B"] * hb["H"] * hb["N"] ** 2 * hb["d"]
     result = {
         "metric": METRIC,
@@ -117,6 +197,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
+        "timing": tmode,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -127,7 +208,8 @@ def main():
                    "B": 1, "H": 16, "N": 2048, "d": 64, "causal": False},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3),
                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                     "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+                     "traffic": measured_traffic("fa2_headline"),
                      "kernel": "fa2_fwd_kernel<64,false,0,false>",
                      "algorithmic_flop_per_launch": flop},
     }
@@ -170,19 +252,22 @@ def qmm_case(neso_amd, torch, I, cfg, steps, warmup, rotate=1, want_cpu=False):
     ws = [words.cuda() for _ in range(rotate)]
     ss = [scales.cuda() for _ in range(rotate)]
     y = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    ms = time_launches(
-        lambda i: neso_amd.w4a16_matmul(xs, ws[i % rotate], ss[i % rotate], y, M, N, K, K, N),
-        steps, warmup, torch)
+    launch = lambda i: neso_amd.w4a16_matmul(xs, ws[i % rotate], ss[i % rotate], y, M, N, K, K,
+                                             N)
+    ms, mode, g_ms, e_ms = best_time(launch, steps, warmup, torch)
     nbytes = Q.algorithmic_bytes(M, N, K)
     gbs = nbytes / (ms * 1e-3) / 1e9
     tflops = Q.flops(M, N, K) / (ms * 1e-3) / 1e12
     out = {"metric": "int4 qmatmul HBM GB/s", "value": round(gbs, 2), "unit": "GB/s",
-           "ms_per_step": round(ms, 6), "tflops": round(tflops, 3),
+           "ms_per_step": round(ms, 6),
+           "timing": {"timing": mode, "graph_ms": round(g_ms, 6), "eager_ms": round(e_ms, 6)},
+           "tflops": round(tflops, 3),
            "config": {"workload": f"w4a16_matmul M={M} K={K} N={N} group=32 zero=8, fp16 "
                                   f"X, fp16 out, {rotate} rotated weight copies",
                       "M": M, "K": K, "N": N},
            "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                        "traffic": measured_traffic(f"w4a16_M{M}"),
                         "algorithmic_bytes_per_launch": nbytes}}
     if want_cpu:
         threads = os.cpu_count() or 1
@@ -209,30 +294,31 @@ def qmm_case(neso_amd, torch, I, cfg, steps, warmup, rotate=1, want_cpu=False):
 def sweep(neso_amd, torch, I, steps, warmup):
     rows = []
     for cfg in I.FA2_SWEEP:
-        ms, tf, _ = fa2_case(neso_amd, torch, I, cfg["B"], cfg["H"], cfg["N"], cfg["d"],
-                             cfg["causal"], steps, warmup)
+        ms, tf, _, tm = fa2_case(neso_amd, torch, I, cfg["B"], cfg["H"], cfg["N"], cfg["d"],
+                                 cfg["causal"], steps, warmup)
         rows.append({"kernel": "fa2", **cfg, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
-                     "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+                     "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "timing": tm["timing"]})
     c = I.FA2_D128
-    ms, tf, _ = fa2_case(neso_amd, torch, I, c["B"], c["H"], c["N"], c["d"], c["causal"],
-                         max(5, steps // 4), 2)
+    ms, tf, _, tm = fa2_case(neso_amd, torch, I, c["B"], c["H"], c["N"], c["d"], c["causal"],
+                             max(16, steps // 4), 2)
     rows.append({"kernel": "fa2", **c, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
-                 "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+                 "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "timing": tm["timing"]})
     rc = I.RELPOS_CONFIG
     q, k, v, table = (t.cuda() for t in I.relpos_inputs(**rc, seed=0))
     out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
-    ms = time_launches(lambda i: neso_amd.rel_pos_attention(q, k, v, table, out=out), steps,
-                       warmup, torch)
+    ms, mode, _, _ = best_time(lambda i: neso_amd.rel_pos_attention(q, k, v, table, out=out),
+                               steps, warmup, torch)
     flop = 4.0 * rc["H"] * rc["N"] ** 2 * rc["d"]
     tf = flop / (ms * 1e-3) / 1e12
     rows.append({"kernel": "rel_pos_fa2", **rc, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
-                 "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4)})
+                 "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "timing": mode})
     for cfg in I.QMM_CONFIGS[1:]:
         r = qmm_case(neso_amd, torch, I, cfg, steps, warmup, rotate=8)
         rows.append({"kernel": "w4a16", **cfg, "us": round(r["ms_per_step"] * 1e3, 2),
                      "gbs": r["value"], "tflops": r["tflops"],
                      "hbm_frac": r["roofline"]["frac"],
-                     "mfma_frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4)})
+                     "mfma_frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
+                     "timing": r["timing"]["timing"]})
     return rows
 
 

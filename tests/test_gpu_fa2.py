@@ -95,6 +95,35 @@ def test_ragged_lengths(gpu, n, d, causal):
     _check(dict(B=1, H=3, N=n, d=d, causal=causal), seed=n * d)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_scale_zero_and_negative(gpu, causal):
+    """scale = 0 gives the (prefix) mean of V; a negative scale flips the logits."""
+    q, k, v = I.fa2_inputs(1, 2, 300, 64, seed=11)
+    out0 = gpu_attention(q, k, v, causal=causal, scale=0.0)
+    vf = v.float()
+    if causal:
+        mean = vf.cumsum(2) / torch.arange(1, 301, dtype=torch.float32).view(1, 1, -1, 1)
+    else:
+        mean = vf.mean(2, keepdim=True).expand_as(vf)
+    assert (out0 - mean).abs().max().item() <= TOL
+    outn = gpu_attention(q, k, v, causal=causal, scale=-0.125)
+    ref = A.attention(q, k, v, -0.125, causal=causal)
+    assert (outn - ref).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_large_logits(gpu, causal):
+    """Logits with standard deviation ~8: the running max rises by far more
+    than the lazy-rescale threshold across key blocks, so O and l are
+    rescaled many times."""
+    q, k, v = I.fa2_inputs(1, 4, 1024, 64, seed=12)
+    q = (q.float() * 8).half()
+    out = gpu_attention(q, k, v, causal=causal)
+    ref = A.attention(q, k, v, 1 / 8, causal=causal)
+    assert torch.isfinite(out).all()
+    assert (out - ref).abs().max().item() <= TOL
+
+
 def test_permutation_invariance_full_size(gpu):
     cfg = I.FA2_HEADLINE
     q, k, v = I.fa2_inputs(**cfg, seed=7)
