@@ -28,15 +28,39 @@ constexpr int kThreads = 256;
 
 __device__ __forceinline__ half2v as_half2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
 
+// 32-bit constants the compiler cannot fold back into literals: gfx9 VOP3
+// encodings take no literal and read at most one SGPR, so v_and_or_b32
+// needs its two constants as one SGPR and one VGPR.
+__device__ __forceinline__ uint32_t sgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
+  return r;
+}
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+  return r;
+}
+
+// Nibble masks and the f16 exponent pattern, held in registers so that
+// (w & mask) | magic is one v_and_or_b32.
+struct Nibbles {
+  uint32_t lo, hi, mag;
+};
+__device__ __forceinline__ Nibbles nibble_consts() {
+  return Nibbles{sgpr_const(0x000F000Fu), sgpr_const(0x00F000F0u), vgpr_const(0x64006400u)};
+}
+
 // Four f16 pairs of one packed word, shifted by the zero point:
 //   r[0] = (c0 - z, c4 - z)        r[1] = 16 * (c1 - z, c5 - z)
 //   r[2] = (c2 - z, c6 - z)        r[3] = 16 * (c3 - z, c7 - z)
-__device__ __forceinline__ void unpack_word(uint32_t w, half2v z1, half2v z16, half2v r[4]) {
+__device__ __forceinline__ void unpack_word(uint32_t w, const Nibbles& k, half2v z1, half2v z16,
+                                            half2v r[4]) {
   const uint32_t w8 = w >> 8;
-  r[0] = as_half2((w & 0x000F000Fu) | 0x64006400u) - z1;
-  r[1] = as_half2((w & 0x00F000F0u) | 0x64006400u) - z16;
-  r[2] = as_half2((w8 & 0x000F000Fu) | 0x64006400u) - z1;
-  r[3] = as_half2((w8 & 0x00F000F0u) | 0x64006400u) - z16;
+  r[0] = as_half2((w & k.lo) | k.mag) - z1;
+  r[1] = as_half2((w & k.hi) | k.mag) - z16;
+  r[2] = as_half2((w8 & k.lo) | k.mag) - z1;
+  r[3] = as_half2((w8 & k.hi) | k.mag) - z16;
 }
 
 // ---------------------------------------------------------------------------
@@ -56,20 +80,6 @@ __device__ __forceinline__ void unpack_word(uint32_t w, half2v z1, half2v z16, h
 // (S_A, S_B = sums of the X elements paired with the two nibble sets)
 // restores sum((c - z) x) = acc1 + acc16 / 16 + corr exactly in real
 // arithmetic.  Per 8 codes: 1 shift, 4 v_and_or_b32, 4 v_dot2.
-
-// 32-bit constants the compiler cannot fold back into literals: gfx9 VOP3
-// encodings take no literal and read at most one SGPR, so v_and_or_b32
-// needs its two constants as one SGPR and one VGPR.
-__device__ __forceinline__ uint32_t sgpr_const(uint32_t v) {
-  uint32_t r;
-  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
-  return r;
-}
-__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
-  uint32_t r;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
-  return r;
-}
 
 // Sum over the 64 lanes with DPP row operations; the total lands in lane 63
 // and is returned to every lane.
@@ -226,6 +236,313 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
 }
 
 // ---------------------------------------------------------------------------
+// Skinny-M regime (5 <= M <= 64): split-K MFMA.
+//
+// A workgroup owns 16*NT rows of W (output columns n) and 16*MT rows of X.
+// Its WV waves split K into contiguous ranges of chunk quads (a quad = 4
+// chunks = 128 codes) and reduce their partial tiles through LDS, so the
+// grid has N / (16*NT) workgroups per 16*MT rows of X and no wave walks all
+// of K.
+//
+// v_mfma_f32_16x16x32_f16, one MFMA per chunk (one scale group when
+// group = 32).  Lane (n = l%16, g = l/16) loads the 16-byte word quad of
+// chunk 4q + g of row n (coalesced), then a 4x4 transpose across the four
+// 16-lane rows (v_permlane32_swap, v_permlane16_swap) leaves register t
+// holding word g of chunk 4q + t.  MFMA t takes that word as its B column
+// slice, so lane (m, g) supplies X[m][32(4q+t) + 8g + {0,4,1,5,2,6,3,7}]:
+// four lanes read 64 contiguous bytes of each X row per load.  Words are
+// dequantised and scaled in fp16 before the MFMA: (c - z) * s, one rounding.
+// Out-of-range rows and chunks are zero-filled by the buffer bounds check
+// (chunks past the wave's range get an out-of-range offset).
+// Word j of register w_j in 16-lane row g (chunk g, word j) becomes word g
+// of chunk j: a 4x4 transpose between the registers and the four rows.
+// v_permlane32_swap exchanges the upper 32 lanes of its first operand with
+// the lower 32 lanes of its second; v_permlane16_swap exchanges the odd rows
+// of its first operand with the even rows of its second.
+__device__ __forceinline__ void transpose_rows4(uint32_t& w0, uint32_t& w1, uint32_t& w2,
+                                                uint32_t& w3) {
+  const auto a = __builtin_amdgcn_permlane32_swap(w0, w2, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(w1, w3, false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  w0 = c[0];
+  w1 = c[1];
+  w2 = d[0];
+  w3 = d[1];
+}
+
+template <int MT, int NT, int WV, bool G32>
+__global__ __launch_bounds__(WV * kWave) void w4a16_skinny_kernel(W4Args a) {
+  constexpr int QB = 2;                   // quads per batch
+  constexpr uint32_t kOut = 0x80000000u;  // offset past every buffer
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int n0 = blockIdx.x * (16 * NT);
+  const int m0 = blockIdx.y * (16 * MT);
+  const int KW = a.K >> 3, SG = a.K / a.group, C = a.K >> 5;
+  const int Q = (C + 3) >> 2;
+  const int QW = (Q + WV - 1) / WV;
+  const int q0 = wave * QW;
+  const int q1 = min(q0 + QW, Q);
+  const int cend = min(4 * q1, C);
+  const int nrows = min(16 * NT, a.N - n0);
+  const int mrows = min(16 * MT, a.M - m0);
+  const rsrc_t rw = make_rsrc(a.W + (int64_t)n0 * KW, (uint32_t)nrows * (uint32_t)KW * 4u);
+  const rsrc_t rs = make_rsrc(a.S + (int64_t)n0 * SG, (uint32_t)nrows * (uint32_t)SG * 2u);
+  const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx,
+                              (uint32_t)((mrows - 1) * a.ldx + a.K) * 2u);
+  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
+  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const Nibbles nib = nibble_consts();
+  const uint32_t gm = (uint32_t)a.group >> 5;  // chunks per scale group
+  const bool gpow2 = (gm & (gm - 1)) == 0;
+  const uint32_t gshift = __builtin_ctz(gm);
+
+  struct Batch {
+    half8v x[QB][MT][4];  // [quad][m tile][chunk t]
+    uint4v w[QB][NT];     // [quad][n tile]: word quad of chunk 4q + l/16
+    half4v s[QB][NT];     // scales of chunks 4q .. 4q+3 of row n
+  };
+  // Offsets are computed unconditionally and OR-ed with kOut when the chunk
+  // is outside the wave's range (in-range offsets are below 2^31), so every
+  // load is issued without a branch.
+  auto load = [&](Batch& b, int q) {
+#pragma unroll
+    for (int qi = 0; qi < QB; ++qi) {
+      const uint32_t cq = 4 * (q + qi);  // first chunk of the quad
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const uint32_t row = 16 * nt + li;
+        // Word quad of chunk cq + lg; the transpose happens at compute time.
+        const uint32_t c = cq + lg;
+        const uint32_t wo = (row * (uint32_t)KW * 4u + c * 16u) | ((int)c < cend ? 0u : kOut);
+        b.w[qi][nt] = __builtin_bit_cast(
+            uint4v, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, kNonTemporal));
+        if constexpr (G32) {
+          // Scales of chunks cq .. cq+3 are contiguous and 8-byte aligned
+          // (the launcher picks this path only for group 32 and K % 128 == 0).
+          const uint32_t so = ((row * (uint32_t)SG + cq) * 2u) | ((int)cq < cend ? 0u : kOut);
+          b.s[qi][nt] = __builtin_bit_cast(
+              half4v, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, kNonTemporal));
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const uint32_t ct = cq + t;
+            const uint32_t sidx = gpow2 ? ct >> gshift : ct / gm;
+            const uint32_t so = ((row * (uint32_t)SG + sidx) * 2u) | ((int)ct < cend ? 0u : kOut);
+            b.s[qi][nt][t] = __builtin_bit_cast(
+                half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, so, 0, kNonTemporal));
+          }
+        }
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const uint32_t ct = cq + t;
+          const uint32_t xo = (((16 * mt + li) * (uint32_t)a.ldx + 32u * ct + 8u * lg) * 2u) |
+                              ((int)ct < cend ? 0u : kOut);
+          b.x[qi][mt][t] = buf_load_half8(rx, xo);
+        }
+      }
+    }
+  };
+
+  float4v acc[MT][NT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mt][nt] = float4v{};
+
+  auto compute = [&](Batch& b) {
+#pragma unroll
+    for (int qi = 0; qi < QB; ++qi) {
+      half8v xa[MT][4];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const half8v x = b.x[qi][mt][t];
+          xa[mt][t] = half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+        }
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        // Word j of chunk cq + l/16  ->  word l/16 of chunk cq + t.
+        uint32_t wt[4] = {b.w[qi][nt][0], b.w[qi][nt][1], b.w[qi][nt][2], b.w[qi][nt][3]};
+        transpose_rows4(wt[0], wt[1], wt[2], wt[3]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const half_t s = b.s[qi][nt][t];
+          const half2v s1 = {s, s};
+          const half_t s16v = s * (half_t)0.0625f;
+          const half2v s16 = {s16v, s16v};
+          half2v r[4];
+          unpack_word(wt[t], nib, z1, z16, r);
+          const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
+          const half8v bv = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16x16x32(xa[mt][t], bv, acc[mt][nt]);
+        }
+      }
+    }
+  };
+
+  // Two batches in flight; loads past the wave's range read zeros.
+  Batch bA, bB;
+  load(bA, q0);
+  for (int q = q0; q < q1; q += 2 * QB) {
+    load(bB, q + QB);
+    compute(bA);
+    load(bA, q + 2 * QB);
+    compute(bB);
+  }
+
+  // Reduce the waves' partial tiles.  acc[mt][nt] register r of lane l is
+  // D[16mt + 4(l/16) + r][16nt + l%16].
+  __shared__ float red[WV][MT * NT * 4][kWave];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[wave][(mt * NT + nt) * 4 + r][lane] = acc[mt][nt][r];
+  lds_barrier();
+  for (int e = threadIdx.x; e < MT * NT * 4 * kWave; e += WV * kWave) {
+    const int slot = e / kWave, ln = e % kWave;
+    float v = 0.f;
+#pragma unroll
+    for (int w = 0; w < WV; ++w) v += red[w][slot][ln];
+    const int mt = slot / (NT * 4), nt = (slot / 4) % NT, r = slot % 4;
+    const int m = m0 + 16 * mt + 4 * (ln >> 4) + r;
+    const int n = n0 + 16 * nt + (ln & 15);
+    if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (half_t)v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Skinny-M regime with X resident in LDS (M <= 16, K <= 4096, group 32).
+//
+// The workload is one burst of N*K/2 bytes: every weight load should be in
+// flight from the start.  One persistent workgroup per CU owns row tiles
+// blockIdx.x + i * gridDim.x (16 rows each, i < T).  Its WV waves split K
+// (wave w takes chunk quads [w*QW, (w+1)*QW)) and issue all their weight
+// and scale loads for all T tiles before anything else waits (plain loads:
+// the non-temporal hint measured slower for these 64-byte row pieces).  X is copied
+// once per workgroup into LDS, already in MFMA A-fragment order (slot
+// (4q + t) * 64 + lane holds X[m][32(4q+t) + 8g + {0,4,1,5,2,6,3,7}] for
+// lane = m + 16g), so the per-tile A operand is one conflict-free
+// ds_read_b128 per MFMA.  MFMA, transpose and dequantisation are those of
+// w4a16_skinny_kernel.  The WV partial tiles are reduced through LDS.
+constexpr int kLdsQuads = 32;  // K <= 4096
+
+template <int WV, int T, int QWMAX>
+__global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) {
+  constexpr uint32_t kOut = 0x80000000u;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int li = lane & 15, lg = lane >> 4;
+  const int KW = a.K >> 3, SG = a.K >> 5, C = a.K >> 5;
+  const int Q = (C + 3) >> 2;
+  const int QW = (Q + WV - 1) / WV;
+  const int q0 = wave * QW;
+  const int cend = min(4 * min(q0 + QW, Q), C);
+  const int ntiles = (a.N + 15) >> 4;
+  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
+  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const Nibbles nib = nibble_consts();
+
+  __shared__ half8v xs[kLdsQuads * 4 * kWave];
+  __shared__ float red[T][WV][4][kWave];
+
+  // All weight and scale loads of this wave, all tiles.
+  uint4v w[T][QWMAX];
+  half4v sc[T][QWMAX];
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    const int tile = blockIdx.x + i * gridDim.x;
+    const int n0 = tile * 16;
+    const int nrows = tile < ntiles ? min(16, a.N - n0) : 0;
+    const rsrc_t rw = make_rsrc(a.W + (int64_t)(nrows ? n0 : 0) * KW, (uint32_t)nrows * KW * 4u);
+    const rsrc_t rs = make_rsrc(a.S + (int64_t)(nrows ? n0 : 0) * SG, (uint32_t)nrows * SG * 2u);
+#pragma unroll
+    for (int qi = 0; qi < QWMAX; ++qi) {
+      const uint32_t cq = 4 * (q0 + qi);
+      const uint32_t c = cq + lg;
+      const bool live = qi < QW;
+      const uint32_t wo = (li * (uint32_t)KW * 4u + c * 16u) | (live && (int)c < cend ? 0u : kOut);
+      w[i][qi] = __builtin_bit_cast(
+          uint4v, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 0));
+      const uint32_t so = ((li * (uint32_t)SG + cq) * 2u) | (live && (int)cq < cend ? 0u : kOut);
+      sc[i][qi] = __builtin_bit_cast(
+          half4v, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+    }
+  }
+
+  // X (L2-resident) after the weights, so the HBM requests leave first:
+  // piece p of the workgroup's share covers LDS slot p = (4q+t)*64 + m + 16g.
+  constexpr int kXPer = (kLdsQuads * 4 * kWave) / (WV * kWave);
+  const rsrc_t rx = make_rsrc(a.X, (uint32_t)((a.M - 1) * a.ldx + a.K) * 2u);
+  half8v xv[kXPer];
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const uint32_t slot = threadIdx.x + i * WV * kWave;
+    const uint32_t ct = slot >> 6, ln = slot & 63, m = ln & 15, g = ln >> 4;
+    const uint32_t oob = ((int)ct < C && (int)m < a.M) ? 0u : kOut;
+    xv[i] = buf_load_half8(rx, ((m * (uint32_t)a.ldx + 32u * ct + 8u * g) * 2u) | oob);
+  }
+
+  // X into LDS in A-fragment order.
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const half8v x = xv[i];
+    xs[threadIdx.x + i * WV * kWave] = half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+  }
+  lds_barrier();
+
+  float4v acc[T];
+#pragma unroll
+  for (int i = 0; i < T; ++i) {
+    acc[i] = float4v{};
+#pragma unroll
+    for (int qi = 0; qi < QWMAX; ++qi) {
+      if (qi >= QW) break;  // uniform
+      const int q = q0 + qi;
+      uint32_t wt[4] = {w[i][qi][0], w[i][qi][1], w[i][qi][2], w[i][qi][3]};
+      transpose_rows4(wt[0], wt[1], wt[2], wt[3]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const half8v xa = xs[(4 * q + t) * kWave + lane];
+        const half_t s = sc[i][qi][t];
+        const half2v s1 = {s, s};
+        const half_t s16v = s * (half_t)0.0625f;
+        const half2v s16 = {s16v, s16v};
+        half2v r[4];
+        unpack_word(wt[t], nib, z1, z16, r);
+        const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
+        const half8v bv = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+        acc[i] = mfma16x16x32(xa, bv, acc[i]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[i][wave][r][lane] = acc[i][r];
+  }
+  lds_barrier();
+
+  // acc[i] register r of lane l is D[4(l/16) + r][l%16] of tile i.
+  for (int e = threadIdx.x; e < T * 4 * kWave; e += WV * kWave) {
+    const int i = e / (4 * kWave), r = (e / kWave) & 3, ln = e & 63;
+    const int tile = blockIdx.x + i * gridDim.x;
+    float v = 0.f;
+#pragma unroll
+    for (int wv = 0; wv < WV; ++wv) v += red[i][wv][r][ln];
+    const int m = 4 * (ln >> 4) + r;
+    const int n = tile * 16 + (ln & 15);
+    if (tile < ntiles && m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (half_t)v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // MFMA regime.  Each wave computes a 32 (m) x 32*TN (n) strip; 4 waves side
 // by side along N.  Per 64-column step of K, lane group g owns columns
 // [kb + 32g, kb + 32g + 32): one 16-byte word quad and one scale per row.
@@ -245,6 +562,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_mfma_kernel(W4Args a) {
   const int SG = a.K / a.group;
   const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
   const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const Nibbles nib = nibble_consts();
 
   float16v acc[TN];
 #pragma unroll
@@ -274,7 +592,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_mfma_kernel(W4Args a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         half2v r[4];
-        unpack_word(w[j], z1, z16, r);
+        unpack_word(w[j], nib, z1, z16, r);
         const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
         const half8v b = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
         acc[t] = mfma32x32x16(xa[j], b, acc[t]);
@@ -366,6 +684,11 @@ hipError_t launch_gemv_mr(const W4Args& a, hipStream_t s) {
 
 int w4a16_gemv_max_k() { return 32 * 256; }
 
+#ifndef NESO_SKINNY_WAVES
+#define NESO_SKINNY_WAVES 4
+#endif
+constexpr int kSkinnyWaves = NESO_SKINNY_WAVES;
+
 hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
   if (a.M <= 4 && a.K <= w4a16_gemv_max_k()) {
     switch (a.M) {
@@ -374,6 +697,49 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
       case 3: return launch_gemv_mr<3>(a, s);
       default: return launch_gemv_mr<4>(a, s);
     }
+  }
+  // Skinny regime: buffer offsets of one workgroup's X rows and W rows must
+  // stay below 2^31 bytes (the out-of-range marker).
+  const bool skinny_fits = (int64_t)32 * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
+                           (int64_t)32 * a.K / 2 < ((int64_t)1 << 31);
+  if (a.M <= 16 && a.group == 32 && a.K % 128 == 0 && a.K <= 32 * 4 * kLdsQuads) {
+    // X in LDS, one persistent workgroup per CU, 8 waves splitting K.
+    const int ntiles = (a.N + 15) / 16;
+    const int cus = device_cu_count();
+    int T = (ntiles + cus - 1) / cus;
+    if (T > 4) T = 4;
+    const dim3 grid((ntiles + T - 1) / T);
+    constexpr int WV = 8, QWMAX = (kLdsQuads + WV - 1) / WV;
+    switch (T) {
+      case 1: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 1, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
+      case 2: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 2, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
+      case 3: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 3, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
+      default: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 4, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
+    }
+    return hipGetLastError();
+  }
+  if (a.M <= 64 && skinny_fits) {
+    // One 8-byte load fetches the scales of a chunk quad when every chunk
+    // has its own scale and rows hold whole quads (8-byte aligned).
+    const bool g32 = a.group == 32 && a.K % 128 == 0;
+    if (a.M <= 16) {
+      const dim3 grid((a.N + 31) / 32, 1);
+      if (g32)
+        hipLaunchKernelGGL((w4a16_skinny_kernel<1, 2, kSkinnyWaves, true>), grid,
+                           dim3(kSkinnyWaves * kWave), 0, s, a);
+      else
+        hipLaunchKernelGGL((w4a16_skinny_kernel<1, 2, kSkinnyWaves, false>), grid,
+                           dim3(kSkinnyWaves * kWave), 0, s, a);
+    } else {
+      const dim3 grid((a.N + 31) / 32, (a.M + 31) / 32);
+      if (g32)
+        hipLaunchKernelGGL((w4a16_skinny_kernel<2, 2, kSkinnyWaves, true>), grid,
+                           dim3(kSkinnyWaves * kWave), 0, s, a);
+      else
+        hipLaunchKernelGGL((w4a16_skinny_kernel<2, 2, kSkinnyWaves, false>), grid,
+                           dim3(kSkinnyWaves * kWave), 0, s, a);
+    }
+    return hipGetLastError();
   }
   constexpr int TN = 2;
   const dim3 grid((a.N + 4 * 32 * TN - 1) / (4 * 32 * TN), (a.M + 31) / 32);
