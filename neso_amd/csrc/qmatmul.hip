@@ -543,6 +543,167 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
 }
 
 // ---------------------------------------------------------------------------
+// Large-M regime (M > 64): LDS-tiled GEMM.
+//
+// A workgroup computes a 128 (m) x 128 (n) tile of Y with WM x WN waves
+// (2 x 4 by default: 64 x 32 each, two v_mfma_f32_32x32x16_f16 tiles, two
+// waves per SIMD so that one wave's dequantisation and LDS reads overlap the
+// other's MFMAs).
+// Per K-step of 64 codes:
+//   * the X tile (128 x 64 fp16) goes through registers into LDS with
+//     coalesced 16-byte loads, each 8-element group stored in the order
+//     {0,4,1,5,2,6,3,7} of unpack_word; rows padded to 72 halves so the
+//     ds_read_b128 fragment reads are conflict-free;
+//   * W never touches LDS: lane (n = l%32, h = l/32) of a wave loads the
+//     16-byte word quad h (chunk k0/32 + h) of each of its 32-row column
+//     tiles and dequantises word ks of it as the B operand of MFMA
+//     k-substep ks, so that MFMA's k-block h holds codes
+//     k0 + 32h + 8ks + {0,4,1,5,2,6,3,7}.  Each W word is dequantised by
+//     the WM waves that share its columns; LDS traffic per step is the X
+//     tile once in and one A-fragment read per wave and MFMA row tile.
+// W loads run kRingW steps ahead (HBM latency), X loads two steps ahead
+// (L2), LDS is double-buffered with one barrier per step.
+constexpr int kGBM = 128, kGBK = 64, kGLD = kGBK + 8;
+constexpr int kRingW = 8;
+
+template <int WM, int WN, int kGBN>
+__global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
+  constexpr int kT = WM * WN * kWave;       // threads
+  constexpr int MI = kGBM / WM / 32;        // 32-row MFMA tiles per wave
+  constexpr int NT = kGBN / WN / 32;        // 32-column MFMA tiles per wave
+  constexpr int XJ = kGBM * kGBK / 8 / kT;  // 16-byte X pieces per thread per step
+  constexpr uint32_t kOut = 0x80000000u;
+  __shared__ half8v xs[2][kGBM * kGLD / 8];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;
+  const int li = lane & 31, lh = lane >> 5;
+  const int mtiles = (a.M + kGBM - 1) / kGBM;
+  const int ntiles = (a.N + kGBN - 1) / kGBN;
+  const int id = (int)xcd_swizzle(blockIdx.x, (uint32_t)(mtiles * ntiles));
+  const int m0 = (id % mtiles) * kGBM, n0 = (id / mtiles) * kGBN;
+  const int KW = a.K >> 3, SG = a.K / a.group;
+  const int mrows = min(kGBM, a.M - m0);
+  // This wave's first W row and row count, forced into SGPRs: computed on
+  // the VALU, the compiler would otherwise treat the buffer descriptors
+  // built from them as divergent and wrap every load in a waterfall loop.
+  const int nw0 = __builtin_amdgcn_readfirstlane(n0 + 32 * NT * wn);
+  const int nwrows = __builtin_amdgcn_readfirstlane(max(0, min(32 * NT, a.N - nw0)));
+  const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)((mrows - 1) * a.ldx + a.K) * 2u);
+  const rsrc_t rw = make_rsrc(a.W + (int64_t)(nwrows ? nw0 : 0) * KW, (uint32_t)nwrows * KW * 4u);
+  const rsrc_t rs = make_rsrc(a.S + (int64_t)(nwrows ? nw0 : 0) * SG, (uint32_t)nwrows * SG * 2u);
+  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
+  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const Nibbles nib = nibble_consts();
+  const uint32_t gm = (uint32_t)a.group >> 5;
+  const bool gpow2 = (gm & (gm - 1)) == 0;
+  const uint32_t gshift = __builtin_ctz(gm);
+
+  // X: rows tid/8 + (kT/8)j, 16-byte piece tid%8 of the step.
+  const int xr0 = tid >> 3, xp = tid & 7;
+  struct XStage {
+    half8v v[XJ];
+  };
+  struct WStage {
+    uint4v w[NT];
+    half_t s[NT];
+  };
+  auto load_x = [&](XStage& g, int k0) {
+    const uint32_t oob = k0 + 8 * xp < a.K ? 0u : kOut;
+#pragma unroll
+    for (int j = 0; j < XJ; ++j)
+      g.v[j] = buf_load_half8(rx, (((uint32_t)(xr0 + kT / 8 * j) * a.ldx + k0 + 8 * xp) * 2u) | oob);
+  };
+  auto load_w = [&](WStage& g, int k0) {
+    const uint32_t chunk = (uint32_t)(k0 >> 5) + lh;
+    const uint32_t oob = (int)(32 * chunk) < a.K ? 0u : kOut;
+    const uint32_t sidx = gpow2 ? chunk >> gshift : chunk / gm;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const uint32_t row = 32 * nt + li;
+      g.w[nt] = __builtin_bit_cast(uint4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                               rw, (row * KW * 4u + chunk * 16u) | oob, 0, 0));
+      g.s[nt] = __builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
+                                               rs, ((row * SG + sidx) * 2u) | oob, 0, 0));
+    }
+  };
+  auto store_x = [&](const XStage& g, int buf) {
+#pragma unroll
+    for (int j = 0; j < XJ; ++j) {
+      const half8v x = g.v[j];
+      xs[buf][((xr0 + kT / 8 * j) * kGLD + 8 * xp) / 8] =
+          half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+    }
+  };
+
+  float16v acc[MI][NT];
+#pragma unroll
+  for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) acc[mi][nt] = float16v{};
+
+  auto compute = [&](const WStage& g, int buf) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      const half2v s1 = {g.s[nt], g.s[nt]};
+      const half_t s16v = g.s[nt] * (half_t)0.0625f;
+      const half2v s16 = {s16v, s16v};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        half2v r[4];
+        unpack_word(g.w[nt][ks], nib, z1, z16, r);
+        const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
+        const half8v bfr = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+#pragma unroll
+        for (int mi = 0; mi < MI; ++mi) {
+          const half8v afr =
+              xs[buf][((32 * MI * wm + 32 * mi + li) * kGLD + 32 * lh + 8 * ks) / 8];
+          acc[mi][nt] = mfma32x32x16(afr, bfr, acc[mi][nt]);
+        }
+      }
+    }
+  };
+
+  // Loads past K read zeros; the trailing steps of the last ring turn
+  // compute on zeros.
+  const int nsteps = (a.K + kGBK - 1) / kGBK;
+  XStage xr[2];
+  WStage wr[kRingW];
+  load_x(xr[0], 0);
+  load_x(xr[1], kGBK);
+#pragma unroll
+  for (int u = 0; u < kRingW; ++u) load_w(wr[u], u * kGBK);
+  store_x(xr[0], 0);
+  lds_barrier();
+  for (int st = 0; st < nsteps; st += kRingW) {
+#pragma unroll
+    for (int u = 0; u < kRingW; ++u) {
+      const int s = st + u;
+      load_x(xr[u & 1], (s + 2) * kGBK);
+      compute(wr[u], u & 1);
+      load_w(wr[u], (s + kRingW) * kGBK);
+      store_x(xr[(u + 1) & 1], (u + 1) & 1);
+      lds_barrier();
+    }
+  }
+
+  // acc[mi][nt] register r: row 32(MI wm + mi) + 8(r/4) + 4(lane/32) + r%4,
+  // column 32(NT wn + nt) + lane%32.
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = nw0 + 32 * nt + li;
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 32 * MI * wm + 32 * mi + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (m < a.M) a.Y[(int64_t)m * a.ldy + n] = (half_t)acc[mi][nt][r];
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // MFMA regime.  Each wave computes a 32 (m) x 32*TN (n) strip; 4 waves side
 // by side along N.  Per 64-column step of K, lane group g owns columns
 // [kb + 32g, kb + 32g + 32): one 16-byte word quad and one scale per row.
@@ -739,6 +900,19 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
         hipLaunchKernelGGL((w4a16_skinny_kernel<2, 2, kSkinnyWaves, false>), grid,
                            dim3(kSkinnyWaves * kWave), 0, s, a);
     }
+    return hipGetLastError();
+  }
+#ifndef NESO_GEMM_WN
+#define NESO_GEMM_WN 2
+#endif
+#ifndef NESO_GEMM_BN
+#define NESO_GEMM_BN 64
+#endif
+  constexpr int WM = 2, WN = NESO_GEMM_WN, BN = NESO_GEMM_BN;
+  if ((int64_t)kGBM * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
+      (int64_t)BN * a.K / 2 < ((int64_t)1 << 31)) {
+    const int tiles = ((a.M + kGBM - 1) / kGBM) * ((a.N + BN - 1) / BN);
+    hipLaunchKernelGGL((w4a16_gemm_kernel<WM, WN, BN>), dim3(tiles), dim3(WM * WN * kWave), 0, s, a);
     return hipGetLastError();
   }
   constexpr int TN = 2;
