@@ -76,6 +76,24 @@ int neso_flash_attention_fwd(const void* Q, const void* K, const void* V, float*
                              int32_t causal, void* stream);
 
 /*
+ * Sliding-window attention.  Replaces the windowed `flash_attention_fwd`
+ * kernel exercised by debug/fa2_correctness_legacy.py:92-102 (buffers
+ * Q, K, V, O; scalars seq_len, stride_h, stride_m, sm_scale, window_left,
+ * window_right, in that order), whose reference is :53-64: key j is visible
+ * to query i iff i - window_left <= j <= i + window_right.  Layout as in the
+ * reference: row i of head h starts at element i * stride_m + h * stride_h
+ * of Q, K, V and O (e.g. [seq][heads * head_dim] with stride_h = head_dim).
+ * Appended: num_heads, head_dim (32, 64, 128), out_dtype (NESO_OUT_F16 as
+ * the reference kernel, or NESO_OUT_F32), stream.  Windows are clamped to
+ * seq_len; negative windows are NESO_EINVAL.
+ */
+int neso_flash_attention_window_fwd(const void* Q, const void* K, const void* V, void* O,
+                                    int32_t seq_len, int32_t stride_h, int32_t stride_m,
+                                    float sm_scale, int32_t window_left, int32_t window_right,
+                                    int32_t num_heads, int32_t head_dim, int32_t out_dtype,
+                                    void* stream);
+
+/*
  * Relative-position-bias FA2.  Replaces `rel_pos_fa2_fwd` of
  * tests/test_rel_pos_fa2.py:157-163 (grid (T/BM, nh) at :364-368).  The
  * first ten parameters keep the reference order and meaning:

@@ -21,6 +21,7 @@ from .kernels import (  # noqa: F401
     KERNELS,
     attention,
     flash_attention_fwd,
+    flash_attention_window_fwd,
     launch,
     rel_pos_attention,
     rel_pos_fa2_fwd,
@@ -28,6 +29,7 @@ from .kernels import (  # noqa: F401
     w4a16_matmul,
     w8a16_matmul,
     w8a16_scaled_matmul,
+    window_attention,
 )
 from .packing import pack_int4, unpack_int4  # noqa: F401
 

@@ -143,9 +143,14 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     qf[ks] = neg ? -t : t;
   }
 
-  // Key blocks this workgroup visits; group kg takes blocks kg + KSPLIT*i.
-  const int kend = CAUSAL ? min(N, q0 + kBM) : N;
-  const int nblk = (kend + kKB - 1) / kKB;
+  // Key blocks this workgroup visits: [blk0, blk0 + nblk); group kg takes
+  // blocks blk0 + kg + KSPLIT*i.  The masked kernels see the keys of the
+  // window [q - wl, q + wr] of their queries only.
+  const int wl = p.win_left, wr = p.win_right;
+  const int kbeg = CAUSAL ? max(0, q0 - wl) : 0;
+  const int kend = CAUSAL ? (int)min((int64_t)N, (int64_t)q0 + kBM + wr) : N;
+  const int blk0 = kbeg / kKB;
+  const int nblk = max(0, (kend + kKB - 1) / kKB - blk0);
   const int my_n = nblk > kg ? (nblk - kg + KSPLIT - 1) / KSPLIT : 0;
   const int iters = (nblk + KSPLIT - 1) / KSPLIT;  // uniform over the workgroup
 
@@ -169,7 +174,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   const int kgu = kg;
 
   auto gload = [&](St& st, int i) {
-    const int blk = min(kgu + KSPLIT * i, nblk - 1);
+    const int blk = blk0 + max(0, min(kgu + KSPLIT * i, nblk - 1));
     const int kb0 = blk * kKB;
     const uint32_t bytes = (uint32_t)min(N - kb0, kKB) * p.stride_kv * 2;
     const rsrc_t rk = make_rsrc(Kh + (int64_t)kb0 * p.stride_kv, bytes);
@@ -227,9 +232,9 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   const half2v ones = {(half_t)1.f, (half_t)1.f};
 
   auto compute = [&](int i, int buf) {
-    const int kb0 = (kg + KSPLIT * i) * kKB;
-    // A wave whose queries all precede this key block has nothing to do.
-    if (CAUSAL && kb0 > qw0 + 31) return;
+    const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
+    // A wave whose 32 queries all miss this key block has nothing to do.
+    if (CAUSAL && (kb0 > qw0 + 31 + wr || kb0 + kKB - 1 < qw0 - wl)) return;
     const half_t* k_l = &smem[(kg * 2 + buf) * SLOT];
     const half_t* v_l = k_l + KHALF;
 
@@ -244,7 +249,10 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     }
 
     // ---- logits x (scaled log2 units for bias modes, raw s otherwise) ----
-    const bool masked = (kb0 + kKB > N) || (CAUSAL && kb0 + kKB - 1 > qw0);
+    // Masked: the block runs past N, or some key of it is outside the
+    // window of some query of this wave.
+    const bool masked =
+        (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
     if (BIAS != kBiasNone) {
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
@@ -269,13 +277,17 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
       // Keeps this a real (scalar) branch: if-converted, the masking would
       // cost 64 VALU ops on every block instead of on the few masked ones.
       asm volatile("");
-      // key >= lim is invisible to this lane's query.
-      const int lim = (CAUSAL ? min(N, q + 1) : N) - kb0 - 8 * g;
+      // Keys outside [lo, lim) (relative to kb0 + 8g) are invisible to this
+      // lane's query.
+      const int lim = (CAUSAL ? (int)min((int64_t)N, (int64_t)q + wr + 1) : N) - kb0 - 8 * g;
+      const int lo = (CAUSAL ? q - wl : 0) - kb0 - 8 * g;
 #pragma unroll
       for (int t = 0; t < NT; ++t)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (32 * t + 16 * (r >> 3) + (r & 7) >= lim) s[t][r] = -INFINITY;
+        for (int r = 0; r < 16; ++r) {
+          const int kr = 32 * t + 16 * (r >> 3) + (r & 7);
+          if (kr >= lim || kr < lo) s[t][r] = -INFINITY;
+        }
     }
 
     // ---- online softmax with lazy rescale ----
@@ -297,7 +309,9 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     const float mx_c = (BIAS != kBiasNone || mx == -INFINITY) ? mx : mx * c;
     if (__any(mx_c > m_run + kLazyLog2)) {
       const float m_new = fmaxf(m_run, mx_c);
-      const float alpha = fast_exp2(m_run - m_new);  // 0 on the first block
+      // 0 on a row's first visible block; 1 while a row has seen no visible
+      // key yet (a windowed row can miss a block its wave still visits).
+      const float alpha = (m_new == -INFINITY) ? 1.f : fast_exp2(m_run - m_new);
       m_run = m_new;
       l_run *= alpha;
 #pragma unroll

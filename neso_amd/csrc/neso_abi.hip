@@ -74,6 +74,24 @@ const char kManifest[] = R"JSON({
       {"index": 13, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
      "threadgroup_size": 256, "block_m": 128, "block_n": 64, "head_dims": [32, 64, 128],
      "grid": ["cdiv(N, 128) * batch_heads", "1", "1"]},
+    {"name": "neso_flash_attention_window_fwd", "replaces": "flash_attention_fwd with window_left/right (debug/fa2_correctness_legacy.py:92-102)",
+     "params": [
+      {"index": 0, "name": "Q", "type": "const fp16*", "is_pointer": true},
+      {"index": 1, "name": "K", "type": "const fp16*", "is_pointer": true},
+      {"index": 2, "name": "V", "type": "const fp16*", "is_pointer": true},
+      {"index": 3, "name": "O", "type": "fp16*|fp32*", "is_pointer": true},
+      {"index": 4, "name": "seq_len", "type": "int32", "is_pointer": false},
+      {"index": 5, "name": "stride_h", "type": "int32", "is_pointer": false},
+      {"index": 6, "name": "stride_m", "type": "int32", "is_pointer": false},
+      {"index": 7, "name": "sm_scale", "type": "fp32", "is_pointer": false},
+      {"index": 8, "name": "window_left", "type": "int32", "is_pointer": false},
+      {"index": 9, "name": "window_right", "type": "int32", "is_pointer": false},
+      {"index": 10, "name": "num_heads", "type": "int32", "is_pointer": false},
+      {"index": 11, "name": "head_dim", "type": "int32", "is_pointer": false},
+      {"index": 12, "name": "out_dtype", "type": "int32", "is_pointer": false},
+      {"index": 13, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
+     "threadgroup_size": 256, "block_m": 128, "block_n": 64,
+     "grid": ["cdiv(seq_len, 128) * num_heads", "1", "1"]},
     {"name": "neso_rel_pos_fa2_fwd", "replaces": "rel_pos_fa2_fwd (tests/test_rel_pos_fa2.py:157-163)",
      "params": [
       {"index": 0, "name": "Q", "type": "const fp16*", "is_pointer": true},
@@ -143,7 +161,7 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
                int32_t stride_q, int32_t stride_kv, int32_t stride_o, float scale,
                int32_t head_dim, int32_t heads, int64_t bh_q, int64_t bh_kv, int64_t bh_o,
                int64_t bias_stride_h, int causal, int bias_kind, bool out_f16, void* stream,
-               const char* name) {
+               const char* name, int32_t win_left = -1, int32_t win_right = -1) {
   if (!Q || !K || !V || !O) return fail(NESO_EINVAL, "%s: null tensor pointer", name);
   if (N < 0) return fail(NESO_EINVAL, "%s: N=%d < 0", name, N);
   if (heads < 0) return fail(NESO_EINVAL, "%s: batch_heads=%d < 0", name, heads);
@@ -188,6 +206,9 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
   a.batch_heads = heads;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.ksplit = env_ksplit();
+  // Causal is the window (N, 0); windows wider than N are clamped to N.
+  a.win_left = win_left < 0 ? N : (win_left < N ? win_left : N);
+  a.win_right = win_right < 0 ? 0 : (win_right < N ? win_right : N);
   return launched(neso::launch_fa2(a, head_dim, causal != 0, bias_kind, out_f16,
                                    static_cast<hipStream_t>(stream)),
                   name);
@@ -241,6 +262,22 @@ int neso_flash_attention_fwd(const void* Q, const void* K, const void* V, float*
   return fa2_common(Q, K, V, O, nullptr, N, stride_qo, stride_kv, stride_qo, scale, head_dim,
                     batch_heads, stride_bh_qo, stride_bh_kv, stride_bh_qo, 0, causal,
                     neso::kBiasNone, false, stream, "flash_attention_fwd");
+}
+
+int neso_flash_attention_window_fwd(const void* Q, const void* K, const void* V, void* O,
+                                    int32_t seq_len, int32_t stride_h, int32_t stride_m,
+                                    float sm_scale, int32_t window_left, int32_t window_right,
+                                    int32_t num_heads, int32_t head_dim, int32_t out_dtype,
+                                    void* stream) {
+  const char* name = "flash_attention_window_fwd";
+  if (window_left < 0 || window_right < 0)
+    return fail(NESO_EINVAL, "%s: window (%d, %d) must be non-negative", name, window_left,
+                window_right);
+  if (out_dtype != NESO_OUT_F16 && out_dtype != NESO_OUT_F32)
+    return fail(NESO_EINVAL, "%s: out_dtype=%d", name, out_dtype);
+  return fa2_common(Q, K, V, O, nullptr, seq_len, stride_m, stride_m, stride_m, sm_scale,
+                    head_dim, num_heads, stride_h, stride_h, stride_h, 0, 1, neso::kBiasNone,
+                    out_dtype == NESO_OUT_F16, stream, name, window_left, window_right);
 }
 
 int neso_rel_pos_fa2_fwd(const void* Q, const void* K, const void* V, const void* bias, void* O,

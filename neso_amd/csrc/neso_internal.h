@@ -30,6 +30,10 @@ struct Fa2Args {
   float scale_log2;     // softmax scale * log2(e)
   int32_t num_qblocks;  // filled in by launch_fa2
   int32_t ksplit;       // key groups per workgroup (1, 2); 0 = chosen from the grid size
+  // Window of the masked (causal) kernels: key j is visible to query i iff
+  // i - win_left <= j <= i + win_right.  Causal is (N, 0).
+  int32_t win_left;
+  int32_t win_right;
 };
 
 // Compute units of the current device (cached per device).

@@ -25,6 +25,7 @@ from . import _lib
 
 __all__ = [
     "flash_attention_fwd",
+    "flash_attention_window_fwd",
     "rel_pos_fa2_fwd",
     "w4a16_matmul",
     "w8a16_matmul",
@@ -33,6 +34,7 @@ __all__ = [
     "KERNELS",
     "attention",
     "rel_pos_attention",
+    "window_attention",
     "w4a16_linear",
 ]
 
@@ -86,6 +88,37 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
         _ptr(O, "O", torch.float32), int(N), int(stride_qo), int(stride_kv), float(scale),
         int(head_dim), int(batch_heads), int(stride_bh_qo), int(stride_bh_kv), int(bool(causal)),
         _stream(stream, Q, O))
+    _lib.check(st)
+
+
+def flash_attention_window_fwd(Q, K, V, O, seq_len: int, stride_h: int, stride_m: int,
+                               sm_scale: float, window_left: int, window_right: int, *,
+                               num_heads: int, head_dim: int | None = None,
+                               stream=None) -> None:
+    """Sliding-window attention: key j is visible to query i iff
+    i - window_left <= j <= i + window_right.
+
+    Positional arguments as the windowed reference kernel
+    (debug/fa2_correctness_legacy.py:92-102): Q, K, V fp16, O, seq_len,
+    stride_h (elements between heads of one row), stride_m (elements
+    between rows), sm_scale, window_left, window_right.  ``num_heads``
+    replaces the reference's grid y.  The output dtype follows O (fp16 as in
+    the reference, or fp32).
+    """
+    if head_dim is None:
+        if not isinstance(Q, torch.Tensor):
+            raise ValueError("head_dim is required when Q is a raw address")
+        head_dim = int(Q.shape[-1])
+    if isinstance(O, torch.Tensor):
+        out_dtype = _lib.NESO_OUT_F32 if O.dtype == torch.float32 else _lib.NESO_OUT_F16
+    else:
+        out_dtype = _lib.NESO_OUT_F16
+    lib = _lib.load()
+    st = lib.neso_flash_attention_window_fwd(
+        _ptr(Q, "Q", torch.float16), _ptr(K, "K", torch.float16), _ptr(V, "V", torch.float16),
+        _ptr(O, "O", (torch.float16, torch.float32)), int(seq_len), int(stride_h), int(stride_m),
+        float(sm_scale), int(window_left), int(window_right), int(num_heads), int(head_dim),
+        int(out_dtype), _stream(stream, Q, O))
     _lib.check(st)
 
 
@@ -154,6 +187,7 @@ def w8a16_scaled_matmul(A, B, C, scale, K: int, stride_am: int, stride_bk: int, 
 
 KERNELS = {
     "flash_attention_fwd": flash_attention_fwd,
+    "flash_attention_window_fwd": flash_attention_window_fwd,
     "rel_pos_fa2_fwd": rel_pos_fa2_fwd,
     "w4a16_matmul": w4a16_matmul,
     "w8a16_matmul": w8a16_matmul,
@@ -202,6 +236,25 @@ def rel_pos_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: 
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     rel_pos_fa2_fwd(q, k, v, table, out, n, d, scale, n * d, 2 * n - 1, num_heads=h, head_dim=d,
                     bias_mode=_lib.NESO_BIAS_TABLE_F32)
+    return out
+
+
+def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_left: int,
+                     window_right: int, *, scale: float | None = None,
+                     out_dtype: torch.dtype = torch.float16,
+                     out: torch.Tensor | None = None) -> torch.Tensor:
+    """Sliding-window attention over fp16 [seq, heads, d] tensors (the
+    reference's [seq][heads * d] rows); returns [seq, heads, d] in out_dtype."""
+    if q.shape != k.shape or q.shape != v.shape or q.dim() != 3:
+        raise ValueError("q, k, v must have the same shape [seq, heads, d]")
+    if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
+        raise ValueError("q, k, v must be contiguous")
+    n, h, d = (int(x) for x in q.shape)
+    if out is None:
+        out = torch.empty((n, h, d), dtype=out_dtype, device=q.device)
+    scale = 1.0 / math.sqrt(d) if scale is None else scale
+    flash_attention_window_fwd(q, k, v, out, n, d, h * d, scale, window_left, window_right,
+                               num_heads=h, head_dim=d)
     return out
 
 

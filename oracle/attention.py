@@ -17,6 +17,7 @@ import torch
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, *,
               causal: bool = False, logit_bias: torch.Tensor | None = None,
+              window: tuple[int, int] | None = None,
               dtype: torch.dtype = torch.float32, chunk_rows: int = 1024) -> torch.Tensor:
     """Closed form O = softmax(Q K^T * scale [+ logit_bias], mask) V on the CPU.
 
@@ -24,7 +25,10 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, *
     subtraction, exp, normalise, weighted sum of V) vectorised over rows and
     over leading (batch, head) dimensions.  ``logit_bias`` [..., N, N] is
     added after scaling (BASELINE rel-pos semantics).  ``causal`` masks key j
-    > query i, the window (inf, 0) of debug/fa2_correctness_legacy.py:53-64.
+    > query i, the window (inf, 0) of debug/fa2_correctness_legacy.py:53-64;
+    ``window`` = (left, right) masks j < i - left and j > i + right (the
+    masked logits get -inf here, -1e9 in the reference: identical results
+    while every row keeps its diagonal, which non-negative windows do).
     Inputs are upcast to ``dtype``; rows are processed in chunks so the score
     matrix stays bounded.  Returns ``dtype`` [..., N, d].
     """
@@ -39,10 +43,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, *
         s = torch.matmul(q[..., r0:r1, :], kt) * scale
         if logit_bias is not None:
             s = s + logit_bias[..., r0:r1, :].to(dtype)
-        if causal:
+        if causal or window is not None:
             rows = torch.arange(r0, r1).unsqueeze(1)
             cols = torch.arange(n).unsqueeze(0)
-            s = s.masked_fill(cols > rows, float("-inf"))
+            left, right = window if window is not None else (n, 0)
+            s = s.masked_fill((cols > rows + right) | (cols < rows - left), float("-inf"))
         m = s.amax(dim=-1, keepdim=True)
         p = torch.exp(s - m)
         out[..., r0:r1, :] = torch.matmul(p, v) / p.sum(dim=-1, keepdim=True)
@@ -91,6 +96,21 @@ def fa2_online(q: np.ndarray, k: np.ndarray, v: np.ndarray, scale: float, *, blo
             m_i = m_new
         out[rows] = acc / np.maximum(l_i, 1e-6)[:, None]
     return out
+
+
+def reference_window_attention(q: np.ndarray, k: np.ndarray, v: np.ndarray, sm_scale: float,
+                               window_left: int, window_right: int) -> np.ndarray:
+    """Sliding-window attention of one head, restating
+    debug/fa2_correctness_legacy.py:53-64: float32 scores * sm_scale, keys
+    j < i - window_left or j > i + window_right set to -1e9, softmax, @ V."""
+    n = q.shape[0]
+    scores = (q.astype(np.float32) @ k.astype(np.float32).T) * np.float32(sm_scale)
+    i = np.arange(n)[:, None]
+    j = np.arange(n)[None, :]
+    scores = np.where((j < i - window_left) | (j > i + window_right), np.float32(-1e9), scores)
+    mx = scores.max(axis=1, keepdims=True)
+    e = np.exp(scores - mx)
+    return (e / e.sum(axis=1, keepdims=True)) @ v.astype(np.float32)
 
 
 def rel_pos_table_to_dense(table: torch.Tensor, n: int) -> torch.Tensor:

@@ -19,6 +19,9 @@ fixtures are independent of ``oracle/`` (which is vectorised torch/numpy):
 * qmm_w8a16_*.npz / qmm_scaled_*.npz / qmm_w4i8_*.npz —
   tests/test_quantized_matmul.py:335-337, :379-381, :423-426 inputs and the
   f64 triple-loop outputs of :288-311.
+* fa2_window_S{seq}_H{h}_d{d}_w{l}_{r}.npz — debug/fa2_correctness_legacy.py:68-79
+  inputs (np.random.seed(42), randn * 0.5 as fp16) and the sliding-window
+  reference of :53-64 (-1e9 outside [i - left, i + right]) in float64 loops.
 * qmm_int4_kat.npz — hand-made packed int4 words with known nibble codes,
   group scales and one-hot activations, expected values from the format
   definition (code of column k = nibble k % 8 of word k // 8).
@@ -85,6 +88,37 @@ def fa2_ref_rows(n: int, d: int) -> None:
                         q=np.array(q, np.float64), k=np.array(k, np.float64),
                         v=np.array(v, np.float64), rows=np.array(rows),
                         expected=np.array(expected, np.float64))
+
+
+def fa2_window_ref(seq: int, heads: int, d: int, wl: int, wr: int) -> None:
+    """debug/fa2_correctness_legacy.py:68-79 inputs (np.random.seed(42), randn * 0.5 as
+    fp16, rows [seq][heads * d]) and the :53-64 reference evaluated with loops in float64."""
+    rs = np.random.RandomState(42)
+    kv = heads * d
+    Q = (rs.randn(seq, kv) * 0.5).astype(np.float16)
+    K = (rs.randn(seq, kv) * 0.5).astype(np.float16)
+    V = (rs.randn(seq, kv) * 0.5).astype(np.float16)
+    scale = 1.0 / math.sqrt(d)
+    out = np.zeros((seq, kv))
+    Qd, Kd, Vd = (a.astype(np.float64) for a in (Q, K, V))
+    for h in range(heads):
+        c0 = h * d
+        for i in range(seq):
+            scores = []
+            for j in range(seq):
+                s = sum(Qd[i, c0 + c] * Kd[j, c0 + c] for c in range(d)) * scale
+                scores.append(-1e9 if (j < i - wl or j > i + wr) else s)
+            mx = max(scores)
+            ex = [math.exp(x - mx) for x in scores]
+            tot = sum(ex)
+            for j in range(seq):
+                w = ex[j] / tot
+                if w:
+                    for c in range(d):
+                        out[i, c0 + c] += w * Vd[j, c0 + c]
+    np.savez_compressed(HERE / f"fa2_window_S{seq}_H{heads}_d{d}_w{wl}_{wr}.npz", seq=seq,
+                        heads=heads, d=d, window_left=wl, window_right=wr, scale=scale,
+                        Q=Q, K=K, V=V, expected=out)
 
 
 def relpos_ref(t: int, d: int, nh: int) -> None:
@@ -174,6 +208,8 @@ def main() -> int:
         fa2_ref_rows(n, d)
     relpos_ref(32, 64, 2)
     relpos_ref(64, 64, 4)
+    fa2_window_ref(64, 3, 64, 16, 0)
+    fa2_window_ref(48, 2, 32, 5, 7)
     qmm_ref("w8a16", 32, 32, 32)
     qmm_ref("w8a16", 64, 64, 128)
     qmm_ref("w4i8", 64, 64, 64)

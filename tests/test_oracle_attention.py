@@ -210,3 +210,54 @@ def test_planted_missing_rescale_is_caught():
         qb_out[rows] = acc / l_i[:, None]
     assert np.max(np.abs(good - ref)) < 1e-5
     assert np.max(np.abs(qb_out - ref)) > 1e-2
+
+
+# ---- sliding window (debug/fa2_correctness_legacy.py:53-64) ----
+
+@pytest.mark.parametrize("n,left,right", [(1, 0, 0), (37, 0, 0), (64, 16, 0), (100, 7, 23),
+                                          (90, 200, 200), (90, 89, 0)])
+def test_window_matches_sdpa_mask(n, left, right):
+    q, k, v = (t[0] for t in I.fa2_inputs(1, 2, n, 64, seed=n + left))
+    i = torch.arange(n).unsqueeze(1)
+    j = torch.arange(n).unsqueeze(0)
+    mask = torch.zeros(n, n, dtype=torch.float64)
+    mask = mask.masked_fill((j < i - left) | (j > i + right), float("-inf"))
+    ref = _sdpa64(q, k, v, 0.125, mask=mask)
+    out = A.attention(q, k, v, 0.125, window=(left, right), dtype=torch.float64)
+    assert torch.allclose(out, ref, atol=1e-12)
+
+
+def test_window_special_cases():
+    q, k, v = (t[0] for t in I.fa2_inputs(1, 3, 120, 32, seed=5))
+    full = A.attention(q, k, v, 0.2, dtype=torch.float64)
+    causal = A.attention(q, k, v, 0.2, causal=True, dtype=torch.float64)
+    assert torch.equal(A.attention(q, k, v, 0.2, window=(120, 120), dtype=torch.float64), full)
+    assert torch.equal(A.attention(q, k, v, 0.2, window=(500, 0), dtype=torch.float64), causal)
+    # (0, 0): every query sees only its own key.
+    diag = A.attention(q, k, v, 0.2, window=(0, 0), dtype=torch.float64)
+    assert torch.allclose(diag, v.double(), atol=1e-15)
+
+
+@pytest.mark.parametrize("name", ["fa2_window_S64_H3_d64_w16_0", "fa2_window_S48_H2_d32_w5_7"])
+def test_window_golden(golden_dir, name):
+    """Reference generator and reference formula (float64 loops) vs both oracle forms."""
+    z = np.load(golden_dir / f"{name}.npz")
+    seq, heads, d = int(z["seq"]), int(z["heads"]), int(z["d"])
+    wl, wr, scale = int(z["window_left"]), int(z["window_right"]), float(z["scale"])
+    for h in range(heads):
+        cols = slice(h * d, (h + 1) * d)
+        exp = z["expected"][:, cols]
+        legacy = A.reference_window_attention(z["Q"][:, cols], z["K"][:, cols], z["V"][:, cols],
+                                              scale, wl, wr)
+        assert np.abs(legacy - exp).max() < 1e-5
+        qt, kt, vt = (torch.from_numpy(z[x][:, cols].astype(np.float32)) for x in "QKV")
+        out = A.attention(qt, kt, vt, scale, window=(wl, wr), dtype=torch.float64).numpy()
+        assert np.abs(out - exp).max() < 1e-10
+
+
+def test_planted_window_off_by_one_is_caught(golden_dir):
+    z = np.load(golden_dir / "fa2_window_S64_H3_d64_w16_0.npz")
+    cols = slice(0, 64)
+    qt, kt, vt = (torch.from_numpy(z[x][:, cols].astype(np.float32)) for x in "QKV")
+    wrong = A.attention(qt, kt, vt, float(z["scale"]), window=(17, 0), dtype=torch.float64)
+    assert np.abs(wrong.numpy() - z["expected"][:, cols]).max() > 1e-3
