@@ -312,6 +312,24 @@ def sweep(neso_amd, torch, I, steps, warmup):
     tf = flop / (ms * 1e-3) / 1e12
     rows.append({"kernel": "rel_pos_fa2", **rc, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
                  "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "timing": mode})
+    # Reference-format W8A16 at the size the reference publishes (4096^3,
+    # PERFORMANCE.md:61-63 and :77-81: 5,744 and 5,976 GFLOP/s on Apple M2 Max).
+    m = n = k = 4096
+    a = torch.randn(m, k, dtype=torch.float16, device="cuda")
+    b = torch.randint(-128, 128, (k, n), dtype=torch.int8, device="cuda")
+    c = torch.empty(m, n, dtype=torch.float32, device="cuda")
+    sc = (torch.rand(n, device="cuda") * 0.1 + 0.001).half()
+    for name, fn, ref_gflops in (
+            ("w8a16_matmul", lambda i: neso_amd.w8a16_matmul(a, b, c, k, k, n, n, M=m, N=n),
+             5744.0),
+            ("w8a16_scaled_matmul",
+             lambda i: neso_amd.w8a16_scaled_matmul(a, b, c, sc, k, k, n, n, M=m, N=n), 5976.0)):
+        ms, mode, _, _ = best_time(fn, max(16, steps // 4), 2, torch)
+        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+        rows.append({"kernel": name, "M": m, "N": n, "K": k, "us": round(ms * 1e3, 2),
+                     "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                     "reference_m2max_tflops": ref_gflops / 1e3,
+                     "x_reference": round(tf / (ref_gflops / 1e3), 1), "timing": mode})
     for cfg in I.QMM_CONFIGS[1:]:
         r = qmm_case(neso_amd, torch, I, cfg, steps, warmup, rotate=8)
         rows.append({"kernel": "w4a16", **cfg, "us": round(r["ms_per_step"] * 1e3, 2),

@@ -775,6 +775,134 @@ __global__ __launch_bounds__(kThreads) void w4a16_mfma_kernel(W4Args a) {
 }
 
 // ---------------------------------------------------------------------------
+// W8A16 GEMM: C[M][N] f32 = A[M][K] f16 * f16(B[K][N] int8) [* scale[n]].
+//
+// Workgroup tile 128 x 128, four waves of 64 x 64 (2 x 2
+// v_mfma_f32_32x32x16_f16 tiles), K-steps of 32.  A goes through LDS with
+// rows padded to 40 halves (conflict-free ds_read_b128).  B is N-contiguous
+// in memory but the MFMA B operand needs 8 consecutive k of one column per
+// lane, so the tile is transposed on the way into LDS: thread (c, kp) loads
+// eight columns of k-rows 2kp and 2kp+1, converts them to f16 exactly
+// (int8 -> f16 via the exponent trick: 0x6400 | (b ^ 0x80) is 1024 + b +
+// 128) and stores (k, k+1) pairs per column, Bs[n][k] (2-way write
+// conflicts).  Double-buffered LDS, global loads one step ahead.
+constexpr int kW8BM = 128, kW8BN = 128, kW8BK = 32, kW8LD = kW8BK + 8;
+
+__global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
+  __shared__ half8v as[2][kW8BM * kW8LD / 8];
+  __shared__ uint32_t bs[2][kW8BN * kW8LD / 2];  // (k, k+1) f16 pairs
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 31, lh = lane >> 5;
+  const int m0 = blockIdx.y * kW8BM, n0 = blockIdx.x * kW8BN;
+  const int mrows = min(kW8BM, a.M - m0);
+  constexpr uint32_t kOut = 0x80000000u;
+  const rsrc_t ra = make_rsrc(a.A + (int64_t)m0 * a.lda, (uint32_t)((mrows - 1) * a.lda + a.K) * 2u);
+  const rsrc_t rb = make_rsrc(a.B + n0, (uint32_t)((a.K - 1) * (int64_t)a.ldb + min(kW8BN, a.N - n0)));
+  // A: rows (tid >> 2) + 64j, 16-byte piece tid & 3 of the step.
+  const int ar = tid >> 2, ap = tid & 3;
+  // B: column chunk c (8 columns), k pair kp.
+  const int bc = tid >> 4, bkp = tid & 15;
+  const uint32_t nlim = (uint32_t)min(kW8BN, a.N - n0);
+  struct Stage {
+    half8v av[2];
+    uint32_t b0[2], b1[2];  // 8 int8 of k-row 2kp and of 2kp+1
+  };
+  auto load = [&](Stage& g, int k0) {
+    const uint32_t aoob = k0 + 8 * ap < a.K ? 0u : kOut;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      g.av[j] = buf_load_half8(ra, (((uint32_t)(ar + 64 * j) * a.lda + k0 + 8 * ap) * 2u) | aoob);
+    const int k = k0 + 2 * bkp;
+    // Columns past N: offsets beyond the row end read the next row's bytes,
+    // so mask them; rows past K fall outside the buffer.
+    const uint32_t coob = (uint32_t)(8 * bc) < nlim ? 0u : kOut;
+    typedef int int2v __attribute__((ext_vector_type(2)));
+    const int2v r0 = __builtin_amdgcn_raw_buffer_load_b64(
+        rb, ((uint32_t)k * a.ldb + 8u * bc) | (k < a.K ? coob : kOut), 0, 0);
+    const int2v r1 = __builtin_amdgcn_raw_buffer_load_b64(
+        rb, ((uint32_t)(k + 1) * a.ldb + 8u * bc) | (k + 1 < a.K ? coob : kOut), 0, 0);
+    g.b0[0] = r0[0]; g.b0[1] = r0[1];
+    g.b1[0] = r1[0]; g.b1[1] = r1[1];
+  };
+  const uint32_t magic = vgpr_const(0x64006400u);
+  const half2v bias = {(half_t)1152, (half_t)1152};
+  auto store = [&](const Stage& g, int buf) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) as[buf][((ar + 64 * j) * kW8LD + 8 * ap) / 8] = g.av[j];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      const uint32_t x0 = g.b0[w] ^ 0x80808080u, x1 = g.b1[w] ^ 0x80808080u;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // Byte e of both k-rows -> the f16 pair (B[k][n], B[k+1][n]).
+        const uint32_t sel = 0x0c000c00u | (uint32_t)(4 + e) << 16 | (uint32_t)e;
+        const uint32_t pr = __builtin_amdgcn_perm(x1, x0, sel) | magic;
+        const half2v v = __builtin_bit_cast(half2v, pr) - bias;
+        const int n = 8 * bc + 4 * w + e;
+        bs[buf][(n * kW8LD + 2 * bkp) / 2] = __builtin_bit_cast(uint32_t, v);
+      }
+    }
+  };
+
+  float16v acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = float16v{};
+  auto compute = [&](int buf) {
+#pragma unroll
+    for (int ks = 0; ks < kW8BK / 16; ++ks) {
+      half8v bf[2];
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni)
+        bf[ni] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4v*>(
+                                                &bs[buf][((64 * wn + 32 * ni + li) * kW8LD + 16 * ks + 8 * lh) / 2]));
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) {
+        const half8v af = as[buf][((64 * wm + 32 * mi + li) * kW8LD + 16 * ks + 8 * lh) / 8];
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma32x32x16(af, bf[ni], acc[mi][ni]);
+      }
+    }
+  };
+
+  const int nsteps = (a.K + kW8BK - 1) / kW8BK;
+  Stage sA, sB;
+  load(sA, 0);
+  store(sA, 0);
+  load(sB, kW8BK);
+  lds_barrier();
+  for (int st = 0; st < nsteps; st += 2) {
+    load(sA, (st + 2) * kW8BK);  // past K: zeros
+    compute(0);
+    store(sB, 1);
+    lds_barrier();
+    load(sB, (st + 3) * kW8BK);
+    compute(1);
+    store(sA, 0);
+    lds_barrier();
+  }
+
+  // acc[mi][ni] register r: row 64wm + 32mi + 8(r/4) + 4(lane/32) + r%4,
+  // column 64wn + 32ni + lane%32.
+#pragma unroll
+  for (int ni = 0; ni < 2; ++ni) {
+    const int n = n0 + 64 * wn + 32 * ni + li;
+    if (n >= a.N) continue;
+    const float s = a.scale ? (float)a.scale[n] : 1.f;
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 64 * wm + 32 * mi + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (m < a.M) a.C[(int64_t)m * a.ldc + n] = acc[mi][ni][r] * s;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // W8A16: one 32x32 output tile per wave, B[K][N] int8 row-major.
 __global__ __launch_bounds__(kThreads) void w8a16_kernel(W8Args a) {
   const int lane = threadIdx.x & 63;
@@ -922,6 +1050,19 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
 }
 
 hipError_t launch_w8a16(const W8Args& a, hipStream_t s) {
+  // The tiled kernel reads A in 16-byte and B in 8-byte pieces: it needs
+  // those pieces aligned and never straddling the end of a row, and buffer
+  // offsets below 2^31 bytes.
+  const bool tiled = a.K % 8 == 0 && a.lda % 8 == 0 && a.N % 8 == 0 && a.ldb % 8 == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.A) & 15u) == 0 &&
+                     (reinterpret_cast<uintptr_t>(a.B) & 7u) == 0 &&
+                     (int64_t)kW8BM * a.lda * 2 < ((int64_t)1 << 31) &&
+                     (int64_t)a.K * a.ldb < ((int64_t)1 << 31);
+  if (tiled) {
+    const dim3 grid((a.N + kW8BN - 1) / kW8BN, (a.M + kW8BM - 1) / kW8BM);
+    hipLaunchKernelGGL(w8a16_gemm_kernel, grid, dim3(kThreads), 0, s, a);
+    return hipGetLastError();
+  }
   const dim3 grid((a.N + 127) / 128, (a.M + 31) / 32);
   hipLaunchKernelGGL(w8a16_kernel, grid, dim3(kThreads), 0, s, a);
   return hipGetLastError();

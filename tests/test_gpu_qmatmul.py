@@ -132,3 +132,25 @@ def test_w8a16_reference_configs(gpu, golden_dir, kind, mnk):
     fixture = golden_dir / f"qmm_{ {'w4a16': 'w4i8'}.get(kind, kind)}_{m}x{n}x{k}.npz"
     if fixture.exists():
         assert Q.rel_err(c.reshape(-1), np.load(fixture)["expected"]) < 1e-2
+
+
+@pytest.mark.parametrize("scaled", [False, True])
+@pytest.mark.parametrize("m,n,k", [(300, 136, 264), (1, 8, 8), (129, 256, 4096), (77, 100, 96),
+                                   (5, 13, 7)])
+def test_w8a16_tiled_and_fallback(gpu, m, n, k, scaled):
+    """The tiled kernel (N, K, strides multiples of 8) on ragged tiles, and the
+    per-element fallback (n = 100, 13; k = 7), against the float64 oracle on
+    the fp16-rounded activations."""
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    a = torch.randn(m, k, generator=g).half()
+    b = torch.randint(-128, 128, (k, n), generator=g, dtype=torch.int8)
+    s = (torch.rand(n, generator=g) * 0.1 + 0.001).half()
+    c = torch.full((m, n), float("nan"), dtype=torch.float32, device=DEV)
+    if scaled:
+        neso_amd.w8a16_scaled_matmul(a.to(DEV), b.to(DEV), c, s.to(DEV), k, k, n, n, M=m, N=n)
+        ref = Q.w8a16_scaled_matmul(a.double().numpy(), b.double().numpy(), s.double().numpy())
+    else:
+        neso_amd.w8a16_matmul(a.to(DEV), b.to(DEV), c, k, k, n, n, M=m, N=n)
+        ref = Q.w8a16_matmul(a.double().numpy(), b.double().numpy())
+    torch.cuda.synchronize()
+    assert Q.rel_err(c.cpu().numpy(), ref) < 1e-4
