@@ -41,6 +41,7 @@ import sys
 import time
 
 MFMA_F16_PEAK_TFLOPS = 2516.6  # 256 CUs * 2.4 GHz * 4096 dense fp16 FLOP/clk/CU
+FP32_MFMA_PEAK_TFLOPS = 157.3  # published dense fp32 MFMA peak
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 METRIC = "FA2 fwd TFLOP/s (d64,N2048) + % MFMA peak; int4 qmatmul HBM GB/s"
 
@@ -303,6 +304,18 @@ def sweep(neso_amd, torch, I, steps, warmup):
                              max(16, steps // 4), 2)
     rows.append({"kernel": "fa2", **c, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
                  "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "timing": tm["timing"]})
+    # fp32 Q/K/V (the reference's default qkv_dtype) at the headline shape:
+    # three fp16 MFMAs per product, so the useful-FLOP rate is compared with
+    # the fp32 dense MFMA peak, the unit that computes in this precision.
+    hb = I.FA2_HEADLINE
+    q, k, v = (t.cuda().float() for t in I.fa2_inputs(hb["B"], hb["H"], hb["N"], hb["d"]))
+    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    ms, mode, _, _ = best_time(lambda i: neso_amd.attention(q, k, v, out=out), steps, warmup,
+                               torch)
+    tf = 4.0 * hb["B"] * hb["H"] * hb["N"] ** 2 * hb["d"] / (ms * 1e-3) / 1e12
+    rows.append({"kernel": "fa2_f32_qkv", **hb, "causal": False, "us": round(ms * 1e3, 2),
+                 "tflops": round(tf, 2), "fp32_mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
+                 "timing": mode})
     rc = I.RELPOS_CONFIG
     q, k, v, table = (t.cuda() for t in I.relpos_inputs(**rc, seed=0))
     out = torch.empty(q.shape, dtype=torch.float32, device="cuda")

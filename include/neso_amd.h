@@ -76,6 +76,25 @@ int neso_flash_attention_fwd(const void* Q, const void* K, const void* V, float*
                              int32_t causal, void* stream);
 
 /*
+ * Flash-Attention-2 forward on fp32 Q, K, V: the reference's default
+ * `generate_fa2_ttir(..., qkv_dtype='f32')` kernel of
+ * tests/test_flash_attention.py:79-89 (f32 buffers packed at :277-280,
+ * same buffer order as above).  Parameters as neso_flash_attention_fwd,
+ * except:
+ *   Q, K, V   fp32 rows; strides and slice strides multiples of 4 elements
+ *   head_dim  32 or 64
+ * Each fp32 operand is split into fp16 hi + lo and every product is formed
+ * as hi*hi + hi*lo + lo*hi on the fp16 MFMA with fp32 accumulation, as is P
+ * for P V, so results track an fp32 computation (about 1e-6 absolute for
+ * unit-scale inputs).  Q, K, V elements must lie within the fp16 range
+ * (|x| < 65504).
+ */
+int neso_flash_attention_f32_fwd(const float* Q, const float* K, const float* V, float* O,
+                                 int32_t N, int32_t stride_qo, int32_t stride_kv, float scale,
+                                 int32_t head_dim, int32_t batch_heads, int64_t stride_bh_qo,
+                                 int64_t stride_bh_kv, int32_t causal, void* stream);
+
+/*
  * Sliding-window attention.  Replaces the windowed `flash_attention_fwd`
  * kernel exercised by debug/fa2_correctness_legacy.py:92-102 (buffers
  * Q, K, V, O; scalars seq_len, stride_h, stride_m, sm_scale, window_left,

@@ -40,6 +40,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_p, _p, _p, _p, _i32, _i32, _i32, _f32, _i32, _i32, _i64, _i64, _i32, _p],
     ),
+    "neso_flash_attention_f32_fwd": (
+        ctypes.c_int,
+        [_p, _p, _p, _p, _i32, _i32, _i32, _f32, _i32, _i32, _i64, _i64, _i32, _p],
+    ),
     "neso_flash_attention_window_fwd": (
         ctypes.c_int,
         [_p, _p, _p, _p, _i32, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _p],

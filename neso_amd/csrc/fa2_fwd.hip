@@ -75,18 +75,40 @@ __device__ __forceinline__ float sum_halves(float x) {
 template <int D>
 constexpr int key_block() { return 64; }
 
-template <int D>
+// One 8-element row piece of K or V in registers: f16, or f32 (two float4).
+template <bool F32IN>
+struct Piece8 {
+  half8v h;
+};
+template <>
+struct Piece8<true> {
+  float4v f[2];
+};
+
+template <int D, bool F32IN>
 struct Staging {
   static constexpr int kKB = key_block<D>();
-  static constexpr int KCH = kKB * D / 8 / kGroup;   // 16-byte K chunks per thread
+  static constexpr int KCH = kKB * D / 8 / kGroup;   // 8-element K pieces per thread
   static constexpr int VJOBS = kKB * D / 16;         // (key pair, 8 columns) jobs
   static constexpr int VCH = (VJOBS + kGroup - 1) / kGroup;
-  half8v k[KCH];
-  half8v v[VCH][2];
+  Piece8<F32IN> k[KCH];
+  Piece8<F32IN> v[VCH][2];
   float b;
 };
 
-template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int KSPLIT>
+// f32 -> (hi, lo) f16 split: x ~= hi + lo to about 2^-22 relative, so the
+// three products hi*hi + hi*lo + lo*hi of two split operands reproduce an
+// f32 product to that accuracy on the f16 MFMA.
+__device__ __forceinline__ void split_f16(const float4v (&f)[2], half8v& hi, half8v& lo) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float x = f[e >> 2][e & 3];
+    hi[e] = (half_t)x;
+    lo[e] = (half_t)(x - (float)hi[e]);
+  }
+}
+
+template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int KSPLIT, bool F32IN>
 __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   constexpr int kKB = key_block<D>();
   constexpr int NT = kKB / 32; // 32-key tiles per block
@@ -95,13 +117,17 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   constexpr int KLD = D + 8;   // LDS row stride of K (halves)
   constexpr int VLD = kKB + 8; // LDS row stride of V^T (halves)
   constexpr int BAND = kBM + kKB - 1;  // bias-table entries per block
-  using St = Staging<D>;
+  using St = Staging<D, F32IN>;
+  using InT = typename std::conditional<F32IN, float, half_t>::type;
+  constexpr int IES = sizeof(InT);  // bytes per input element
   static_assert(St::KCH >= 1 && kKB * D / 8 % kGroup == 0, "K tile split");
 
   // LDS: per key group two block slots, each K [KB][KLD] then V^T [D][VLD]
-  // (halves); reused after the loop for the key-group merge.
+  // (halves), followed for f32 input by the low halves of both; reused
+  // after the loop for the key-group merge.
   constexpr int KHALF = kKB * KLD;
-  constexpr int SLOT = KHALF + D * VLD;
+  constexpr int LO = KHALF + D * VLD;  // offset of the low-half tiles
+  constexpr int SLOT = F32IN ? 2 * LO : LO;
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * 2 * SLOT];
   __shared__ float sBias[KSPLIT][2][BIAS == kBiasTableF32 ? BAND + 1 : 1];
 
@@ -124,9 +150,9 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   const int qw0 = q0 + wave * 32;  // first query of this wave
   const int q = qw0 + ql;          // this lane's query
 
-  const half_t* Qh = p.Q + (int64_t)bh * p.bh_stride_q;
-  const half_t* Kh = p.K + (int64_t)bh * p.bh_stride_kv;
-  const half_t* Vh = p.V + (int64_t)bh * p.bh_stride_kv;
+  const InT* Qh = static_cast<const InT*>(p.Q) + (int64_t)bh * p.bh_stride_q;
+  const InT* Kh = static_cast<const InT*>(p.K) + (int64_t)bh * p.bh_stride_kv;
+  const InT* Vh = static_cast<const InT*>(p.V) + (int64_t)bh * p.bh_stride_kv;
 
   // Softmax constant c = |scale| log2(e) > 0; a negative scale flips Q.
   const bool neg = p.scale_log2 < 0.f;
@@ -135,12 +161,21 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   // Q fragments: B operand of S^T, lane holds Q[q][16*ks + 8*g .. +7].
   // Rows past N read as zeros (buffer bounds check).
   const int qrows = min(N - q0, kBM);
-  const rsrc_t rsQ = make_rsrc(Qh + (int64_t)q0 * p.stride_q, (uint32_t)qrows * p.stride_q * 2);
+  const rsrc_t rsQ = make_rsrc(Qh + (int64_t)q0 * p.stride_q, (uint32_t)qrows * p.stride_q * IES);
   half8v qf[KS];
+  half8v qlo[F32IN ? KS : 1];  // low halves of an f32 Q
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    half8v t = buf_load_half8(rsQ, ((q - q0) * p.stride_q + 16 * ks + 8 * g) * 2);
-    qf[ks] = neg ? -t : t;
+    const uint32_t off = ((q - q0) * p.stride_q + 16 * ks + 8 * g) * IES;
+    if constexpr (F32IN) {
+      float4v f[2] = {__builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rsQ, off, 0, 0)),
+                      __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(rsQ, off + 16, 0, 0))};
+      if (neg) { f[0] = -f[0]; f[1] = -f[1]; }
+      split_f16(f, qf[ks], qlo[ks]);
+    } else {
+      half8v t = buf_load_half8(rsQ, off);
+      qf[ks] = neg ? -t : t;
+    }
   }
 
   // Key blocks this workgroup visits: [blk0, blk0 + nblk); group kg takes
@@ -163,28 +198,36 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
 #pragma unroll
   for (int j = 0; j < St::KCH; ++j) {
     const int c8 = gtid + kGroup * j;
-    k_off[j] = ((c8 / (D / 8)) * p.stride_kv + 8 * (c8 % (D / 8))) * 2;
+    k_off[j] = ((c8 / (D / 8)) * p.stride_kv + 8 * (c8 % (D / 8))) * IES;
   }
   uint32_t v_off[St::VCH];
 #pragma unroll
   for (int j = 0; j < St::VCH; ++j) {
     const int job = min(gtid + kGroup * j, St::VJOBS - 1);
-    v_off[j] = (2 * (job % (kKB / 2)) * p.stride_kv + 8 * (job / (kKB / 2))) * 2;
+    v_off[j] = (2 * (job % (kKB / 2)) * p.stride_kv + 8 * (job / (kKB / 2))) * IES;
   }
   const int kgu = kg;
 
   auto gload = [&](St& st, int i) {
     const int blk = blk0 + max(0, min(kgu + KSPLIT * i, nblk - 1));
     const int kb0 = blk * kKB;
-    const uint32_t bytes = (uint32_t)min(N - kb0, kKB) * p.stride_kv * 2;
+    const uint32_t bytes = (uint32_t)min(N - kb0, kKB) * p.stride_kv * IES;
     const rsrc_t rk = make_rsrc(Kh + (int64_t)kb0 * p.stride_kv, bytes);
     const rsrc_t rv = make_rsrc(Vh + (int64_t)kb0 * p.stride_kv, bytes);
+    auto ld = [&](Piece8<F32IN>& d, rsrc_t r, uint32_t off) {
+      if constexpr (F32IN) {
+        d.f[0] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+        d.f[1] = __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, off + 16, 0, 0));
+      } else {
+        d.h = buf_load_half8(r, off);
+      }
+    };
 #pragma unroll
-    for (int j = 0; j < St::KCH; ++j) st.k[j] = buf_load_half8(rk, k_off[j]);
+    for (int j = 0; j < St::KCH; ++j) ld(st.k[j], rk, k_off[j]);
 #pragma unroll
     for (int j = 0; j < St::VCH; ++j) {
-      st.v[j][0] = buf_load_half8(rv, v_off[j]);
-      st.v[j][1] = buf_load_half8(rv, v_off[j] + p.stride_kv * 2);
+      ld(st.v[j][0], rv, v_off[j]);
+      ld(st.v[j][1], rv, v_off[j] + p.stride_kv * IES);
     }
     if (BIAS == kBiasTableF32) {
       // Band of table[h][q - key + N - 1] for q in [q0, q0+BM), key in
@@ -203,7 +246,15 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
 #pragma unroll
     for (int j = 0; j < St::KCH; ++j) {
       const int c8 = gtid + kGroup * j;
-      *reinterpret_cast<half8v*>(&k_l[(c8 / (D / 8)) * KLD + 8 * (c8 % (D / 8))]) = st.k[j];
+      const int at = (c8 / (D / 8)) * KLD + 8 * (c8 % (D / 8));
+      if constexpr (F32IN) {
+        half8v hi, lo;
+        split_f16(st.k[j].f, hi, lo);
+        *reinterpret_cast<half8v*>(&k_l[at]) = hi;
+        *reinterpret_cast<half8v*>(&k_l[LO + at]) = lo;
+      } else {
+        *reinterpret_cast<half8v*>(&k_l[at]) = st.k[j].h;
+      }
     }
 #pragma unroll
     for (int j = 0; j < St::VCH; ++j) {
@@ -211,10 +262,19 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
       if (St::VJOBS % kGroup == 0 || job < St::VJOBS) {
         const int kp = 2 * (job % (kKB / 2));
         const int col = 8 * (job / (kKB / 2));
+        half8v v0, v1, l0, l1;
+        if constexpr (F32IN) {
+          split_f16(st.v[j][0].f, v0, l0);
+          split_f16(st.v[j][1].f, v1, l1);
+        } else {
+          v0 = st.v[j][0].h;
+          v1 = st.v[j][1].h;
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          half2v pr = {st.v[j][0][e], st.v[j][1][e]};
-          *reinterpret_cast<half2v*>(&v_l[(col + e) * VLD + kp]) = pr;
+          *reinterpret_cast<half2v*>(&v_l[(col + e) * VLD + kp]) = half2v{v0[e], v1[e]};
+          if constexpr (F32IN)
+            *reinterpret_cast<half2v*>(&v_l[LO + (col + e) * VLD + kp]) = half2v{l0[e], l1[e]};
         }
       }
     }
@@ -245,7 +305,14 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
       s[t] = float16v{};
       const half_t* kp = &k_l[(32 * t + krow) * KLD + 8 * g];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) s[t] = mfma32x32x16(load_half8(kp + 16 * ks), qf[ks], s[t]);
+      for (int ks = 0; ks < KS; ++ks) {
+        const half8v kh = load_half8(kp + 16 * ks);
+        s[t] = mfma32x32x16(kh, qf[ks], s[t]);
+        if constexpr (F32IN) {  // + K_hi Q_lo + K_lo Q_hi
+          s[t] = mfma32x32x16(kh, qlo[ks], s[t]);
+          s[t] = mfma32x32x16(load_half8(kp + LO + 16 * ks), qf[ks], s[t]);
+        }
+      }
     }
 
     // ---- logits x (scaled log2 units for bias modes, raw s otherwise) ----
@@ -322,23 +389,36 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
 
     half8v pb[2 * NT];
+    half8v pl[F32IN ? 2 * NT : 1];  // low halves of an f32 P
+    float ls[2 * NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float e = (BIAS != kBiasNone) ? s[t][r] - m_use : __builtin_fmaf(s[t][r], c, -m_use);
-        pb[2 * t + (r >> 3)][r & 7] = (half_t)fast_exp2(e);
+        const float pv = fast_exp2(e);
+        const half_t ph = (half_t)pv;
+        pb[2 * t + (r >> 3)][r & 7] = ph;
+        if constexpr (F32IN) {
+          pl[2 * t + (r >> 3)][r & 7] = (half_t)(pv - (float)ph);
+          if ((r & 7) == 0)
+            ls[2 * t + (r >> 3)] = pv;
+          else
+            ls[2 * t + (r >> 3)] += pv;
+        }
       }
     }
-    // Row sum of the fp16 P that feeds the MFMA (one dot2 chain per chunk).
-    float ls[2 * NT];
+    // Row sum of the P that feeds the MFMA: the f32 P itself for split
+    // input, else the fp16 P (one dot2 chain per chunk).
+    if constexpr (!F32IN) {
 #pragma unroll
-    for (int cc = 0; cc < 2 * NT; ++cc) {
-      const half8v& v8 = pb[cc];
-      float a = __builtin_amdgcn_fdot2(half2v{v8[0], v8[1]}, ones, 0.f, false);
-      a = __builtin_amdgcn_fdot2(half2v{v8[2], v8[3]}, ones, a, false);
-      a = __builtin_amdgcn_fdot2(half2v{v8[4], v8[5]}, ones, a, false);
-      ls[cc] = __builtin_amdgcn_fdot2(half2v{v8[6], v8[7]}, ones, a, false);
+      for (int cc = 0; cc < 2 * NT; ++cc) {
+        const half8v& v8 = pb[cc];
+        float a = __builtin_amdgcn_fdot2(half2v{v8[0], v8[1]}, ones, 0.f, false);
+        a = __builtin_amdgcn_fdot2(half2v{v8[2], v8[3]}, ones, a, false);
+        a = __builtin_amdgcn_fdot2(half2v{v8[4], v8[5]}, ones, a, false);
+        ls[cc] = __builtin_amdgcn_fdot2(half2v{v8[6], v8[7]}, ones, a, false);
+      }
     }
 #pragma unroll
     for (int w = 1; w < 2 * NT; w *= 2)
@@ -351,7 +431,14 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     for (int u = 0; u < DT; ++u) {
       const half_t* vp = &v_l[(32 * u + ql) * VLD + 8 * g];
 #pragma unroll
-      for (int cc = 0; cc < 2 * NT; ++cc) o[u] = mfma32x32x16(load_half8(vp + 16 * cc), pb[cc], o[u]);
+      for (int cc = 0; cc < 2 * NT; ++cc) {
+        const half8v vh = load_half8(vp + 16 * cc);
+        o[u] = mfma32x32x16(vh, pb[cc], o[u]);
+        if constexpr (F32IN) {  // + V_hi P_lo + V_lo P_hi
+          o[u] = mfma32x32x16(vh, pl[cc], o[u]);
+          o[u] = mfma32x32x16(load_half8(vp + LO + 16 * cc), pb[cc], o[u]);
+        }
+      }
     }
   };
 
@@ -440,32 +527,32 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
 }
 
 // Static LDS of one workgroup with K key groups.
-template <int D, int BIAS>
+template <int D, int BIAS, bool F32IN>
 constexpr int fa2_lds_bytes(int K) {
   constexpr int kb = key_block<D>();
-  const int slot = (kb * (D + 8) + D * (kb + 8)) * 2;
+  const int slot = (kb * (D + 8) + D * (kb + 8)) * 2 * (F32IN ? 2 : 1);
   const int bias = BIAS == kBiasTableF32 ? (kBM + kb) * 4 : 4;
   return K * 2 * (slot + bias);
 }
 
-template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int K>
+template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int K, bool F32IN>
 bool launch_fa2_k(const Fa2Args& a, hipStream_t stream) {
-  if constexpr (fa2_lds_bytes<D, BIAS>(K) <= 160 * 1024) {
-    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, K>),
+  if constexpr (fa2_lds_bytes<D, BIAS, F32IN>(K) <= 160 * 1024) {
+    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, K, F32IN>),
                        dim3(a.num_qblocks * a.batch_heads), dim3(K * kGroup), 0, stream, a);
     return true;
   }
   return false;
 }
 
-template <int D, bool CAUSAL, int BIAS, bool OUT_F16>
+template <int D, bool CAUSAL, int BIAS, bool OUT_F16, bool F32IN = false>
 hipError_t launch_fa2_t(const Fa2Args& a, int ksplit, hipStream_t stream) {
   // Use the requested key split, or the largest smaller one whose LDS fits.
   bool done = false;
-  if (ksplit >= 4) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 4>(a, stream);
-  if (!done && ksplit >= 3) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 3>(a, stream);
-  if (!done && ksplit >= 2) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 2>(a, stream);
-  if (!done) launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 1>(a, stream);
+  if (ksplit >= 4) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 4, F32IN>(a, stream);
+  if (!done && ksplit >= 3) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 3, F32IN>(a, stream);
+  if (!done && ksplit >= 2) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 2, F32IN>(a, stream);
+  if (!done) launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 1, F32IN>(a, stream);
   return hipGetLastError();
 }
 
@@ -477,6 +564,19 @@ hipError_t launch_fa2_c(const Fa2Args& a, bool causal, int ksplit, hipStream_t s
     if (causal) return hipErrorInvalidValue;  // the biased entry point is never causal
   }
   return launch_fa2_t<D, false, BIAS, OUT_F16>(a, ksplit, s);
+}
+
+// f32 Q/K/V (split into f16 hi + lo), no bias, f32 output, d <= 64.
+hipError_t launch_fa2_f32in(const Fa2Args& a, int d, bool causal, int ksplit, hipStream_t s) {
+  switch (d) {
+    case 32:
+      return causal ? launch_fa2_t<32, true, kBiasNone, false, true>(a, ksplit, s)
+                    : launch_fa2_t<32, false, kBiasNone, false, true>(a, ksplit, s);
+    case 64:
+      return causal ? launch_fa2_t<64, true, kBiasNone, false, true>(a, ksplit, s)
+                    : launch_fa2_t<64, false, kBiasNone, false, true>(a, ksplit, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 template <int BIAS, bool OUT_F16>
@@ -494,12 +594,16 @@ hipError_t launch_fa2_d(const Fa2Args& a, int d, bool causal, int ksplit, hipStr
 int fa2_query_block() { return kBM; }
 
 hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool out_f16,
-                      hipStream_t stream) {
+                      hipStream_t stream, bool in_f32) {
   a.num_qblocks = (a.N + kBM - 1) / kBM;
   // Split the keys of a workgroup over two wave groups when the grid alone
   // gives fewer than two workgroups per compute unit.
   const int64_t wgs = (int64_t)a.num_qblocks * a.batch_heads;
   const int ksplit = (a.ksplit > 0) ? a.ksplit : (wgs < 2 * (int64_t)device_cu_count() ? 2 : 1);
+  if (in_f32) {
+    if (bias_kind != kBiasNone || out_f16) return hipErrorInvalidValue;
+    return launch_fa2_f32in(a, head_dim, causal, ksplit, stream);
+  }
   if (bias_kind == kBiasNone) {
     return out_f16 ? launch_fa2_d<kBiasNone, true>(a, head_dim, causal, ksplit, stream)
                    : launch_fa2_d<kBiasNone, false>(a, head_dim, causal, ksplit, stream);

@@ -7,6 +7,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include "../../include/neso_amd.h"
@@ -73,6 +74,25 @@ const char kManifest[] = R"JSON({
       {"index": 12, "name": "causal", "type": "int32", "is_pointer": false},
       {"index": 13, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
      "threadgroup_size": 256, "block_m": 128, "block_n": 64, "head_dims": [32, 64, 128],
+     "grid": ["cdiv(N, 128) * batch_heads", "1", "1"]},
+    {"name": "neso_flash_attention_f32_fwd", "replaces": "flash_attention_fwd with qkv_dtype='f32' (tests/test_flash_attention.py:79-89,250-290)",
+     "params": [
+      {"index": 0, "name": "Q", "type": "const fp32*", "is_pointer": true},
+      {"index": 1, "name": "K", "type": "const fp32*", "is_pointer": true},
+      {"index": 2, "name": "V", "type": "const fp32*", "is_pointer": true},
+      {"index": 3, "name": "O", "type": "fp32*", "is_pointer": true},
+      {"index": 4, "name": "N", "type": "int32", "is_pointer": false},
+      {"index": 5, "name": "stride_qo", "type": "int32", "is_pointer": false},
+      {"index": 6, "name": "stride_kv", "type": "int32", "is_pointer": false},
+      {"index": 7, "name": "scale", "type": "fp32", "is_pointer": false},
+      {"index": 8, "name": "head_dim", "type": "int32", "is_pointer": false},
+      {"index": 9, "name": "batch_heads", "type": "int32", "is_pointer": false},
+      {"index": 10, "name": "stride_bh_qo", "type": "int64", "is_pointer": false},
+      {"index": 11, "name": "stride_bh_kv", "type": "int64", "is_pointer": false},
+      {"index": 12, "name": "causal", "type": "int32", "is_pointer": false},
+      {"index": 13, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
+     "threadgroup_size": 256, "block_m": 128, "head_dims": [32, 64],
+     "precision": "f32 inputs split into f16 hi + lo, three f16 MFMAs per product, f32 accumulation",
      "grid": ["cdiv(N, 128) * batch_heads", "1", "1"]},
     {"name": "neso_flash_attention_window_fwd", "replaces": "flash_attention_fwd with window_left/right (debug/fa2_correctness_legacy.py:92-102)",
      "params": [
@@ -161,22 +181,33 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
                int32_t stride_q, int32_t stride_kv, int32_t stride_o, float scale,
                int32_t head_dim, int32_t heads, int64_t bh_q, int64_t bh_kv, int64_t bh_o,
                int64_t bias_stride_h, int causal, int bias_kind, bool out_f16, void* stream,
-               const char* name, int32_t win_left = -1, int32_t win_right = -1) {
+               const char* name, int32_t win_left = -1, int32_t win_right = -1,
+               bool in_f32 = false) {
   if (!Q || !K || !V || !O) return fail(NESO_EINVAL, "%s: null tensor pointer", name);
   if (N < 0) return fail(NESO_EINVAL, "%s: N=%d < 0", name, N);
   if (heads < 0) return fail(NESO_EINVAL, "%s: batch_heads=%d < 0", name, heads);
   int st = check_head_dim(head_dim);
   if (st != NESO_OK) return st;
+  if (in_f32 && head_dim > 64)
+    return fail(NESO_EUNSUPPORTED, "%s: f32 Q/K/V supports head_dim 32 and 64, got %d", name,
+                head_dim);
   if (!isfinite(scale)) return fail(NESO_EINVAL, "%s: scale is not finite", name);
   if (causal != 0 && causal != 1) return fail(NESO_EINVAL, "%s: causal=%d", name, causal);
   if (stride_q < head_dim || stride_kv < head_dim || stride_o < head_dim)
     return fail(NESO_EINVAL, "%s: row stride smaller than head_dim %d", name, head_dim);
-  if (stride_q % 8 || stride_kv % 8 || stride_o % 4)
-    return fail(NESO_EINVAL, "%s: row strides must be multiples of 8 elements", name);
-  if (bh_q % 8 || bh_kv % 8 || bh_o % 4 || bh_q < 0 || bh_kv < 0 || bh_o < 0)
-    return fail(NESO_EINVAL, "%s: head strides must be non-negative multiples of 8", name);
+  // Q/K/V rows are read in 16-byte pieces: 8 f16 or 4 f32 elements.
+  const int in_mult = in_f32 ? 4 : 8;
+  if (stride_q % in_mult || stride_kv % in_mult || stride_o % 4)
+    return fail(NESO_EINVAL, "%s: row strides must be multiples of %d elements", name, in_mult);
+  if (bh_q % in_mult || bh_kv % in_mult || bh_o % 4 || bh_q < 0 || bh_kv < 0 || bh_o < 0)
+    return fail(NESO_EINVAL, "%s: head strides must be non-negative multiples of %d", name,
+                in_mult);
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V) || !aligned16(O))
     return fail(NESO_EINVAL, "%s: Q/K/V/O must be 16-byte aligned", name);
+  // A block of 128 rows is addressed with 32-bit byte offsets.
+  const int64_t max_stride = std::max({(int64_t)stride_q, (int64_t)stride_kv, (int64_t)stride_o});
+  if (max_stride * neso::fa2_query_block() * 4 >= (int64_t)1 << 32)
+    return fail(NESO_EUNSUPPORTED, "%s: row stride %lld too large", name, (long long)max_stride);
   if (bias_kind != neso::kBiasNone) {
     if (!bias) return fail(NESO_EINVAL, "%s: null bias pointer", name);
     if (bias_stride_h < 0) return fail(NESO_EINVAL, "%s: bias_stride_h < 0", name);
@@ -190,9 +221,9 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
     return fail(NESO_EUNSUPPORTED, "%s: grid too large", name);
 
   neso::Fa2Args a{};
-  a.Q = static_cast<const neso::half_t*>(Q);
-  a.K = static_cast<const neso::half_t*>(K);
-  a.V = static_cast<const neso::half_t*>(V);
+  a.Q = Q;
+  a.K = K;
+  a.V = V;
   a.O = O;
   a.bias = bias;
   a.N = N;
@@ -210,7 +241,7 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
   a.win_left = win_left < 0 ? N : (win_left < N ? win_left : N);
   a.win_right = win_right < 0 ? 0 : (win_right < N ? win_right : N);
   return launched(neso::launch_fa2(a, head_dim, causal != 0, bias_kind, out_f16,
-                                   static_cast<hipStream_t>(stream)),
+                                   static_cast<hipStream_t>(stream), in_f32),
                   name);
 }
 
@@ -262,6 +293,15 @@ int neso_flash_attention_fwd(const void* Q, const void* K, const void* V, float*
   return fa2_common(Q, K, V, O, nullptr, N, stride_qo, stride_kv, stride_qo, scale, head_dim,
                     batch_heads, stride_bh_qo, stride_bh_kv, stride_bh_qo, 0, causal,
                     neso::kBiasNone, false, stream, "flash_attention_fwd");
+}
+
+int neso_flash_attention_f32_fwd(const float* Q, const float* K, const float* V, float* O,
+                                 int32_t N, int32_t stride_qo, int32_t stride_kv, float scale,
+                                 int32_t head_dim, int32_t batch_heads, int64_t stride_bh_qo,
+                                 int64_t stride_bh_kv, int32_t causal, void* stream) {
+  return fa2_common(Q, K, V, O, nullptr, N, stride_qo, stride_kv, stride_qo, scale, head_dim,
+                    batch_heads, stride_bh_qo, stride_bh_kv, stride_bh_qo, 0, causal,
+                    neso::kBiasNone, false, stream, "flash_attention_f32_fwd", -1, -1, true);
 }
 
 int neso_flash_attention_window_fwd(const void* Q, const void* K, const void* V, void* O,

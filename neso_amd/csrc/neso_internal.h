@@ -13,9 +13,9 @@ namespace neso {
 enum BiasKind { kBiasNone = 0, kBiasTableF32 = 1, kBiasDenseF16 = 2 };
 
 struct Fa2Args {
-  const half_t* Q;
-  const half_t* K;
-  const half_t* V;
+  const void* Q;        // f16, or f32 for the f32-input kernels
+  const void* K;
+  const void* V;
   void* O;              // f32 or f16, [batch_heads][N][stride_o]
   const void* bias;     // table f32 [h][2N-1] or dense f16 [h][N][N]
   int32_t N;            // queries == keys per (batch, head)
@@ -41,7 +41,7 @@ int device_cu_count();
 
 int fa2_query_block();
 hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool out_f16,
-                      hipStream_t stream);
+                      hipStream_t stream, bool in_f32 = false);
 
 // Y[M][N] (f16, row stride ldy) = X[M][K] (f16, row stride ldx) * dequant(W)^T
 // with W packed 8 int4 codes per int32 along K ([N][K/8]), scales f16

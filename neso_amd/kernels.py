@@ -68,23 +68,30 @@ def _stream(stream: Any, *tensors: Any) -> int:
 def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scale: float, *,
                         head_dim: int | None = None, batch_heads: int = 1,
                         stride_bh_qo: int = 0, stride_bh_kv: int = 0, causal: bool = False,
-                        stream=None) -> None:
+                        qkv_dtype: str | None = None, stream=None) -> None:
     """FA2 forward, O = softmax(Q K^T * scale) V.
 
     Positional arguments as the reference kernel (tests/test_flash_attention.py
-    :149-153): Q, K, V fp16 [N, d] rows, O fp32 rows with row stride
+    :149-153): Q, K, V [N, d] rows, O fp32 rows with row stride
     ``stride_qo``, N, stride_qo, stride_kv (elements), scale.  Keyword
     extensions: ``head_dim`` (inferred from ``Q.shape[-1]`` for tensors),
     ``batch_heads`` with ``stride_bh_qo`` / ``stride_bh_kv`` for B*H slices
-    in one launch, and ``causal``.
+    in one launch, and ``causal``.  ``qkv_dtype`` is 'f16' or 'f32' as in
+    the reference's generator (:79-89); for tensors it follows Q's dtype.
     """
     if head_dim is None:
         if not isinstance(Q, torch.Tensor):
             raise ValueError("head_dim is required when Q is a raw address")
         head_dim = int(Q.shape[-1])
+    if qkv_dtype is None:
+        qkv_dtype = "f32" if isinstance(Q, torch.Tensor) and Q.dtype == torch.float32 else "f16"
+    if qkv_dtype not in ("f16", "f32"):
+        raise ValueError(f"qkv_dtype must be 'f16' or 'f32', got {qkv_dtype!r}")
     lib = _lib.load()
-    st = lib.neso_flash_attention_fwd(
-        _ptr(Q, "Q", torch.float16), _ptr(K, "K", torch.float16), _ptr(V, "V", torch.float16),
+    dt = torch.float32 if qkv_dtype == "f32" else torch.float16
+    fn = lib.neso_flash_attention_f32_fwd if qkv_dtype == "f32" else lib.neso_flash_attention_fwd
+    st = fn(
+        _ptr(Q, "Q", dt), _ptr(K, "K", dt), _ptr(V, "V", dt),
         _ptr(O, "O", torch.float32), int(N), int(stride_qo), int(stride_kv), float(scale),
         int(head_dim), int(batch_heads), int(stride_bh_qo), int(stride_bh_kv), int(bool(causal)),
         _stream(stream, Q, O))
@@ -209,11 +216,14 @@ def launch(name: str, *args, **kwargs) -> None:
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = False,
               scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
-    """FA2 forward over [..., N, d] fp16 tensors (contiguous); returns fp32 [..., N, d]."""
+    """FA2 forward over [..., N, d] fp16 or fp32 tensors (contiguous, one
+    dtype); returns fp32 [..., N, d]."""
     if q.shape != k.shape or q.shape != v.shape:
         raise ValueError("q, k, v must have the same shape [..., N, d]")
     if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
         raise ValueError("q, k, v must be contiguous")
+    if not q.dtype == k.dtype == v.dtype:
+        raise TypeError("q, k, v must share one dtype")
     n, d = int(q.shape[-2]), int(q.shape[-1])
     bh = q.numel() // max(n * d, 1) if n * d else 0
     if out is None:

@@ -101,6 +101,26 @@ def test_fa2_validation(lib, kw, status):
         assert lib.neso_last_error()
 
 
+def fa2_f32(lib, **kw):
+    args = dict(Q=A16, K=A16, V=A16, O=A16, N=0, stride_qo=64, stride_kv=64, scale=0.125,
+                head_dim=64, batch_heads=1, stride_bh_qo=0, stride_bh_kv=0, causal=0, stream=None)
+    args.update(kw)
+    return lib.neso_flash_attention_f32_fwd(*args.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(head_dim=128, stride_qo=128, stride_kv=128), _lib.NESO_EUNSUPPORTED),
+    (dict(stride_qo=66), _lib.NESO_EINVAL),          # f32 rows need multiples of 4
+    (dict(stride_qo=68, stride_kv=68), _lib.NESO_OK),  # ... not of 8
+    (dict(stride_bh_kv=6), _lib.NESO_EINVAL),
+    (dict(V=A16 + 4), _lib.NESO_EINVAL),
+    (dict(stride_qo=1 << 24), _lib.NESO_EUNSUPPORTED),  # 128-row block exceeds 32-bit offsets
+    (dict(head_dim=32, stride_qo=32, stride_kv=32), _lib.NESO_OK),
+])
+def test_fa2_f32_validation(lib, kw, status):
+    assert fa2_f32(lib, **kw) == status
+
+
 def relpos(lib, **kw):
     args = dict(Q=A16, K=A16, V=A16, bias=A16, O=A16, T=0, stride=64, scale=0.125, stride_h=0,
                 bias_stride_h=0, num_heads=1, head_dim=64, bias_mode=1, out_dtype=1, stream=None)
