@@ -64,13 +64,30 @@ def log(msg):
 GRAPH_LAUNCHES = 16
 
 
+# Seconds the GPU is kept busy with the timed workload before each
+# measurement.  An idle MI355X starts a burst of kernels at 1.5-1.7 GHz and
+# reaches its sustained ~2.2 GHz only after tens of milliseconds of load;
+# without this the first cases would be timed at the idle clock.
+CLOCK_RAMP_S = 0.3
+
+
+def ramp_clock(run_once, torch, seconds=CLOCK_RAMP_S):
+    """Repeat ``run_once()`` (asynchronous GPU work) for ``seconds`` of wall time."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            run_once()
+        torch.cuda.synchronize()
+
+
 def time_launches(launch, steps, warmup, torch, per_graph=GRAPH_LAUNCHES):
     """ms per launch of ``launch(i)``, replayed from a HIP graph.
 
     ``per_graph`` consecutive launches (i = 0 .. per_graph-1) are captured
     once; the graph is replayed ceil(steps / per_graph) times between two
     events recorded on the current stream, which is the stream the replays
-    run on.  ``warmup`` launches run eagerly first (and compile nothing).
+    run on.  ``warmup`` launches run eagerly first (and compile nothing),
+    then the graph is replayed for CLOCK_RAMP_S seconds (untimed).
     """
     for i in range(warmup):
         launch(i % per_graph)
@@ -81,6 +98,7 @@ def time_launches(launch, steps, warmup, torch, per_graph=GRAPH_LAUNCHES):
             launch(i)
     graph.replay()
     torch.cuda.synchronize()
+    ramp_clock(graph.replay, torch)
     replays = max(1, -(-steps // per_graph))
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -96,6 +114,7 @@ def time_eager(launch, steps, torch):
     """ms per launch when launched one by one from Python (host-bound for short kernels)."""
     launch(0)
     torch.cuda.synchronize()
+    ramp_clock(lambda: launch(0), torch, CLOCK_RAMP_S / 3)
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()

@@ -22,7 +22,7 @@ BUILD_DIR = PKG / "_build"
 LIB_PATH = PKG / "libneso_amd.so"
 ARCH = "gfx950"
 
-SOURCES = ["neso_abi.hip", "fa2_fwd.hip", "qmatmul.hip"]
+SOURCES = ["neso_abi.hip", "fa2_fwd.hip", "fa2_fast.hip", "qmatmul.hip"]
 
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -1,0 +1,549 @@
+// Flash-Attention-2 forward for fp16 Q/K/V without a bias: the fast path.
+//
+// Same algorithm and result as fa2_fwd_kernel (reference: the TTIR loop of
+// `flash_attention_fwd`, tests/test_flash_attention.py:79-247; final
+// O / max(l, 1e-6), src/neso/backend/codegen/lowering.py:4352-4353), with the
+// per-score work cut to what the transcendental unit and the P conversion
+// need.  Tile layout as in fa2_fwd.hip: a key group is 4 waves and 128
+// queries, each wave owns 32 queries, scores are computed transposed
+// (S^T = K Q^T, v_mfma_f32_32x32x16_f16) so that lane l holds 32 keys of query
+// l % 32 and exp(S^T) in fp16 is directly the B operand of O^T = V^T P^T.
+//
+// What differs:
+// * No row max per block.  The running max m only has to keep p = 2^(c s - m)
+//   (c = |scale| log2(e)) in fp16 range, not equal the row max, so each lane
+//   compares the sum of its 32 fp16 P values (needed for l anyway, from
+//   v_dot2_f32_f16) with 2^12.  A block over the bound, a row's first
+//   visible block and every block with masked keys take the slow path:
+//   exact row max, m raised to it, O and l rescaled, P redone.  As m only
+//   rises and starts at a row's first block max, l >= 1 once a row has seen
+//   a key, so p cannot underflow the whole row.  A score then costs one FMA,
+//   one v_exp_f32, half a v_cvt_pk_f16_f32 and half a v_dot2_f32_f16.
+// * Software pipeline: block i+1's scores (MFMA) are issued in the same
+//   straight-line stretch as block i's softmax (VALU), so the matrix unit and
+//   the VALU work at the same time inside one wave; two waves per SIMD (two
+//   key groups) fill the remaining gaps.  K and V^T of a block share one
+//   slot of a 3-slot LDS ring, which leaves one barrier per block and keeps
+//   block i's K in LDS while block i is processed (the slow path recomputes
+//   its scores from there); global loads run one block ahead of the LDS
+//   stores through registers.
+#include "common.h"
+#include "fa2_tiles.h"
+#include "neso_internal.h"
+
+namespace neso {
+
+namespace {
+
+constexpr int kBM = 128;          // queries per workgroup
+constexpr int kKB = 64;           // keys per block
+constexpr int kGroup = 256;       // threads per key group (4 waves)
+constexpr float kPSumMax = 4096.f;  // fast-path bound on a lane's block sum of P
+
+template <int D>
+struct FastStage {
+  static constexpr int KCH = kKB * D / 8 / kGroup;   // 8-element K pieces per thread
+  static constexpr int VCH = kKB * D / 16 / kGroup;  // (key pair, 8 columns) V jobs
+  half8v k[KCH];
+  half8v v[VCH][2];
+};
+
+// LDS halves of one key group: a 4-slot ring, each slot K [KB][D+8] then
+// V^T [D][KB+8].
+constexpr int kSlots = 4;
+template <int D>
+constexpr int fast_group_lds_halves() {
+  return kSlots * (kKB * (D + 8) + D * (kKB + 8));
+}
+
+template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT>
+__global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
+  constexpr int NT = kKB / 32;  // 32-key tiles per block
+  constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
+  constexpr int DT = D / 32;    // 32-row tiles of O^T
+  constexpr int KLD = D + 8;    // LDS row stride of K (halves)
+  constexpr int VLD = kKB + 8;  // LDS row stride of V^T (halves)
+  constexpr int KSLOT = kKB * KLD;
+  constexpr int VSLOT = D * VLD;
+  constexpr int GLDS = fast_group_lds_halves<D>();
+  using St = FastStage<D>;
+  static_assert(St::KCH >= 1 && St::VCH >= 1 && kKB * D % (8 * kGroup) == 0 &&
+                    kKB * D % (16 * kGroup) == 0,
+                "tile split");
+  __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
+
+  const int tid = threadIdx.x;
+  const int kg = __builtin_amdgcn_readfirstlane(tid / kGroup);  // key group
+  const int gtid = tid % kGroup;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(gtid >> 6);  // query slice (0..3)
+  const int g = lane >> 5;
+  const int ql = lane & 31;
+
+  const uint32_t wg = xcd_swizzle(blockIdx.x, gridDim.x);
+  const int bh = wg / p.num_qblocks;
+  int qblk = wg % p.num_qblocks;
+  if (CAUSAL) qblk = p.num_qblocks - 1 - qblk;  // longest rows first
+  const int N = p.N;
+  const int q0 = qblk * kBM;
+  const int qw0 = q0 + wave * 32;
+  const int q = qw0 + ql;
+
+  const half_t* Qh = static_cast<const half_t*>(p.Q) + (int64_t)bh * p.bh_stride_q;
+  const half_t* Kh = static_cast<const half_t*>(p.K) + (int64_t)bh * p.bh_stride_kv;
+  const half_t* Vh = static_cast<const half_t*>(p.V) + (int64_t)bh * p.bh_stride_kv;
+
+  // Q fragments (B operand of S^T); a negative scale flips Q so that
+  // c = |scale| log2(e) > 0 (kept above 0 so that -inf * c stays -inf).
+  // Rows past N read as zeros.
+  const bool neg = p.scale_log2 < 0.f;
+  const float c = fmaxf(fabsf(p.scale_log2), 1.17549435e-38f);
+  const int qrows = min(N - q0, kBM);
+  const rsrc_t rsQ = make_rsrc(Qh + (int64_t)q0 * p.stride_q, (uint32_t)qrows * p.stride_q * 2);
+  half8v qf[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) {
+    const half8v t = buf_load_half8(rsQ, ((q - q0) * p.stride_q + 16 * ks + 8 * g) * 2);
+    qf[ks] = neg ? -t : t;
+  }
+
+  // Key blocks of this workgroup: [blk0, blk0 + nblk); group kg takes blocks
+  // blk0 + kg + KSPLIT*i.  Masked kernels visit the keys of their queries'
+  // windows [q - wl, q + wr] only.
+  const int wl = p.win_left, wr = p.win_right;
+  const int kbeg = CAUSAL ? max(0, q0 - wl) : 0;
+  const int kend = CAUSAL ? (int)min((int64_t)N, (int64_t)q0 + kBM + wr) : N;
+  const int blk0 = kbeg / kKB;
+  const int nblk = max(0, (kend + kKB - 1) / kKB - blk0);
+  const int my_n = nblk > kg ? (nblk - kg + KSPLIT - 1) / KSPLIT : 0;
+  const int iters = (nblk + KSPLIT - 1) / KSPLIT;  // uniform over the workgroup
+
+  uint32_t k_off[St::KCH];
+#pragma unroll
+  for (int j = 0; j < St::KCH; ++j) {
+    const int c8 = gtid + kGroup * j;
+    k_off[j] = ((c8 / (D / 8)) * p.stride_kv + 8 * (c8 % (D / 8))) * 2;
+  }
+  uint32_t v_off[St::VCH];
+#pragma unroll
+  for (int j = 0; j < St::VCH; ++j) {
+    const int job = gtid + kGroup * j;
+    v_off[j] = (2 * (job % (kKB / 2)) * p.stride_kv + 8 * (job / (kKB / 2))) * 2;
+  }
+
+  // Global -> registers.  Steps past the group's last block reload that
+  // block, so every step issues the same loads (the compiler's load counter
+  // stays exact) and a late store rewrites a slot with the data it already
+  // holds: the last block's V^T stays valid for the P V after the loop.
+  auto gload = [&](St& st, int i) {
+    const int blk = blk0 + kg + KSPLIT * max(0, min(i, my_n - 1));
+    const int kb0 = blk * kKB;
+    // readfirstlane: min/max of scalars may be formed on the VALU, and a
+    // descriptor in VGPRs would wrap every load in a waterfall loop.
+    const uint32_t bytes = __builtin_amdgcn_readfirstlane(max(0, min(N - kb0, kKB)) * p.stride_kv * 2);
+    const rsrc_t rk = make_rsrc(Kh + (int64_t)kb0 * p.stride_kv, bytes);
+    const rsrc_t rv = make_rsrc(Vh + (int64_t)kb0 * p.stride_kv, bytes);
+#pragma unroll
+    for (int j = 0; j < St::KCH; ++j) st.k[j] = buf_load_half8(rk, k_off[j]);
+#pragma unroll
+    for (int j = 0; j < St::VCH; ++j) {
+      st.v[j][0] = buf_load_half8(rv, v_off[j]);
+      st.v[j][1] = buf_load_half8(rv, v_off[j] + p.stride_kv * 2);
+    }
+  };
+
+  St st;  // one block in flight between global memory and LDS
+  half_t* gbase = &smem[kg * GLDS];
+  auto kslot = [&](int s) { return gbase + s * (KSLOT + VSLOT); };
+  auto vslot = [&](int s) { return gbase + s * (KSLOT + VSLOT) + KSLOT; };
+
+  // Registers -> LDS: K row-major [key][KLD], V transposed [d][VLD] as
+  // 32-bit key pairs.  Split in pieces so that the fused step can spread
+  // them over its MFMA slots: piece 0 stores K, pieces 1..4 a quarter of the
+  // V^T pairs each.
+  constexpr int kStorePieces = 5;
+  auto sstore_piece = [&](const St& st, half_t* k_l, half_t* v_l, int piece) {
+    if (piece == 0) {
+#pragma unroll
+      for (int j = 0; j < St::KCH; ++j) {
+        const int c8 = gtid + kGroup * j;
+        *reinterpret_cast<half8v*>(&k_l[(c8 / (D / 8)) * KLD + 8 * (c8 % (D / 8))]) = st.k[j];
+      }
+      return;
+    }
+#pragma unroll
+    for (int j = 0; j < St::VCH; ++j) {
+      const int job = gtid + kGroup * j;
+      const int kp = 2 * (job % (kKB / 2));
+      const int col = 8 * (job / (kKB / 2));
+#pragma unroll
+      for (int e = 2 * (piece - 1); e < 2 * piece; ++e)
+        *reinterpret_cast<half2v*>(&v_l[(col + e) * VLD + kp]) =
+            half2v{st.v[j][0][e], st.v[j][1][e]};
+    }
+  };
+  auto sstore = [&](const St& st, half_t* k_l, half_t* v_l) {
+#pragma unroll
+    for (int piece = 0; piece < kStorePieces; ++piece) sstore_piece(st, k_l, v_l, piece);
+  };
+
+  float m_run = -INFINITY;  // running max (log2 units); -inf: the row has seen no key yet
+  float m_use = 0.f;        // value subtracted from c*s (m_run once finite)
+  float thr = -1.f;         // fast-path bound on the lane's P sum; -1 forces the slow path
+  float l_run = 0.f;        // this lane's partial row sum
+  float16v o[DT];
+#pragma unroll
+  for (int u = 0; u < DT; ++u) o[u] = float16v{};
+  const int krow = kRowPerm(ql);
+  const half2v ones = {(half_t)1.f, (half_t)1.f};
+
+  auto qk = [&](float16v(&s)[NT], const half_t* k_l) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const half_t* kp = &k_l[(32 * t + krow) * KLD + 8 * g];
+      s[t] = mfma32x32x16(load_half8(kp), qf[0], float16v{});
+#pragma unroll
+      for (int ks = 1; ks < KS; ++ks) s[t] = mfma32x32x16(load_half8(kp + 16 * ks), qf[ks], s[t]);
+    }
+  };
+
+  // P = 2^s in fp16 (the B operand of the P V product) and the lane's sum
+  // of that fp16 P.
+  auto expsum = [&](const float16v(&s)[NT], half8v(&pb)[2 * NT]) {
+    float ls[2 * NT];
+#pragma unroll
+    for (int cc = 0; cc < 2 * NT; ++cc) {
+      const float16v& v = s[cc >> 1];
+      const int o8 = 8 * (cc & 1);
+      float a = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const half2v h = {(half_t)fast_exp2(__builtin_fmaf(v[o8 + e], c, -m_use)),
+                          (half_t)fast_exp2(__builtin_fmaf(v[o8 + e + 1], c, -m_use))};
+        pb[cc][e] = h[0];
+        pb[cc][e + 1] = h[1];
+        a = __builtin_amdgcn_fdot2(h, ones, a, false);
+      }
+      ls[cc] = a;
+    }
+#pragma unroll
+    for (int w = 1; w < 2 * NT; w *= 2)
+#pragma unroll
+      for (int cc = 0; cc + w < 2 * NT; cc += 2 * w) ls[cc] += ls[cc + w];
+    return ls[0];
+  };
+
+  // acc += h.x + h.y (v_dot2_f32_f16).
+  auto dot2_acc = [&](float& acc, half2v h) { acc = __builtin_amdgcn_fdot2(h, ones, acc, false); };
+
+  // The common step, one straight-line stretch per block i: the scores of
+  // block i+1 (KS*NT MFMAs, K from slot k_l), the P V product of block i-1
+  // (DT*2NT MFMAs, V^T from slot v_l, P in pprev) and the softmax of block
+  // i (scores s -> P in pcur, VALU).  MFMA slots alternate score and P V
+  // products, so each accumulator chain has three other MFMAs between its
+  // steps; fragments are read AHEAD slots early; every slot carries the
+  // VALU work of SPJ scores, staggered (fma of slot j+1, exp of slot j,
+  // cvt + dot2 of slot j-1) so that no VALU op waits on the one before it.
+  // sched_barrier pins that order.  Returns the lane's sum of fp16 pcur.
+  auto fused = [&](const float16v(&s)[NT], float16v(&sn)[NT], const half_t* k_l,
+                   const half_t* v_l, const half8v(&pprev)[2 * NT], half8v(&pcur)[2 * NT],
+                   int i) {
+    constexpr int NQ = KS * NT;       // score MFMAs
+    constexpr int NP = DT * 2 * NT;   // P V MFMAs
+    constexpr int NJ = NQ + NP;       // slots
+    constexpr int SPJ = 32 / NJ;      // scores per slot
+    constexpr int AHEAD = 4;
+    static_assert(NQ == NP && 32 % NJ == 0 && SPJ == 2, "slot split");
+    const half_t* kp = &k_l[krow * KLD + 8 * g];
+    const half_t* vp = &v_l[ql * VLD + 8 * g];
+    // Fragment of slot j: even j -> K (tile q % NT, k-step q / NT),
+    // odd j -> V^T (tile q % DT, key chunk q / DT), q = j / 2.
+    auto frag = [&](int j) {
+      const int q = j / 2;
+      return (j % 2 == 0) ? load_half8(kp + 32 * (q % NT) * KLD + 16 * (q / NT))
+                          : load_half8(vp + 32 * (q % DT) * VLD + 16 * (q / DT));
+    };
+    auto score = [&](int sc) {  // score sc (0..31) of this lane
+      const int cc = sc / 8;
+      return s[cc >> 1][8 * (cc & 1) + sc % 8];
+    };
+    half8v fr[NJ];
+#pragma unroll
+    for (int j = 0; j < AHEAD; ++j) fr[j] = frag(j);
+    float acc[2 * NT];
+#pragma unroll
+    for (int cc = 0; cc < 2 * NT; ++cc) acc[cc] = 0.f;
+    float ev[NJ][2], pv[NJ][2];
+    ev[0][0] = __builtin_fmaf(score(0), c, -m_use);
+    ev[0][1] = __builtin_fmaf(score(1), c, -m_use);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int q = j / 2;
+      if (j % 2 == 0) {
+        const int t = q % NT, ks = q / NT;
+        sn[t] = mfma32x32x16(fr[j], qf[ks], ks == 0 ? float16v{} : sn[t]);
+      } else {
+        const int u = q % DT, cc = q / DT;
+        o[u] = mfma32x32x16(fr[j], pprev[cc], o[u]);
+      }
+      if (j + AHEAD < NJ) fr[j + AHEAD] = frag(j + AHEAD);
+      if (j + 1 < NJ) {
+        ev[j + 1][0] = __builtin_fmaf(score(2 * j + 2), c, -m_use);
+        ev[j + 1][1] = __builtin_fmaf(score(2 * j + 3), c, -m_use);
+      }
+      pv[j][0] = fast_exp2(ev[j][0]);
+      pv[j][1] = fast_exp2(ev[j][1]);
+      if (j >= 1) {
+        const int sc = 2 * (j - 1), cc = sc / 8, e = sc % 8;
+        const half2v h = {(half_t)pv[j - 1][0], (half_t)pv[j - 1][1]};
+        pcur[cc][e] = h[0];
+        pcur[cc][e + 1] = h[1];
+        dot2_acc(acc[cc], h);
+      }
+      // Block i+2 into LDS (its slot is not read in this step) and the loads
+      // of block i+3, in the second half of the slots so that the loads
+      // issued a step ago have landed.
+      if (j >= NJ - kStorePieces - 2 && j < NJ - 2)
+        sstore_piece(st, kslot((i + 2) & 3), vslot((i + 2) & 3), j - (NJ - kStorePieces - 2));
+      if (j == NJ - 2) gload(st, i + 3);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    {
+      const int sc = 2 * (NJ - 1), cc = sc / 8, e = sc % 8;
+      const half2v h = {(half_t)pv[NJ - 1][0], (half_t)pv[NJ - 1][1]};
+      pcur[cc][e] = h[0];
+      pcur[cc][e + 1] = h[1];
+      dot2_acc(acc[cc], h);
+    }
+#pragma unroll
+    for (int w = 1; w < 2 * NT; w *= 2)
+#pragma unroll
+      for (int cc = 0; cc + w < 2 * NT; cc += 2 * w) acc[cc] += acc[cc + w];
+    return acc[0];
+  };
+
+  // Slow path for block i (K in slot si): its scores are recomputed from LDS
+  // (so the fast path need not keep them live), masked keys set to -inf,
+  // the exact row max formed, m raised to it, O and l rescaled, P redone.
+  auto slow = [&](int si, int kb0, bool masked, half8v(&pb)[2 * NT]) {
+    float16v s[NT];
+    qk(s, kslot(si));
+    if (masked) {
+      // Keys outside [lo, lim) (relative to kb0 + 8g) are invisible to this
+      // lane's query.
+      const int lim = (CAUSAL ? (int)min((int64_t)N, (int64_t)q + wr + 1) : N) - kb0 - 8 * g;
+      const int lo = (CAUSAL ? q - wl : 0) - kb0 - 8 * g;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kr = 32 * t + 16 * (r >> 3) + (r & 7);
+          if (kr >= lim || kr < lo) s[t][r] = -INFINITY;
+        }
+    }
+    float m8[2 * NT];
+#pragma unroll
+    for (int cc = 0; cc < 2 * NT; ++cc) {
+      const float16v& v = s[cc >> 1];
+      const int o8 = 8 * (cc & 1);
+      m8[cc] = fmaxf(fmaxf(fmaxf(v[o8], v[o8 + 1]), fmaxf(v[o8 + 2], v[o8 + 3])),
+                     fmaxf(fmaxf(v[o8 + 4], v[o8 + 5]), fmaxf(v[o8 + 6], v[o8 + 7])));
+    }
+#pragma unroll
+    for (int w = 1; w < 2 * NT; w *= 2)
+#pragma unroll
+      for (int cc = 0; cc + w < 2 * NT; cc += 2 * w) m8[cc] = fmaxf(m8[cc], m8[cc + w]);
+    const float mx = max_halves(m8[0]);                         // raw row max of the block
+    const float mx_c = (mx == -INFINITY) ? mx : mx * c;         // c > 0: scaling is monotone
+    const float m_new = fmaxf(m_run, mx_c);                     // -inf while nothing seen
+    const bool none = (m_new == -INFINITY);
+    const float alpha = none ? 1.f : fast_exp2(m_run - m_new);  // 0 on the first visible block
+    m_run = m_new;
+    m_use = none ? 0.f : m_new;
+    thr = none ? -1.f : kPSumMax;
+    l_run *= alpha;
+#pragma unroll
+    for (int u = 0; u < DT; ++u)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[u][r] *= alpha;
+    return expsum(s, pb);
+  };
+
+  // P V of one block on its own (a group's last block, after the loop).
+  auto pv_only = [&](const half8v(&pb)[2 * NT], const half_t* v_l) {
+#pragma unroll
+    for (int u = 0; u < DT; ++u) {
+      const half_t* vp = &v_l[(32 * u + ql) * VLD + 8 * g];
+#pragma unroll
+      for (int cc = 0; cc < 2 * NT; ++cc) o[u] = mfma32x32x16(load_half8(vp + 16 * cc), pb[cc], o[u]);
+    }
+  };
+
+  // One block step i: scores of block i+1 into sn, softmax of block i
+  // (scores in s, P into pcur), P V of block i-1 (P in pprev), block i+2
+  // into LDS and the loads of block i+3 (inside the fused stretch), barrier.  Block j lives in LDS slot j % 4,
+  // so the four blocks a step touches (i-1, i, i+1, i+2) never share one.
+  auto body = [&](int i, float16v(&s)[NT], float16v(&sn)[NT], half8v(&pprev)[2 * NT],
+                  half8v(&pcur)[2 * NT]) {
+    const int si = i & 3;
+    if (i < my_n) {
+      const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
+      // Some key of the block is past N or outside some query's window.
+      const bool masked =
+          (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
+      // After the group's last block the next scores come from a stale
+      // slot and are never used.  Before the first block, pprev is zero and
+      // slot 3 holds zeros, so the P V term adds nothing.
+      float ls = fused(s, sn, kslot((i + 1) & 3), vslot((i + 3) & 3), pprev, pcur, i);
+      // ls enters the condition so that the softmax cannot sink below it.
+      if (__any(masked || !(ls <= thr))) ls = slow(si, kb0, masked, pcur);
+      l_run += ls;
+    } else {
+      sstore(st, kslot((i + 2) & 3), vslot((i + 2) & 3));
+      gload(st, i + 3);
+    }
+    lds_barrier();
+  };
+
+  // ---- prologue: blocks 0 and 1 into LDS, 2 in flight, scores of 0;
+  // V^T of slot 3 (the P V of "block -1") cleared ----
+  {
+    half_t* v3 = vslot(3);
+    for (int k = gtid; k < VSLOT / 8; k += kGroup)
+      *reinterpret_cast<half8v*>(&v3[8 * k]) = half8v{};
+  }
+  {
+    St st1;  // blocks 0 and 1 in one round trip to memory
+    gload(st, 0);
+    gload(st1, 1);
+    sstore(st, kslot(0), vslot(0));
+    sstore(st1, kslot(1), vslot(1));
+  }
+  gload(st, 2);
+  lds_barrier();
+  float16v sa[NT], sb[NT];
+  qk(sa, kslot(0));
+  half8v pa[2 * NT], pb2[2 * NT];
+#pragma unroll
+  for (int cc = 0; cc < 2 * NT; ++cc) pa[cc] = pb2[cc] = half8v{};
+
+  // Unrolled by two so that the score and P arrays swap roles without copies.
+  for (int i = 0; i < iters; i += 2) {
+    body(i, sa, sb, pa, pb2);
+    body(i + 1, sb, sa, pb2, pa);
+  }
+  // P V of the group's last block.  Step j writes block j's P into pb2
+  // when j is even, into pa when j is odd.
+  if (my_n > 0) {
+    if ((my_n - 1) & 1)
+      pv_only(pa, vslot((my_n - 1) & 3));
+    else
+      pv_only(pb2, vslot((my_n - 1) & 3));
+  }
+
+  // ---- merge the key groups through LDS ----
+  if constexpr (KSPLIT > 1) {
+    // The partials below overwrite the start of the LDS, where group 0's
+    // last-block P V above may still be reading V^T.
+    lds_barrier();
+    constexpr int SLOTS = 16 * DT + 2;
+    constexpr int PART = 4 * SLOTS * 64;  // floats per published group
+    static_assert(sizeof(smem) >= (size_t)(KSPLIT - 1) * PART * sizeof(float), "merge buffer");
+    float* red = reinterpret_cast<float*>(smem) + (size_t)wave * SLOTS * 64 + lane;
+    if (kg > 0) {
+      float* mine = red + (size_t)(kg - 1) * PART;
+      mine[0] = m_run;
+      mine[64] = l_run;
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mine[(2 + 16 * u + r) * 64] = o[u][r];
+    }
+    lds_barrier();
+    if (kg != 0) return;
+#pragma unroll
+    for (int j = 0; j < KSPLIT - 1; ++j) {
+      const float* other = red + (size_t)j * PART;
+      const float m1 = other[0];
+      const float l1 = other[64];
+      const float mm = fmaxf(m_run, m1);
+      const float mu = (mm == -INFINITY) ? 0.f : mm;
+      const float a0 = fast_exp2(m_run - mu);
+      const float a1 = fast_exp2(m1 - mu);
+      m_run = mm;
+      l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+      for (int u = 0; u < DT; ++u)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[u][r] = o[u][r] * a0 + other[(2 + 16 * u + r) * 64] * a1;
+    }
+  }
+
+  // ---- normalise and store: lane holds O[q][32u + 8b + 4g + 0..3] ----
+  const float l_tot = sum_halves(l_run);
+  const float inv = 1.f / fmaxf(l_tot, 1e-6f);
+  constexpr int ES = OUT_F16 ? 2 : 4;
+  const rsrc_t rsO = make_rsrc(static_cast<char*>(p.O) +
+                                   ((int64_t)bh * p.bh_stride_o + (int64_t)q0 * p.stride_o) * ES,
+                               (uint32_t)qrows * p.stride_o * ES);
+#pragma unroll
+  for (int u = 0; u < DT; ++u) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int col = 32 * u + 8 * b + 4 * g;
+      const uint32_t off = ((q - q0) * p.stride_o + col) * ES;
+      float4v v = {o[u][4 * b] * inv, o[u][4 * b + 1] * inv, o[u][4 * b + 2] * inv,
+                   o[u][4 * b + 3] * inv};
+      if (OUT_F16) {
+        buf_store_f16x4(half4v{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]}, rsO, off);
+      } else {
+        buf_store_f32x4(v, rsO, off);
+      }
+    }
+  }
+}
+
+template <int D, bool CAUSAL, bool OUT_F16, int K>
+bool launch_fast_k(const Fa2Args& a, hipStream_t stream) {
+  if constexpr (K * fast_group_lds_halves<D>() * 2 <= 160 * 1024) {
+    hipLaunchKernelGGL((fa2_fast_kernel<D, CAUSAL, OUT_F16, K>),
+                       dim3(a.num_qblocks * a.batch_heads), dim3(K * kGroup), 0, stream, a);
+    return true;
+  }
+  return false;
+}
+
+template <int D, bool CAUSAL, bool OUT_F16>
+hipError_t launch_fast_t(const Fa2Args& a, int ksplit, hipStream_t stream) {
+  bool done = false;
+  if (ksplit >= 3) done = launch_fast_k<D, CAUSAL, OUT_F16, 3>(a, stream);
+  if (!done && ksplit >= 2) done = launch_fast_k<D, CAUSAL, OUT_F16, 2>(a, stream);
+  if (!done) launch_fast_k<D, CAUSAL, OUT_F16, 1>(a, stream);
+  return hipGetLastError();
+}
+
+template <bool OUT_F16>
+hipError_t launch_fast_d(const Fa2Args& a, int d, bool causal, int ksplit, hipStream_t s) {
+  switch (d) {
+    case 64:
+      return causal ? launch_fast_t<64, true, OUT_F16>(a, ksplit, s)
+                    : launch_fast_t<64, false, OUT_F16>(a, ksplit, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32) {
+  return head_dim == 64 && bias_kind == kBiasNone && !in_f32;
+}
+
+hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, int ksplit,
+                           hipStream_t stream) {
+  a.num_qblocks = (a.N + kBM - 1) / kBM;
+  return out_f16 ? launch_fast_d<true>(a, head_dim, causal, ksplit, stream)
+                 : launch_fast_d<false>(a, head_dim, causal, ksplit, stream);
+}
+
+}  // namespace neso

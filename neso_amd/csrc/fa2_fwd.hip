@@ -37,6 +37,7 @@
 // * Workgroups of one head are placed on one XCD (xcd_swizzle) so K/V of
 //   that head are fetched into a single L2.
 #include "common.h"
+#include "fa2_tiles.h"
 #include "neso_internal.h"
 
 namespace neso {
@@ -47,28 +48,6 @@ constexpr int kBM = 128;       // queries per workgroup
 constexpr int kGroup = 256;    // threads per key group (4 waves)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.f;  // rescale threshold (log2 units)
-
-// Row of the 32-key tile loaded into A-operand row rho (= lane % 32) so that
-// accumulator register r of lane group g holds key 16*(r/8) + 8*g + r%8.
-// Accumulator row rho = 8*(r/4) + 4*g + r%4 (see mfma32x32x16).
-__device__ __forceinline__ int kRowPerm(int rho) {
-  const int b = rho >> 3, g = (rho >> 2) & 1, j = rho & 3;
-  return 16 * (b >> 1) + 8 * g + 4 * (b & 1) + j;
-}
-
-// max over lanes l and l ^ 32 (v_permlane32_swap returns the lower-half and
-// upper-half values of the lane's position within its half).
-__device__ __forceinline__ float max_halves(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-
-__device__ __forceinline__ float sum_halves(float x) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
-                                                  false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 // Keys per LDS block.  64 measured faster than 128 at d = 64 on MI355X
 // (fewer live registers; the extra barriers are not the bottleneck).
@@ -600,6 +579,8 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
   // gives fewer than two workgroups per compute unit.
   const int64_t wgs = (int64_t)a.num_qblocks * a.batch_heads;
   const int ksplit = (a.ksplit > 0) ? a.ksplit : (wgs < 2 * (int64_t)device_cu_count() ? 2 : 1);
+  if (a.allow_fast && fa2_fast_supported(head_dim, bias_kind, in_f32))
+    return launch_fa2_fast(a, head_dim, causal, out_f16, ksplit, stream);
   if (in_f32) {
     if (bias_kind != kBiasNone || out_f16) return hipErrorInvalidValue;
     return launch_fa2_f32in(a, head_dim, causal, ksplit, stream);

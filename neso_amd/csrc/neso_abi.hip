@@ -47,6 +47,13 @@ int env_ksplit() {
   return (k >= 1 && k <= 4) ? k : 0;
 }
 
+// NESO_AMD_FA2_FAST=0 routes every FA2 call to the generic kernel (tests
+// compare both paths).
+int env_allow_fast() {
+  const char* v = getenv("NESO_AMD_FA2_FAST");
+  return (v && v[0] == '0') ? 0 : 1;
+}
+
 int check_head_dim(int32_t d) {
   if (d == 32 || d == 64 || d == 128) return NESO_OK;
   return fail(NESO_EUNSUPPORTED, "head_dim %d not supported (32, 64, 128)", d);
@@ -237,6 +244,7 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
   a.batch_heads = heads;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.ksplit = env_ksplit();
+  a.allow_fast = env_allow_fast();
   // Causal is the window (N, 0); windows wider than N are clamped to N.
   a.win_left = win_left < 0 ? N : (win_left < N ? win_left : N);
   a.win_right = win_right < 0 ? 0 : (win_right < N ? win_right : N);
