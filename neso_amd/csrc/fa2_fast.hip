@@ -131,10 +131,8 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     v_off[j] = (2 * (job % (kKB / 2)) * p.stride_kv + 8 * (job / (kKB / 2))) * 2;
   }
 
-  // Global -> registers.  Steps past the group's last block reload that
-  // block, so every step issues the same loads (the compiler's load counter
-  // stays exact) and a late store rewrites a slot with the data it already
-  // holds: the last block's V^T stays valid for the P V after the loop.
+  // Global -> registers.  Loads for blocks past the group's last reload
+  // that block (in range, never used).
   auto gload = [&](St& st, int i) {
     const int blk = blk0 + kg + KSPLIT * max(0, min(i, my_n - 1));
     const int kb0 = blk * kKB;
@@ -323,12 +321,10 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     return acc[0];
   };
 
-  // Slow path for block i (K in slot si): its scores are recomputed from LDS
-  // (so the fast path need not keep them live), masked keys set to -inf,
-  // the exact row max formed, m raised to it, O and l rescaled, P redone.
-  auto slow = [&](int si, int kb0, bool masked, half8v(&pb)[2 * NT]) {
-    float16v s[NT];
-    qk(s, kslot(si));
+  // Slow path on the scores s of the block at kb0 (raw Q K^T, modified in
+  // place): masked keys set to -inf, the exact row max formed, m raised to
+  // it, O and l rescaled, P redone into pb.  Returns the lane's P sum.
+  auto slow_scores = [&](float16v(&s)[NT], int kb0, bool masked, half8v(&pb)[2 * NT]) {
     if (masked) {
       // Keys outside [lo, lim) (relative to kb0 + 8g) are invisible to this
       // lane's query.
@@ -370,6 +366,14 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     return expsum(s, pb);
   };
 
+  // Slow path for block i of a step (K in slot si): its scores are
+  // recomputed from LDS, so the fused step need not keep them live.
+  auto slow = [&](int si, int kb0, bool masked, half8v(&pb)[2 * NT]) {
+    float16v s[NT];
+    qk(s, kslot(si));
+    return slow_scores(s, kb0, masked, pb);
+  };
+
   // P V of one block on its own (a group's last block, after the loop).
   auto pv_only = [&](const half8v(&pb)[2 * NT], const half_t* v_l) {
 #pragma unroll
@@ -393,26 +397,21 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       const bool masked =
           (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
       // After the group's last block the next scores come from a stale
-      // slot and are never used.  Before the first block, pprev is zero and
-      // slot 3 holds zeros, so the P V term adds nothing.
+      // slot and are never used.
       float ls = fused(s, sn, kslot((i + 1) & 3), vslot((i + 3) & 3), pprev, pcur, i);
       // ls enters the condition so that the softmax cannot sink below it.
       if (__any(masked || !(ls <= thr))) ls = slow(si, kb0, masked, pcur);
       l_run += ls;
-    } else {
-      sstore(st, kslot((i + 2) & 3), vslot((i + 2) & 3));
-      gload(st, i + 3);
     }
+    // Steps past the group's last block store and load nothing: no later
+    // step reads those blocks, and the last block's V^T (read by the P V
+    // after the loop) stays in place.  (A store here would also let the
+    // compiler hoist the V^T packing, and with it a wait for this step's
+    // loads, to the top of every step.)
     lds_barrier();
   };
 
-  // ---- prologue: blocks 0 and 1 into LDS, 2 in flight, scores of 0;
-  // V^T of slot 3 (the P V of "block -1") cleared ----
-  {
-    half_t* v3 = vslot(3);
-    for (int k = gtid; k < VSLOT / 8; k += kGroup)
-      *reinterpret_cast<half8v*>(&v3[8 * k]) = half8v{};
-  }
+  // ---- prologue: blocks 0 and 1 into LDS, 2 in flight, scores of 0 ----
   {
     St st1;  // blocks 0 and 1 in one round trip to memory
     gload(st, 0);
@@ -425,13 +424,25 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   float16v sa[NT], sb[NT];
   qk(sa, kslot(0));
   half8v pa[2 * NT], pb2[2 * NT];
-#pragma unroll
-  for (int cc = 0; cc < 2 * NT; ++cc) pa[cc] = pb2[cc] = half8v{};
 
-  // Unrolled by two so that the score and P arrays swap roles without copies.
-  for (int i = 0; i < iters; i += 2) {
-    body(i, sa, sb, pa, pb2);
-    body(i + 1, sb, sa, pb2, pa);
+  // ---- step 0, peeled: block 0 is every row's first visible block, so its
+  // softmax is the slow path on the scores above; scores of block 1 ----
+  if (my_n > 0) {
+    const int kb0 = (blk0 + kg) * kKB;
+    const bool masked =
+        (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
+    qk(sb, kslot(1));
+    l_run += slow_scores(sa, kb0, masked, pb2);
+  }
+  sstore(st, kslot(2), vslot(2));
+  gload(st, 3);
+  lds_barrier();
+
+  // Steps 1, 2, ...: unrolled by two so that the score and P arrays swap
+  // roles without copies.
+  for (int i = 1; i < iters; i += 2) {
+    body(i, sb, sa, pb2, pa);
+    body(i + 1, sa, sb, pa, pb2);
   }
   // P V of the group's last block.  Step j writes block j's P into pb2
   // when j is even, into pa when j is odd.
@@ -537,6 +548,14 @@ hipError_t launch_fast_d(const Fa2Args& a, int d, bool causal, int ksplit, hipSt
 
 bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32) {
   return head_dim == 64 && bias_kind == kBiasNone && !in_f32;
+}
+
+bool fa2_fast_preferred(bool causal, int32_t N) {
+  // Measured on MI355X (B*H = 16..64, d = 64): the fast kernel is 2-9%
+  // faster from N = 2048 up without a mask; below that its deeper prologue
+  // costs more than its cheaper blocks save, and causal rows gain more from
+  // the generic kernel's per-wave skipping of invisible blocks.
+  return !causal && N >= 1536;
 }
 
 hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, int ksplit,

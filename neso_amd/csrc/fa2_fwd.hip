@@ -579,7 +579,8 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
   // gives fewer than two workgroups per compute unit.
   const int64_t wgs = (int64_t)a.num_qblocks * a.batch_heads;
   const int ksplit = (a.ksplit > 0) ? a.ksplit : (wgs < 2 * (int64_t)device_cu_count() ? 2 : 1);
-  if (a.allow_fast && fa2_fast_supported(head_dim, bias_kind, in_f32))
+  if (a.allow_fast && fa2_fast_supported(head_dim, bias_kind, in_f32) &&
+      (a.allow_fast == 2 || fa2_fast_preferred(causal, a.N)))
     return launch_fa2_fast(a, head_dim, causal, out_f16, ksplit, stream);
   if (in_f32) {
     if (bias_kind != kBiasNone || out_f16) return hipErrorInvalidValue;

@@ -47,11 +47,14 @@ int env_ksplit() {
   return (k >= 1 && k <= 4) ? k : 0;
 }
 
-// NESO_AMD_FA2_FAST=0 routes every FA2 call to the generic kernel (tests
-// compare both paths).
+// FA2 kernel choice for fp16 calls without a bias (tests cover both
+// kernels): NESO_AMD_FA2_FAST=0 always takes the generic kernel, =2 the fast
+// kernel wherever it applies; unset or 1 chooses by shape.
 int env_allow_fast() {
   const char* v = getenv("NESO_AMD_FA2_FAST");
-  return (v && v[0] == '0') ? 0 : 1;
+  if (!v) return 1;
+  if (v[0] == '0') return 0;
+  return v[0] == '2' ? 2 : 1;
 }
 
 int check_head_dim(int32_t d) {

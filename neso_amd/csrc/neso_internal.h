@@ -34,8 +34,9 @@ struct Fa2Args {
   // i - win_left <= j <= i + win_right.  Causal is (N, 0).
   int32_t win_left;
   int32_t win_right;
-  // 1: fp16 calls without a bias may take the fast kernel (fa2_fast.hip);
-  // 0: always the generic kernel.
+  // Kernel choice for fp16 calls without a bias: 1 = the fast kernel
+  // (fa2_fast.hip) where it is measured faster, 2 = the fast kernel
+  // wherever it applies, 0 = always the generic kernel.
   int32_t allow_fast;
 };
 
@@ -43,8 +44,10 @@ struct Fa2Args {
 int device_cu_count();
 
 int fa2_query_block();
-// The fast kernel covers fp16 Q/K/V without a bias at head_dim 64.
+// The fast kernel covers fp16 Q/K/V without a bias at head_dim 64, and is
+// the faster one for unmasked attention from N ~ 2048 up.
 bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32);
+bool fa2_fast_preferred(bool causal, int32_t N);
 hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, int ksplit,
                            hipStream_t stream);
 hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool out_f16,

@@ -1,0 +1,113 @@
+"""Both FA2 kernels for fp16 Q/K/V, and the fast kernel's rescale paths, vs the CPU oracle.
+
+head_dim 64 without a bias runs the fast kernel where it is the faster one
+(unmasked, N >= 1536); ``NESO_AMD_FA2_FAST=2`` forces it wherever it applies
+and ``NESO_AMD_FA2_FAST=0`` forces the generic kernel.  Both must meet the
+attention bar (max abs error <= 2e-3 against the fp32 CPU softmax(QK^T s) V)
+for every key split, ragged and block-aligned lengths, causal or not.
+
+The fast kernel bounds each block's P by the lane's row sum instead of
+forming a row max (the running max is raised only when a block's fp16 P sum
+exceeds 2^12).  The inputs below force that path: key blocks whose logits
+jump far above the running max, fall far below it, or are huge throughout.
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import neso_amd
+from oracle import attention as A
+from oracle import inputs as I
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+
+
+def run(q, k, v, causal=False, scale=None):
+    dev = torch.device("cuda:0")
+    out = neso_amd.attention(q.to(dev), k.to(dev), v.to(dev), causal=causal, scale=scale)
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def check(q, k, v, causal=False, scale=None, tol=TOL):
+    s = 1 / math.sqrt(q.shape[-1]) if scale is None else scale
+    out = run(q, k, v, causal, scale)
+    ref = A.attention(q, k, v, s, causal=causal)
+    assert torch.isfinite(out).all()
+    err = (out - ref).abs().max().item()
+    assert err <= tol, err
+    return err
+
+
+@pytest.mark.parametrize("path", ["fast", "generic"])
+@pytest.mark.parametrize("ksplit", [1, 2])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 128, 192, 320, 1000])
+def test_paths_and_splits(gpu, monkeypatch, path, ksplit, causal, n):
+    """Key groups with equal and unequal block counts (odd block totals),
+    single-block groups and tails shorter than a block."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2" if path == "fast" else "0")
+    monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
+    q, k, v = I.fa2_inputs(1, 2, n, 64, seed=n + 7 * ksplit)
+    check(q, k, v, causal)
+
+
+def _stepped_keys(n, steps, seed):
+    """K rows scaled by a factor that changes per 64-key block."""
+    q, k, v = I.fa2_inputs(1, 2, n, 64, seed=seed)
+    k = k.float()
+    for b in range(0, n, 64):
+        k[:, :, b:b + 64] *= steps[(b // 64) % len(steps)]
+    return q, k.half(), v
+
+
+@pytest.mark.parametrize("ksplit", [1, 2])
+@pytest.mark.parametrize("causal", [False, True])
+def test_running_max_jumps_up(gpu, monkeypatch, ksplit, causal):
+    """Each later block's logits are far above the running max: P of the new
+    block would overflow fp16 without the slow path's rescale."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
+    q, k, v = _stepped_keys(768, [0.5, 1.5, 3.0, 6.0, 9.0, 12.0], seed=31)
+    check(q, k, v, causal)
+
+
+@pytest.mark.parametrize("ksplit", [1, 2])
+def test_running_max_falls(gpu, monkeypatch, ksplit):
+    """The first block holds the largest logits; later blocks contribute
+    little and must not disturb the result (no rescale needed)."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
+    q, k, v = _stepped_keys(768, [12.0, 4.0, 1.0, 0.25, 0.0, 0.1], seed=32)
+    check(q, k, v)
+
+
+def test_alternating_magnitudes(gpu, monkeypatch):
+    """Large and small logit blocks alternate: the running max rises in
+    steps and the fast path's bound is exceeded repeatedly."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    q, k, v = _stepped_keys(1024, [0.2, 8.0, 0.2, 11.0, 0.2, 14.0, 0.2, 16.0], seed=33)
+    check(q, k, v)
+
+
+@pytest.mark.parametrize("scale", [4.0, -4.0, 1e-6])
+def test_extreme_scales(gpu, monkeypatch, scale):
+    """|scale * log2(e)| far above 1 (logits of hundreds) and nearly 0."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    q, k, v = I.fa2_inputs(1, 2, 256, 64, seed=34)
+    check(q, k, v, scale=scale)
+
+
+def test_fast_equals_generic(gpu, monkeypatch):
+    """The two kernels agree with each other on the headline shape (a check
+    that does not depend on the oracle)."""
+    q, k, v = I.fa2_inputs(1, 16, 2048, 64, seed=35)
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    fast = run(q, k, v)
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "0")
+    generic = run(q, k, v)
+    assert (fast - generic).abs().max().item() <= 1e-3
