@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calibrate-copy", action="store_true")
+    ap.add_argument("--ramp", type=float, default=CLOCK_RAMP_S,
+                    help="seconds of untimed load before each measurement (clock ramp); "
+                         "0 for counter runs, whose per-dispatch figures do not depend on the clock")
     return ap.parse_args()
 
 
@@ -71,8 +74,9 @@ GRAPH_LAUNCHES = 16
 CLOCK_RAMP_S = 0.3
 
 
-def ramp_clock(run_once, torch, seconds=CLOCK_RAMP_S):
+def ramp_clock(run_once, torch, seconds=None):
     """Repeat ``run_once()`` (asynchronous GPU work) for ``seconds`` of wall time."""
+    seconds = CLOCK_RAMP_S if seconds is None else seconds
     t0 = time.perf_counter()
     while time.perf_counter() - t0 < seconds:
         for _ in range(8):
@@ -186,7 +190,9 @@ def fa2_case(neso_amd, torch, I, B, H, N, d, causal, steps, warmup, seed=0):
 
 
 def main():
+    global CLOCK_RAMP_S
     args = parse()
+    CLOCK_RAMP_S = max(0.0, args.ramp)
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1",
                           "n_gpus": args.gpus}))
@@ -230,7 +236,7 @@ def main():
                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("fa2_headline"),
-                     "kernel": "fa2_fwd_kernel<64,false,0,false>",
+                     "kernel": "fa2_fast_kernel<64,false,false,2>",
                      "algorithmic_flop_per_launch": flop},
     }
 
