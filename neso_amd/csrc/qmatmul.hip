@@ -704,6 +704,198 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
 }
 
 // ---------------------------------------------------------------------------
+// Large-M regime, dequantise-once tile GEMM (M >= 128).
+//
+// A workgroup computes a 128 (m) x 128 (n) tile of Y.  Its 8 waves form two
+// K-groups of 4 waves (64 x 64 each, 2 x 2 v_mfma_f32_32x32x16_f16 tiles):
+// group g takes the K-steps s = g, g + 2, ... in its own LDS buffers, so a
+// SIMD holds two waves whose loads, dequantisation and LDS traffic overlap
+// each other's MFMAs; the two partial tiles are summed through LDS at the
+// end.  Per K-step of 64 codes and group:
+//   * X tile 128 x 64 fp16 -> LDS, each 8-element group stored in the order
+//     {0,4,1,5,2,6,3,7} of unpack_word, rows padded to 72 halves;
+//   * W tile 128 rows x 64 codes: thread t loads word quad t&1 (32 codes,
+//     16 bytes) of row t>>1 and its scale, dequantises (c - z) * s once for
+//     the group (one fp16 rounding) and stores the 32 halves to an LDS B
+//     tile [n][k] in the same nibble order, rows padded to 72 halves;
+//   * each wave reads its A and B fragments (ds_read_b128) and issues 16
+//     MFMAs; a fragment feeds two MFMAs (4 KiB of LDS reads per 4 MFMAs).
+// LDS is double-buffered per group (2 x 72 KiB); global loads run two of
+// the group's steps ahead in registers; the next step's dequantisation and
+// LDS stores are issued among the current step's MFMAs.  One barrier per
+// step.
+constexpr int kTT = 128, kTK = 64, kTLD = kTK + 8;
+
+template <int kTKG>  // K-groups per workgroup (1 or 2)
+__global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
+  constexpr uint32_t kOut = 0x80000000u;  // buffer offset past any extent: loads return 0
+  constexpr int kBuf = kTT * kTLD / 8;    // half8v per LDS tile
+  __shared__ half8v lds[kTKG][2][2][kBuf];  // [group][buffer][X, W]
+  const int tid = threadIdx.x % 256, lane = tid & 63;
+  const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x / 256);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave >> 1, wn = wave & 1;
+  const int li = lane & 31, lh = lane >> 5;
+  const int mtiles = (a.M + kTT - 1) / kTT;
+  const int ntiles = (a.N + kTT - 1) / kTT;
+  const int id = (int)xcd_swizzle(blockIdx.x, (uint32_t)(mtiles * ntiles));
+  const int m0 = (id % mtiles) * kTT, n0 = (id / mtiles) * kTT;
+  const int KW = a.K >> 3, SG = a.K / a.group;
+  const int mrows = __builtin_amdgcn_readfirstlane(min(kTT, a.M - m0));
+  const int nrows = __builtin_amdgcn_readfirstlane(min(kTT, a.N - n0));
+  const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)((mrows - 1) * a.ldx + a.K) * 2u);
+  const rsrc_t rw = make_rsrc(a.W + (int64_t)n0 * KW, (uint32_t)nrows * KW * 4u);
+  const rsrc_t rs = make_rsrc(a.S + (int64_t)n0 * SG, (uint32_t)nrows * SG * 2u);
+  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
+  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const Nibbles nib = nibble_consts();
+  const uint32_t gm = (uint32_t)a.group >> 5;  // 32-code chunks per scale group
+  const bool gpow2 = (gm & (gm - 1)) == 0;
+  const uint32_t gshift = __builtin_ctz(gm);
+
+  // X: row tid/8 + 32j, 16-byte piece tid%8 of the step.  W: row tid/2,
+  // word quad tid&1.
+  const int xr0 = tid >> 3, xp = tid & 7;
+  const int wrow = tid >> 1, wq = tid & 1;
+  struct Stage {
+    half8v x[4];
+    uint4v w;
+    half_t s;
+  };
+  // Loads of the group's step t (global step kTKG t + kg).  Steps past K
+  // read zeros.
+  auto gload = [&](Stage& g, int t) {
+    const int k0 = (kTKG * t + kg) * kTK;
+    const uint32_t xoob = k0 + 8 * xp < a.K ? 0u : kOut;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      g.x[j] = buf_load_half8(rx, (((uint32_t)(xr0 + 32 * j) * a.ldx + k0 + 8 * xp) * 2u) | xoob);
+    const uint32_t chunk = (uint32_t)(k0 >> 5) + wq;
+    const uint32_t woob = (int)(32 * chunk) < a.K ? 0u : kOut;
+    const uint32_t sidx = gpow2 ? chunk >> gshift : chunk / gm;
+    g.w = __builtin_bit_cast(uint4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                         rw, ((uint32_t)wrow * KW * 4u + chunk * 16u) | woob, 0, 0));
+    g.s = __builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
+                                         rs, (((uint32_t)wrow * SG + sidx) * 2u) | woob, 0, 0));
+  };
+  // Piece 0..3: X row piece j; 4..7: dequantised W word i = piece - 4.
+  auto sstore_piece = [&](const Stage& g, int buf, int piece) {
+    if (piece < 4) {
+      const half8v x = g.x[piece];
+      lds[kg][buf][0][((xr0 + 32 * piece) * kTLD + 8 * xp) / 8] =
+          half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+    } else {
+      const int i = piece - 4;
+      const half2v s1 = {g.s, g.s};
+      const half_t s16v = g.s * (half_t)0.0625f;
+      const half2v s16 = {s16v, s16v};
+      half2v r[4];
+      unpack_word(g.w[i], nib, z1, z16, r);
+      const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
+      lds[kg][buf][1][(wrow * kTLD + 32 * wq + 8 * i) / 8] =
+          half8v{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
+    }
+  };
+
+  float16v acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = float16v{};
+
+  // One K-step on LDS buffer buf, with the next step's LDS stores (from
+  // stage g into buffer buf ^ 1) spread over its MFMAs.
+  auto step = [&](int buf, const Stage& g, bool store_next) {
+    const half8v* xb = lds[kg][buf][0];
+    const half8v* wb = lds[kg][buf][1];
+    auto afrag = [&](int mi, int ks) { return xb[((64 * wm + 32 * mi + li) * kTLD + 16 * ks + 8 * lh) / 8]; };
+    auto bfrag = [&](int nj, int ks) { return wb[((64 * wn + 32 * nj + li) * kTLD + 16 * ks + 8 * lh) / 8]; };
+    half8v af[2][2], bf[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) { af[0][t] = afrag(t, 0); bf[0][t] = bfrag(t, 0); }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int c = ks & 1;
+      if (ks + 1 < 4) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) { af[c ^ 1][t] = afrag(t, ks + 1); bf[c ^ 1][t] = bfrag(t, ks + 1); }
+      }
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = mfma32x32x16(af[c][mi], bf[c][nj], acc[mi][nj]);
+      if (store_next) {
+        sstore_piece(g, buf ^ 1, 2 * ks);
+        sstore_piece(g, buf ^ 1, 2 * ks + 1);
+      }
+    }
+  };
+
+  // Group steps: both groups run the same count (the barrier is shared);
+  // a group's steps past K compute on zeros.
+  const int nsteps = (a.K + kTK - 1) / kTK;
+  const int T = (nsteps + kTKG - 1) / kTKG;
+  Stage g0, g1;
+  gload(g0, 0);
+  gload(g1, 1);
+#pragma unroll
+  for (int piece = 0; piece < 8; ++piece) sstore_piece(g0, 0, piece);
+  gload(g0, 2);
+  lds_barrier();
+  // Step t computes buffer t&1 and stores step t+1 (stage (t+1)&1, loaded
+  // two steps ahead) into buffer (t+1)&1, then reloads that stage for step
+  // t+3.  Unrolled by two so the stages swap roles without copies.
+  for (int t0 = 0; t0 < T; t0 += 2) {
+    step(0, g1, t0 + 1 < T);
+    gload(g1, t0 + 3);
+    lds_barrier();
+    if (t0 + 1 < T) {
+      step(1, g0, t0 + 2 < T);
+      gload(g0, t0 + 4);
+      lds_barrier();
+    }
+  }
+
+  // Sum the groups' partial tiles: group 1 publishes, group 0 adds and
+  // stores.  The loop's last barrier ordered every LDS read before this.
+  if constexpr (kTKG == 2) {
+    static_assert(sizeof(lds) >= (size_t)4 * 64 * 64 * sizeof(float), "reduction buffer");
+    float* red = reinterpret_cast<float*>(lds) + (size_t)wave * 64 * 64 + lane;
+    if (kg == 1) {
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) red[((2 * mi + nj) * 16 + r) * 64] = acc[mi][nj][r];
+    }
+    lds_barrier();
+    if (kg == 1) return;
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int nj = 0; nj < 2; ++nj)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[mi][nj][r] += red[((2 * mi + nj) * 16 + r) * 64];
+  }
+
+  // acc[mi][nj] register r: row 64 wm + 32 mi + 8(r/4) + 4 lh + r%4,
+  // column 64 wn + 32 nj + li.
+#pragma unroll
+  for (int nj = 0; nj < 2; ++nj) {
+    const int n = n0 + 64 * wn + 32 * nj + li;
+    if (n >= a.N) continue;
+#pragma unroll
+    for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int m = m0 + 64 * wm + 32 * mi + 8 * (r >> 2) + 4 * lh + (r & 3);
+        if (m < a.M) a.Y[(int64_t)m * a.ldy + n] = (half_t)acc[mi][nj][r];
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // MFMA regime.  Each wave computes a 32 (m) x 32*TN (n) strip; 4 waves side
 // by side along N.  Per 64-column step of K, lane group g owns columns
 // [kb + 32g, kb + 32g + 32): one 16-byte word quad and one scale per row.
@@ -1036,6 +1228,28 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
 #ifndef NESO_GEMM_BN
 #define NESO_GEMM_BN 64
 #endif
+  // Dequantise-once tile GEMM: 128 x 128 tiles; its buffer offsets (one
+  // tile's X rows, W rows and scales) must stay below 2^31 bytes.
+  const bool tile_fits = (int64_t)kTT * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
+                         (int64_t)kTT * a.K / 2 < ((int64_t)1 << 31);
+  const char* tile_env = getenv("NESO_AMD_W4_TILE_GEMM");
+  const int tile_mode = tile_env ? atoi(tile_env) : -1;
+  // Measured at K = 4096, N = 11008: the tile GEMM wins from M = 256 up (two
+  // K-groups while the tiles fit on the CUs, one workgroup each; one K-group,
+  // two workgroups per CU, beyond); at M = 128 its 86 tiles leave most CUs
+  // idle and the 128 x 64 kernel below is faster.
+  // NESO_AMD_W4_TILE_GEMM = 0 / 1 / 2 forces off / one / two K-groups.
+  const int tiles = ((a.M + kTT - 1) / kTT) * ((a.N + kTT - 1) / kTT);
+  const int kgroups = tile_mode >= 0 ? tile_mode
+                      : a.M < 192    ? 0
+                                     : (tiles <= device_cu_count() ? 2 : 1);
+  if (kgroups && tile_fits) {
+    if (kgroups == 2)
+      hipLaunchKernelGGL(w4a16_tile_gemm_kernel<2>, dim3(tiles), dim3(512), 0, s, a);
+    else
+      hipLaunchKernelGGL(w4a16_tile_gemm_kernel<1>, dim3(tiles), dim3(256), 0, s, a);
+    return hipGetLastError();
+  }
   constexpr int WM = 2, WN = NESO_GEMM_WN, BN = NESO_GEMM_BN;
   if ((int64_t)kGBM * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
       (int64_t)BN * a.K / 2 < ((int64_t)1 << 31)) {

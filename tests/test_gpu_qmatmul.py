@@ -154,3 +154,29 @@ def test_w8a16_tiled_and_fallback(gpu, m, n, k, scaled):
         ref = Q.w8a16_matmul(a.double().numpy(), b.double().numpy())
     torch.cuda.synchronize()
     assert Q.rel_err(c.cpu().numpy(), ref) < 1e-4
+
+
+@pytest.mark.parametrize("kgroups", ["1", "2"])
+@pytest.mark.parametrize("m,n,k", [(128, 11008, 4096), (200, 300, 4096), (256, 1000, 4128),
+                                   (300, 129, 96), (640, 256, 1024)])
+def test_tile_gemm(gpu, monkeypatch, kgroups, m, n, k):
+    """The dequantise-once tile GEMM with one and two K-groups: ragged M and N
+    tiles, K not a multiple of its 64-code step, and a K shorter than one
+    step per group."""
+    monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n + k)
+    words = Q.pack_int4(codes.numpy())
+    y = gpu_w4(x, words, scales)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
+    assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("kgroups", ["1", "2"])
+@pytest.mark.parametrize("group,zero", [(64, 8), (128, 7), (32, 0), (4096, 15)])
+def test_tile_gemm_groups(gpu, monkeypatch, kgroups, group, zero):
+    monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
+    x, codes, scales = I.qmatmul_inputs(256, 4096, 300, group=group, seed=group + zero)
+    words = Q.pack_int4(codes.numpy())
+    y = gpu_w4(x, words, scales, group, zero)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy(), group, zero)
+    assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
