@@ -804,8 +804,10 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
     for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = float16v{};
 
   // One K-step on LDS buffer buf, with the next step's LDS stores (from
-  // stage g into buffer buf ^ 1) spread over its MFMAs.
-  auto step = [&](int buf, const Stage& g, bool store_next) {
+  // stage g into buffer buf ^ 1) spread over its MFMAs.  After the last
+  // step the stage holds the zeros loaded past K; storing them into the
+  // idle buffer is harmless and keeps the step one basic block.
+  auto step = [&](int buf, const Stage& g) {
     const half8v* xb = lds[kg][buf][0];
     const half8v* wb = lds[kg][buf][1];
     auto afrag = [&](int mi, int ks) { return xb[((64 * wm + 32 * mi + li) * kTLD + 16 * ks + 8 * lh) / 8]; };
@@ -824,10 +826,8 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
       for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
         for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = mfma32x32x16(af[c][mi], bf[c][nj], acc[mi][nj]);
-      if (store_next) {
-        sstore_piece(g, buf ^ 1, 2 * ks);
-        sstore_piece(g, buf ^ 1, 2 * ks + 1);
-      }
+      sstore_piece(g, buf ^ 1, 2 * ks);
+      sstore_piece(g, buf ^ 1, 2 * ks + 1);
     }
   };
 
@@ -846,11 +846,11 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   // two steps ahead) into buffer (t+1)&1, then reloads that stage for step
   // t+3.  Unrolled by two so the stages swap roles without copies.
   for (int t0 = 0; t0 < T; t0 += 2) {
-    step(0, g1, t0 + 1 < T);
+    step(0, g1);
     gload(g1, t0 + 3);
     lds_barrier();
     if (t0 + 1 < T) {
-      step(1, g0, t0 + 2 < T);
+      step(1, g0);
       gload(g0, t0 + 4);
       lds_barrier();
     }
@@ -880,17 +880,22 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   }
 
   // acc[mi][nj] register r: row 64 wm + 32 mi + 8(r/4) + 4 lh + r%4,
-  // column 64 wn + 32 nj + li.
+  // column 64 wn + 32 nj + li of the tile at (m0, n0).  Rows past M fall
+  // outside the buffer resource (ldy >= N >= n0 + nrows); columns past N
+  // get an out-of-range offset.
+  const rsrc_t ry = make_rsrc(a.Y + (int64_t)m0 * a.ldy + n0, (uint32_t)((mrows - 1) * a.ldy + nrows) * 2u);
 #pragma unroll
   for (int nj = 0; nj < 2; ++nj) {
-    const int n = n0 + 64 * wn + 32 * nj + li;
-    if (n >= a.N) continue;
+    const int nl = 64 * wn + 32 * nj + li;
+    const uint32_t noob = nl < nrows ? 0u : kOut;
 #pragma unroll
     for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + 64 * wm + 32 * mi + 8 * (r >> 2) + 4 * lh + (r & 3);
-        if (m < a.M) a.Y[(int64_t)m * a.ldy + n] = (half_t)acc[mi][nj][r];
+        const int ml = 64 * wm + 32 * mi + 8 * (r >> 2) + 4 * lh + (r & 3);
+        const uint32_t off = (((uint32_t)ml * a.ldy + (uint32_t)nl) * 2u) | noob;
+        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (half_t)acc[mi][nj][r]),
+                                              ry, off, 0, 0);
       }
   }
 }
