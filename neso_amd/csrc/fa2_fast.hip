@@ -23,7 +23,7 @@
 //   straight-line stretch as block i's softmax (VALU), so the matrix unit and
 //   the VALU work at the same time inside one wave; two waves per SIMD (two
 //   key groups) fill the remaining gaps.  K and V^T of a block share one
-//   slot of a 3-slot LDS ring, which leaves one barrier per block and keeps
+//   slot of a 4-slot LDS ring, which leaves one barrier per block and keeps
 //   block i's K in LDS while block i is processed (the slow path recomputes
 //   its scores from there); global loads run one block ahead of the LDS
 //   stores through registers.
