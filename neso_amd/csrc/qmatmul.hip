@@ -102,10 +102,14 @@ template <int GI>
 struct GemvRow {
   uint4v w[GI];
   float s[GI];
+  uint32_t sw;  // GI == 2, group 32: scales 2l and 2l+1 of the row
 };
 
-template <int MR, int GI, int R>
+// PS (two chunks per lane, group 32): the scales come as one 4-byte load per
+// row and lane.
+template <int MR, int GI, int R, bool PS>
 __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
+  static_assert(!PS || GI == 2, "paired scales need two chunks per lane");
   const int lane = threadIdx.x & 63;
   const int wid = blockIdx.x * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int T = gridDim.x * (kThreads / kWave);
@@ -129,13 +133,32 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
       const int gch = lane + 64 * gi;
       r.w[gi] = __builtin_bit_cast(uint4v, __builtin_amdgcn_raw_buffer_load_b128(
                                                rw, (uint32_t)gch * 16u, 0, kNonTemporal));
-      const uint32_t sidx = (uint32_t)(32 * gch) / (uint32_t)a.group;
-      r.s[gi] = (float)__builtin_bit_cast(
-          half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, sidx * 2u, 0, kNonTemporal));
+      if constexpr (!PS) {
+        const uint32_t sidx = (uint32_t)(32 * gch) / (uint32_t)a.group;
+        r.s[gi] = (float)__builtin_bit_cast(
+            half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(rs, sidx * 2u, 0, kNonTemporal));
+      }
+    }
+    // Two chunks per lane with one scale each: the row's 128 scales in one
+    // 4-byte load per lane (half as many load instructions), handed to the
+    // lanes that own those chunks in row_dot.
+    if constexpr (PS)
+      r.sw = __builtin_amdgcn_raw_buffer_load_b32(rs, (uint32_t)lane * 4u, 0, kNonTemporal);
+  };
+
+  // Scales of chunks l and l + 64 from lanes l/2 and 32 + l/2 (half l % 2).
+  auto pair_scales_of = [&](GemvRow<GI>& r) {
+    if constexpr (PS) {
+      const int sh = (lane & 1) * 16;
+      const uint32_t d0 = (uint32_t)__builtin_amdgcn_ds_bpermute((lane >> 1) * 4, (int)r.sw);
+      const uint32_t d1 = (uint32_t)__builtin_amdgcn_ds_bpermute((32 + (lane >> 1)) * 4, (int)r.sw);
+      r.s[0] = (float)__builtin_bit_cast(half_t, (uint16_t)(d0 >> sh));
+      r.s[1] = (float)__builtin_bit_cast(half_t, (uint16_t)(d1 >> sh));
     }
   };
 
-  auto row_dot = [&](const GemvRow<GI>& r, float (&y)[MR]) {
+  auto row_dot = [&](GemvRow<GI>& r, float (&y)[MR]) {
+    pair_scales_of(r);
 #pragma unroll
     for (int m = 0; m < MR; ++m) y[m] = 0.f;
 #pragma unroll
@@ -1137,11 +1160,13 @@ hipError_t launch_gemv_r(const W4Args& a, hipStream_t s) {
   const int blocks = (waves + 3) / 4;
   const int G = a.K / 32;
   if (G <= 64) {
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 1, R>), dim3(blocks), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 1, R, false>), dim3(blocks), dim3(kThreads), 0, s, a);
+  } else if (G <= 128 && a.group == 32 && G % 2 == 0) {  // whole 4-byte scale pairs
+    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 2, R, true>), dim3(blocks), dim3(kThreads), 0, s, a);
   } else if (G <= 128) {
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 2, R>), dim3(blocks), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 2, R, false>), dim3(blocks), dim3(kThreads), 0, s, a);
   } else if (G <= 256) {
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 4, R>), dim3(blocks), dim3(kThreads), 0, s, a);
+    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 4, R, false>), dim3(blocks), dim3(kThreads), 0, s, a);
   } else {
     return hipErrorInvalidValue;
   }

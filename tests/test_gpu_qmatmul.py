@@ -58,6 +58,22 @@ def test_ragged(gpu, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
+@pytest.mark.parametrize("m", [1, 3])
+@pytest.mark.parametrize("k", [2048, 2080, 2112, 4064, 4096, 6144])
+@pytest.mark.parametrize("n", [1, 65, 300])
+def test_gemv_chunks_per_lane(gpu, m, k, n):
+    """GEMV with one, two and four 32-code chunks per lane.  With two chunks
+    and an even chunk count (K = 2112, 4096) the row's scales arrive as one
+    4-byte load per lane and are handed between lanes; an odd count (2080,
+    4064) keeps one 2-byte load per chunk.  Distinct per-(row, group) scales
+    catch a scale delivered to the wrong lane."""
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=k + n + m)
+    words = Q.pack_int4(codes.numpy())
+    y = gpu_w4(x, words, scales)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
+    assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
+
+
 @pytest.mark.parametrize("group,zero", [(64, 8), (128, 7), (32, 0), (4096, 15)])
 @pytest.mark.parametrize("m", [1, 16])
 def test_group_and_zero_point(gpu, group, zero, m):
