@@ -22,11 +22,15 @@
 // * Software pipeline: block i+1's scores (MFMA) are issued in the same
 //   straight-line stretch as block i's softmax (VALU), so the matrix unit and
 //   the VALU work at the same time inside one wave; two waves per SIMD (two
-//   key groups) fill the remaining gaps.  K and V^T of a block share one
+//   key groups) fill the remaining gaps.  K and V of a block share one
 //   slot of a 4-slot LDS ring, which leaves one barrier per block and keeps
 //   block i's K in LDS while block i is processed (the slow path recomputes
 //   its scores from there); global loads run one block ahead of the LDS
 //   stores through registers.
+// * V stays row-major in LDS (plain 16-byte stores, chunks swizzled against
+//   bank conflicts) and the V^T operand of P V is read with gfx950's
+//   transposing LDS load, ds_read_b64_tr_b16, instead of being transposed
+//   with register permutes before the store.
 #include "common.h"
 #include "fa2_tiles.h"
 #include "neso_internal.h"
@@ -42,18 +46,32 @@ constexpr float kPSumMax = 4096.f;  // fast-path bound on a lane's block sum of 
 
 template <int D>
 struct FastStage {
-  static constexpr int KCH = kKB * D / 8 / kGroup;   // 8-element K pieces per thread
-  static constexpr int VCH = kKB * D / 16 / kGroup;  // (key pair, 8 columns) V jobs
+  static constexpr int KCH = kKB * D / 8 / kGroup;  // 8-element K (and V) pieces per thread
   half8v k[KCH];
-  half8v v[VCH][2];
+  half8v v[KCH];
 };
 
 // LDS halves of one key group: a 4-slot ring, each slot K [KB][D+8] then
-// V^T [D][KB+8].
+// V [KB][D] (row-major, 16-byte chunks swizzled; read transposed).
 constexpr int kSlots = 4;
 template <int D>
 constexpr int fast_group_lds_halves() {
-  return kSlots * (kKB * (D + 8) + D * (kKB + 8));
+  return kSlots * (kKB * (D + 8) + kKB * D);
+}
+
+// Chunk swizzle of the V rows: 16-byte chunk c of key row r sits at chunk
+// c ^ vswz(r) (D = 64: 8 chunks per row).  With it, both the 16-byte stores
+// and the transposed 8-byte reads below touch every LDS bank once per pass.
+__device__ __forceinline__ int vswz(int r) { return ((r >> 1) & 1) * 4; }
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane 4e + t passes the
+// address of 4 halves (row e, columns 4t..4t+3 of a 4 x 16 tile) and lane j
+// receives column j: the 4 rows' element j.
+__device__ __forceinline__ half4v lds_read_tr16(const half_t* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(const_cast<half_t*>(p)));
+  return __builtin_bit_cast(half4v, r);
 }
 
 template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT>
@@ -62,14 +80,12 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
   constexpr int KLD = D + 8;    // LDS row stride of K (halves)
-  constexpr int VLD = kKB + 8;  // LDS row stride of V^T (halves)
   constexpr int KSLOT = kKB * KLD;
-  constexpr int VSLOT = D * VLD;
+  constexpr int VSLOT = kKB * D;
+  static_assert(D == 64, "V swizzle and transposed reads assume 8 chunks per row");
   constexpr int GLDS = fast_group_lds_halves<D>();
   using St = FastStage<D>;
-  static_assert(St::KCH >= 1 && St::VCH >= 1 && kKB * D % (8 * kGroup) == 0 &&
-                    kKB * D % (16 * kGroup) == 0,
-                "tile split");
+  static_assert(St::KCH >= 1 && kKB * D % (8 * kGroup) == 0, "tile split");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
 
   const int tid = threadIdx.x;
@@ -124,12 +140,6 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     const int c8 = gtid + kGroup * j;
     k_off[j] = ((c8 / (D / 8)) * p.stride_kv + 8 * (c8 % (D / 8))) * 2;
   }
-  uint32_t v_off[St::VCH];
-#pragma unroll
-  for (int j = 0; j < St::VCH; ++j) {
-    const int job = gtid + kGroup * j;
-    v_off[j] = (2 * (job % (kKB / 2)) * p.stride_kv + 8 * (job / (kKB / 2))) * 2;
-  }
 
   // Global -> registers.  Loads for blocks past the group's last reload
   // that block (in range, never used).
@@ -144,10 +154,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 #pragma unroll
     for (int j = 0; j < St::KCH; ++j) st.k[j] = buf_load_half8(rk, k_off[j]);
 #pragma unroll
-    for (int j = 0; j < St::VCH; ++j) {
-      st.v[j][0] = buf_load_half8(rv, v_off[j]);
-      st.v[j][1] = buf_load_half8(rv, v_off[j] + p.stride_kv * 2);
-    }
+    for (int j = 0; j < St::KCH; ++j) st.v[j] = buf_load_half8(rv, k_off[j]);
   };
 
   St st;  // one block in flight between global memory and LDS
@@ -155,30 +162,19 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   auto kslot = [&](int s) { return gbase + s * (KSLOT + VSLOT); };
   auto vslot = [&](int s) { return gbase + s * (KSLOT + VSLOT) + KSLOT; };
 
-  // Registers -> LDS: K row-major [key][KLD], V transposed [d][VLD] as
-  // 32-bit key pairs.  Split in pieces so that the fused step can spread
-  // them over its MFMA slots: piece 0 stores K, pieces 1..4 a quarter of the
-  // V^T pairs each.
-  constexpr int kStorePieces = 5;
+  // Registers -> LDS: K row-major [key][KLD], V row-major [key][D] with
+  // swizzled chunks, 16 bytes per store.  One store per piece so that the
+  // fused step can spread them over its MFMA slots: pieces 0..KCH-1 store
+  // K, the rest V.
+  constexpr int kStorePieces = 2 * St::KCH;
   auto sstore_piece = [&](const St& st, half_t* k_l, half_t* v_l, int piece) {
-    if (piece == 0) {
-#pragma unroll
-      for (int j = 0; j < St::KCH; ++j) {
-        const int c8 = gtid + kGroup * j;
-        *reinterpret_cast<half8v*>(&k_l[(c8 / (D / 8)) * KLD + 8 * (c8 % (D / 8))]) = st.k[j];
-      }
-      return;
-    }
-#pragma unroll
-    for (int j = 0; j < St::VCH; ++j) {
-      const int job = gtid + kGroup * j;
-      const int kp = 2 * (job % (kKB / 2));
-      const int col = 8 * (job / (kKB / 2));
-#pragma unroll
-      for (int e = 2 * (piece - 1); e < 2 * piece; ++e)
-        *reinterpret_cast<half2v*>(&v_l[(col + e) * VLD + kp]) =
-            half2v{st.v[j][0][e], st.v[j][1][e]};
-    }
+    const int j = piece % St::KCH;
+    const int c8 = gtid + kGroup * j;
+    const int r = c8 / (D / 8), c = c8 % (D / 8);
+    if (piece < St::KCH)
+      *reinterpret_cast<half8v*>(&k_l[r * KLD + 8 * c]) = st.k[j];
+    else
+      *reinterpret_cast<half8v*>(&v_l[r * D + 8 * (c ^ vswz(r))]) = st.v[j];
   };
   auto sstore = [&](const St& st, half_t* k_l, half_t* v_l) {
 #pragma unroll
@@ -194,6 +190,28 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   for (int u = 0; u < DT; ++u) o[u] = float16v{};
   const int krow = kRowPerm(ql);
   const half2v ones = {(half_t)1.f, (half_t)1.f};
+
+  // Transposed V fragment (A operand of O^T = V^T P^T; d tile u, key chunk
+  // cc): lane l gets V[16cc + 8(l/32) + 0..7][32u + l%32], two 4-key reads.
+  // In read r lane l addresses key row 16cc + 8(l/32) + 4r + (l%16)/4 and
+  // columns 32u + 16((l/16)%2) + 4(l%4) .. +3 (chunk swizzled; the swizzle
+  // depends on bit 1 of the row only, which 16cc and 4r leave alone).
+  int vtr[DT];
+  {
+    const int row = 8 * (lane >> 5) + ((lane & 15) >> 2);
+    const int col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+    for (int u = 0; u < DT; ++u) {
+      const int cu = 32 * u + col;
+      vtr[u] = row * D + 8 * ((cu >> 3) ^ vswz(row)) + (cu & 7);
+    }
+  }
+  auto vfrag = [&](const half_t* v_l, int u, int cc) {
+    const half_t* pp = v_l + vtr[u] + 16 * cc * D;
+    const half4v a = lds_read_tr16(pp);
+    const half4v b = lds_read_tr16(pp + 4 * D);
+    return half8v{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  };
 
   auto qk = [&](float16v(&s)[NT], const half_t* k_l) {
 #pragma unroll
@@ -253,13 +271,12 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     constexpr int AHEAD = 4;
     static_assert(NQ == NP && 32 % NJ == 0 && SPJ == 2, "slot split");
     const half_t* kp = &k_l[krow * KLD + 8 * g];
-    const half_t* vp = &v_l[ql * VLD + 8 * g];
     // Fragment of slot j: even j -> K (tile q % NT, k-step q / NT),
     // odd j -> V^T (tile q % DT, key chunk q / DT), q = j / 2.
     auto frag = [&](int j) {
       const int q = j / 2;
       return (j % 2 == 0) ? load_half8(kp + 32 * (q % NT) * KLD + 16 * (q / NT))
-                          : load_half8(vp + 32 * (q % DT) * VLD + 16 * (q / DT));
+                          : vfrag(v_l, q % DT, q / DT);
     };
     auto score = [&](int sc) {  // score sc (0..31) of this lane
       const int cc = sc / 8;
@@ -377,11 +394,9 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // P V of one block on its own (a group's last block, after the loop).
   auto pv_only = [&](const half8v(&pb)[2 * NT], const half_t* v_l) {
 #pragma unroll
-    for (int u = 0; u < DT; ++u) {
-      const half_t* vp = &v_l[(32 * u + ql) * VLD + 8 * g];
+    for (int u = 0; u < DT; ++u)
 #pragma unroll
-      for (int cc = 0; cc < 2 * NT; ++cc) o[u] = mfma32x32x16(load_half8(vp + 16 * cc), pb[cc], o[u]);
-    }
+      for (int cc = 0; cc < 2 * NT; ++cc) o[u] = mfma32x32x16(vfrag(v_l, u, cc), pb[cc], o[u]);
   };
 
   // One block step i: scores of block i+1 into sn, softmax of block i
@@ -404,9 +419,9 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       l_run += ls;
     }
     // Steps past the group's last block store and load nothing: no later
-    // step reads those blocks, and the last block's V^T (read by the P V
+    // step reads those blocks, and the last block's V (read by the P V
     // after the loop) stays in place.  (A store here would also let the
-    // compiler hoist the V^T packing, and with it a wait for this step's
+    // compiler hoist the stores, and with them a wait for this step's
     // loads, to the top of every step.)
     lds_barrier();
   };
