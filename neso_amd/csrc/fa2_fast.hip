@@ -59,21 +59,6 @@ constexpr int fast_group_lds_halves() {
   return kSlots * (kKB * (D + 8) + kKB * D);
 }
 
-// Chunk swizzle of the V rows: 16-byte chunk c of key row r sits at chunk
-// c ^ vswz(r) (D = 64: 8 chunks per row).  With it, both the 16-byte stores
-// and the transposed 8-byte reads below touch every LDS bank once per pass.
-__device__ __forceinline__ int vswz(int r) { return ((r >> 1) & 1) * 4; }
-
-// ds_read_b64_tr_b16: in each group of 16 lanes, lane 4e + t passes the
-// address of 4 halves (row e, columns 4t..4t+3 of a 4 x 16 tile) and lane j
-// receives column j: the 4 rows' element j.
-__device__ __forceinline__ half4v lds_read_tr16(const half_t* p) {
-  typedef short v4s __attribute__((ext_vector_type(4)));
-  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4s*)(const_cast<half_t*>(p)));
-  return __builtin_bit_cast(half4v, r);
-}
-
 template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT>
 __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   constexpr int NT = kKB / 32;  // 32-key tiles per block
@@ -82,7 +67,6 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   constexpr int KLD = D + 8;    // LDS row stride of K (halves)
   constexpr int KSLOT = kKB * KLD;
   constexpr int VSLOT = kKB * D;
-  static_assert(D == 64, "V swizzle and transposed reads assume 8 chunks per row");
   constexpr int GLDS = fast_group_lds_halves<D>();
   using St = FastStage<D>;
   static_assert(St::KCH >= 1 && kKB * D % (8 * kGroup) == 0, "tile split");
@@ -174,7 +158,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     if (piece < St::KCH)
       *reinterpret_cast<half8v*>(&k_l[r * KLD + 8 * c]) = st.k[j];
     else
-      *reinterpret_cast<half8v*>(&v_l[r * D + 8 * (c ^ vswz(r))]) = st.v[j];
+      *reinterpret_cast<half8v*>(&v_l[v_store_at<D>(r, c)]) = st.v[j];
   };
   auto sstore = [&](const St& st, half_t* k_l, half_t* v_l) {
 #pragma unroll
@@ -191,27 +175,12 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   const int krow = kRowPerm(ql);
   const half2v ones = {(half_t)1.f, (half_t)1.f};
 
-  // Transposed V fragment (A operand of O^T = V^T P^T; d tile u, key chunk
-  // cc): lane l gets V[16cc + 8(l/32) + 0..7][32u + l%32], two 4-key reads.
-  // In read r lane l addresses key row 16cc + 8(l/32) + 4r + (l%16)/4 and
-  // columns 32u + 16((l/16)%2) + 4(l%4) .. +3 (chunk swizzled; the swizzle
-  // depends on bit 1 of the row only, which 16cc and 4r leave alone).
+  // Transposed V fragments (A operand of O^T = V^T P^T, d tile u, key
+  // chunk cc): this lane's offsets into a V tile.
   int vtr[DT];
-  {
-    const int row = 8 * (lane >> 5) + ((lane & 15) >> 2);
-    const int col = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 #pragma unroll
-    for (int u = 0; u < DT; ++u) {
-      const int cu = 32 * u + col;
-      vtr[u] = row * D + 8 * ((cu >> 3) ^ vswz(row)) + (cu & 7);
-    }
-  }
-  auto vfrag = [&](const half_t* v_l, int u, int cc) {
-    const half_t* pp = v_l + vtr[u] + 16 * cc * D;
-    const half4v a = lds_read_tr16(pp);
-    const half4v b = lds_read_tr16(pp + 4 * D);
-    return half8v{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-  };
+  for (int u = 0; u < DT; ++u) vtr[u] = v_tr_offset<D>(lane, u);
+  auto vfrag = [&](const half_t* v_l, int u, int cc) { return v_frag_tr<D>(v_l, vtr[u], cc); };
 
   auto qk = [&](float16v(&s)[NT], const half_t* k_l) {
 #pragma unroll

@@ -27,8 +27,9 @@
 //   S^T accumulator registers of lane group g are exactly 8 consecutive keys
 //   per 16-key chunk.  exp(S^T) converted to f16 is therefore directly the
 //   B operand of O^T = V^T P^T: P never goes through LDS.
-// * V is written to LDS transposed ([d][key]) as 32-bit key pairs, which is
-//   bank-conflict free, so the A operand V^T is one ds_read_b128 per lane.
+// * V is stored to LDS row-major ([key][d], 16-byte chunks swizzled) and
+//   its V^T operand is read with the transposing LDS load
+//   ds_read_b64_tr_b16, two per fragment (v_frag_tr in fa2_tiles.h).
 // * Softmax runs in the log2 domain with one FMA + one v_exp_f32 per score:
 //   p = 2^(s*c - m), c = |scale| * log2(e).  The running max m is only
 //   raised (and O, l rescaled) when a row max exceeds it by more than
@@ -67,11 +68,9 @@ struct Piece8<true> {
 template <int D, bool F32IN>
 struct Staging {
   static constexpr int kKB = key_block<D>();
-  static constexpr int KCH = kKB * D / 8 / kGroup;   // 8-element K pieces per thread
-  static constexpr int VJOBS = kKB * D / 16;         // (key pair, 8 columns) jobs
-  static constexpr int VCH = (VJOBS + kGroup - 1) / kGroup;
+  static constexpr int KCH = kKB * D / 8 / kGroup;   // 8-element K (and V) pieces per thread
   Piece8<F32IN> k[KCH];
-  Piece8<F32IN> v[VCH][2];
+  Piece8<F32IN> v[KCH];
   float b;
 };
 
@@ -94,18 +93,17 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;   // 32-row tiles of O^T
   constexpr int KLD = D + 8;   // LDS row stride of K (halves)
-  constexpr int VLD = kKB + 8; // LDS row stride of V^T (halves)
   constexpr int BAND = kBM + kKB - 1;  // bias-table entries per block
   using St = Staging<D, F32IN>;
   using InT = typename std::conditional<F32IN, float, half_t>::type;
   constexpr int IES = sizeof(InT);  // bytes per input element
   static_assert(St::KCH >= 1 && kKB * D / 8 % kGroup == 0, "K tile split");
 
-  // LDS: per key group two block slots, each K [KB][KLD] then V^T [D][VLD]
-  // (halves), followed for f32 input by the low halves of both; reused
-  // after the loop for the key-group merge.
+  // LDS: per key group two block slots, each K [KB][KLD] then V [KB][D]
+  // (halves, swizzled chunks), followed for f32 input by the low halves of
+  // both; reused after the loop for the key-group merge.
   constexpr int KHALF = kKB * KLD;
-  constexpr int LO = KHALF + D * VLD;  // offset of the low-half tiles
+  constexpr int LO = KHALF + kKB * D;  // offset of the low-half tiles
   constexpr int SLOT = F32IN ? 2 * LO : LO;
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * 2 * SLOT];
   __shared__ float sBias[KSPLIT][2][BIAS == kBiasTableF32 ? BAND + 1 : 1];
@@ -179,12 +177,6 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     const int c8 = gtid + kGroup * j;
     k_off[j] = ((c8 / (D / 8)) * p.stride_kv + 8 * (c8 % (D / 8))) * IES;
   }
-  uint32_t v_off[St::VCH];
-#pragma unroll
-  for (int j = 0; j < St::VCH; ++j) {
-    const int job = min(gtid + kGroup * j, St::VJOBS - 1);
-    v_off[j] = (2 * (job % (kKB / 2)) * p.stride_kv + 8 * (job / (kKB / 2))) * IES;
-  }
   const int kgu = kg;
 
   auto gload = [&](St& st, int i) {
@@ -204,10 +196,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
 #pragma unroll
     for (int j = 0; j < St::KCH; ++j) ld(st.k[j], rk, k_off[j]);
 #pragma unroll
-    for (int j = 0; j < St::VCH; ++j) {
-      ld(st.v[j][0], rv, v_off[j]);
-      ld(st.v[j][1], rv, v_off[j] + p.stride_kv * IES);
-    }
+    for (int j = 0; j < St::KCH; ++j) ld(st.v[j], rv, k_off[j]);
     if (BIAS == kBiasTableF32) {
       // Band of table[h][q - key + N - 1] for q in [q0, q0+BM), key in
       // [kb0, kb0+KB): entry i is index q0 - kb0 - (KB-1) + N - 1 + i;
@@ -236,25 +225,16 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
       }
     }
 #pragma unroll
-    for (int j = 0; j < St::VCH; ++j) {
-      const int job = gtid + kGroup * j;
-      if (St::VJOBS % kGroup == 0 || job < St::VJOBS) {
-        const int kp = 2 * (job % (kKB / 2));
-        const int col = 8 * (job / (kKB / 2));
-        half8v v0, v1, l0, l1;
-        if constexpr (F32IN) {
-          split_f16(st.v[j][0].f, v0, l0);
-          split_f16(st.v[j][1].f, v1, l1);
-        } else {
-          v0 = st.v[j][0].h;
-          v1 = st.v[j][1].h;
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          *reinterpret_cast<half2v*>(&v_l[(col + e) * VLD + kp]) = half2v{v0[e], v1[e]};
-          if constexpr (F32IN)
-            *reinterpret_cast<half2v*>(&v_l[LO + (col + e) * VLD + kp]) = half2v{l0[e], l1[e]};
-        }
+    for (int j = 0; j < St::KCH; ++j) {
+      const int c8 = gtid + kGroup * j;
+      const int at = v_store_at<D>(c8 / (D / 8), c8 % (D / 8));
+      if constexpr (F32IN) {
+        half8v hi, lo;
+        split_f16(st.v[j].f, hi, lo);
+        *reinterpret_cast<half8v*>(&v_l[at]) = hi;
+        *reinterpret_cast<half8v*>(&v_l[LO + at]) = lo;
+      } else {
+        *reinterpret_cast<half8v*>(&v_l[at]) = st.v[j].h;
       }
     }
     if (BIAS == kBiasTableF32) {
@@ -408,14 +388,14 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
     // ---- O^T += V^T P^T ----
 #pragma unroll
     for (int u = 0; u < DT; ++u) {
-      const half_t* vp = &v_l[(32 * u + ql) * VLD + 8 * g];
+      const int vo = v_tr_offset<D>(lane, u);
 #pragma unroll
       for (int cc = 0; cc < 2 * NT; ++cc) {
-        const half8v vh = load_half8(vp + 16 * cc);
+        const half8v vh = v_frag_tr<D>(v_l, vo, cc);
         o[u] = mfma32x32x16(vh, pb[cc], o[u]);
         if constexpr (F32IN) {  // + V_hi P_lo + V_lo P_hi
           o[u] = mfma32x32x16(vh, pl[cc], o[u]);
-          o[u] = mfma32x32x16(load_half8(vp + LO + 16 * cc), pb[cc], o[u]);
+          o[u] = mfma32x32x16(v_frag_tr<D>(v_l + LO, vo, cc), pb[cc], o[u]);
         }
       }
     }
@@ -509,7 +489,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
 template <int D, int BIAS, bool F32IN>
 constexpr int fa2_lds_bytes(int K) {
   constexpr int kb = key_block<D>();
-  const int slot = (kb * (D + 8) + D * (kb + 8)) * 2 * (F32IN ? 2 : 1);
+  const int slot = (kb * (D + 8) + kb * D) * 2 * (F32IN ? 2 : 1);
   const int bias = BIAS == kBiasTableF32 ? (kBM + kb) * 4 : 4;
   return K * 2 * (slot + bias);
 }

@@ -32,4 +32,59 @@ __device__ __forceinline__ float sum_halves(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// V tiles live row-major in LDS, [key][D] halves without padding, and the
+// P V product reads its V^T operand with gfx950's transposing LDS load.
+// 16-byte chunk c of key row r is stored at chunk c ^ vswz<D>(r), which
+// makes both the 16-byte stores and the transposed reads below touch every
+// LDS bank once per 32-lane pass: a pass reads rows r0..r0+3 (r0 % 4 == 0),
+// four chunks each.  D = 32: rows are 16 dwords, four rows fill the banks.
+// D = 64: rows r and r+2 share banks unless bit 1 of r flips chunk bit 2.
+// D = 128: a row spans all banks, so row r % 4 picks one of four 4-chunk
+// sets.
+template <int D>
+__device__ __forceinline__ int vswz(int r) {
+  static_assert(D == 32 || D == 64 || D == 128, "head dim");
+  if constexpr (D == 128) return (r & 3) * 4;
+  else if constexpr (D == 64) return ((r >> 1) & 1) * 4;
+  else return 0;
+}
+
+// Position (halves) of the 8-element V piece of key row r, chunk c.
+template <int D>
+__device__ __forceinline__ int v_store_at(int r, int c) {
+  return r * D + 8 * (c ^ vswz<D>(r));
+}
+
+// ds_read_b64_tr_b16: in each group of 16 lanes, lane 4e + t passes the
+// address of 4 halves (row e, columns 4t..4t+3 of a 4 x 16 tile) and lane j
+// receives column j, the 4 rows' element j.
+__device__ __forceinline__ half4v lds_read_tr16(const half_t* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(const_cast<half_t*>(p)));
+  return __builtin_bit_cast(half4v, r);
+}
+
+// This lane's offset (halves) into a V tile for d tile u: key row
+// 8 (l / 32) + (l % 16) / 4, columns 32u + 16 ((l / 16) % 2) + 4 (l % 4)
+// .. +3, swizzled.  Adding 16 cc or 4 rows leaves the swizzle unchanged
+// (it depends on row bits 0 and 1 only).
+template <int D>
+__device__ __forceinline__ int v_tr_offset(int lane, int u) {
+  const int row = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int cu = 32 * u + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  return row * D + 8 * ((cu >> 3) ^ vswz<D>(row)) + (cu & 7);
+}
+
+// A operand of O^T += V^T P^T for the 16-key chunk cc (off = v_tr_offset
+// of the d tile): lane l gets V[16 cc + 8 (l / 32) + 0..7][32 u + l % 32],
+// two 4-key transposed reads.
+template <int D>
+__device__ __forceinline__ half8v v_frag_tr(const half_t* v_l, int off, int cc) {
+  const half_t* pp = v_l + off + 16 * cc * D;
+  const half4v a = lds_read_tr16(pp);
+  const half4v b = lds_read_tr16(pp + 4 * D);
+  return half8v{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+}
+
 }  // namespace neso
