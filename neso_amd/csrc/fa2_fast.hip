@@ -25,12 +25,14 @@
 //   key groups) fill the remaining gaps.  K and V of a block share one
 //   slot of a 4-slot LDS ring, which leaves one barrier per block and keeps
 //   block i's K in LDS while block i is processed (the slow path recomputes
-//   its scores from there); global loads run one block ahead of the LDS
-//   stores through registers.
-// * V stays row-major in LDS (plain 16-byte stores, chunks swizzled against
-//   bank conflicts) and the V^T operand of P V is read with gfx950's
-//   transposing LDS load, ds_read_b64_tr_b16, instead of being transposed
-//   with register permutes before the store.
+//   its scores from there).
+// * K and V go from global memory straight into LDS (buffer_load_dwordx4
+//   ... lds, no staging registers, no LDS stores): step i issues block
+//   i+2's loads into its free slot before the fused stretch and waits for
+//   them before the step's barrier.  Both tiles are row-major without
+//   padding, 16-byte chunks swizzled against bank conflicts, and the V^T
+//   operand of P V is read with gfx950's transposing LDS load,
+//   ds_read_b64_tr_b16.
 #include "common.h"
 #include "fa2_tiles.h"
 #include "neso_internal.h"
@@ -44,19 +46,43 @@ constexpr int kKB = 64;           // keys per block
 constexpr int kGroup = 256;       // threads per key group (4 waves)
 constexpr float kPSumMax = 4096.f;  // fast-path bound on a lane's block sum of P
 
-template <int D>
-struct FastStage {
-  static constexpr int KCH = kKB * D / 8 / kGroup;  // 8-element K (and V) pieces per thread
-  half8v k[KCH];
-  half8v v[KCH];
-};
-
-// LDS halves of one key group: a 4-slot ring, each slot K [KB][D+8] then
-// V [KB][D] (row-major, 16-byte chunks swizzled; read transposed).
+// LDS halves of one key group: a 4-slot ring, each slot K [KB][D] then
+// V [KB][D], both row-major with 16-byte chunks swizzled (no padding: the
+// blocks arrive by LDS-direct loads, which fill LDS linearly).
 constexpr int kSlots = 4;
 template <int D>
 constexpr int fast_group_lds_halves() {
-  return kSlots * (kKB * (D + 8) + kKB * D);
+  return kSlots * 2 * kKB * D;
+}
+
+// Chunk swizzle of the K rows (D = 64, 8 chunks per row): chunk c of key
+// row r sits at chunk c ^ kswz(r).  A K fragment read takes one chunk from
+// each of 16 rows per 16-lane pass, rows 0..15 of a 32-row tile in
+// kRowPerm order; a 128-byte row covers half the banks, so rows of equal
+// parity need 8 distinct chunk positions, which bits 1..3 of r give.
+__device__ __forceinline__ int kswz(int r) { return (r >> 1) & 7; }
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// 16 bytes per lane from the buffer into LDS (buffer_load_dwordx4 ... lds):
+// lane l's bytes land at LDS byte address lds + 16 l.  Written as asm so
+// that the compiler does not make the kernel's LDS reads wait for it (it
+// cannot tell that they read other slots); the kernel orders these writes
+// itself with s_waitcnt vmcnt(0) and a barrier before the slot is read.
+// Vector loads only; M0 holds the LDS base (one wait state after writing
+// it).
+__device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(r)
+      : "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const half_t* p) {
+  return (uint32_t)(size_t)(__attribute__((address_space(3))) const half_t*)p;
 }
 
 template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT>
@@ -64,12 +90,11 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   constexpr int NT = kKB / 32;  // 32-key tiles per block
   constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
-  constexpr int KLD = D + 8;    // LDS row stride of K (halves)
-  constexpr int KSLOT = kKB * KLD;
+  constexpr int KSLOT = kKB * D;
   constexpr int VSLOT = kKB * D;
   constexpr int GLDS = fast_group_lds_halves<D>();
-  using St = FastStage<D>;
-  static_assert(St::KCH >= 1 && kKB * D % (8 * kGroup) == 0, "tile split");
+  constexpr int LCH = kKB * D / 8 / 64 / 4;  // 1 KiB load instructions per wave and matrix
+  static_assert(D == 64 && LCH >= 1 && kKB * D * 2 == 4 * LCH * 1024, "tile split");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
 
   const int tid = threadIdx.x;
@@ -118,51 +143,35 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   const int my_n = nblk > kg ? (nblk - kg + KSPLIT - 1) / KSPLIT : 0;
   const int iters = (nblk + KSPLIT - 1) / KSPLIT;  // uniform over the workgroup
 
-  uint32_t k_off[St::KCH];
-#pragma unroll
-  for (int j = 0; j < St::KCH; ++j) {
-    const int c8 = gtid + kGroup * j;
-    k_off[j] = ((c8 / (D / 8)) * p.stride_kv + 8 * (c8 % (D / 8))) * 2;
-  }
+  half_t* gbase = &smem[kg * GLDS];
+  auto kslot = [&](int s) { return gbase + s * (KSLOT + VSLOT); };
+  auto vslot = [&](int s) { return gbase + s * (KSLOT + VSLOT) + KSLOT; };
 
-  // Global -> registers.  Loads for blocks past the group's last reload
-  // that block (in range, never used).
-  auto gload = [&](St& st, int i) {
-    const int blk = blk0 + kg + KSPLIT * max(0, min(i, my_n - 1));
-    const int kb0 = blk * kKB;
+  // Global -> LDS directly (buffer_load_dwordx4 ... lds).  One instruction
+  // fills 1 KiB of LDS, lane l's 16 bytes at byte 16 l, i.e. 8 rows of a
+  // block; so lane l loads the chunk that the swizzled layout puts at its
+  // position: row 8x + l / 8 (x = instruction of the group), position l % 8,
+  // chunk (l % 8) ^ swizzle(row).  Rows past N read as zeros.
+  uint32_t kgo[LCH], vgo[LCH];
+#pragma unroll
+  for (int j = 0; j < LCH; ++j) {
+    const int row = 8 * (LCH * wave + j) + (lane >> 3), pos = lane & 7;
+    kgo[j] = (row * p.stride_kv + 8 * (pos ^ kswz(row))) * 2;
+    vgo[j] = (row * p.stride_kv + 8 * (pos ^ vswz<D>(row))) * 2;
+  }
+  auto lds_load = [&](int i, int s) {
+    const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
     // readfirstlane: min/max of scalars may be formed on the VALU, and a
     // descriptor in VGPRs would wrap every load in a waterfall loop.
     const uint32_t bytes = __builtin_amdgcn_readfirstlane(max(0, min(N - kb0, kKB)) * p.stride_kv * 2);
     const rsrc_t rk = make_rsrc(Kh + (int64_t)kb0 * p.stride_kv, bytes);
     const rsrc_t rv = make_rsrc(Vh + (int64_t)kb0 * p.stride_kv, bytes);
 #pragma unroll
-    for (int j = 0; j < St::KCH; ++j) st.k[j] = buf_load_half8(rk, k_off[j]);
-#pragma unroll
-    for (int j = 0; j < St::KCH; ++j) st.v[j] = buf_load_half8(rv, k_off[j]);
-  };
-
-  St st;  // one block in flight between global memory and LDS
-  half_t* gbase = &smem[kg * GLDS];
-  auto kslot = [&](int s) { return gbase + s * (KSLOT + VSLOT); };
-  auto vslot = [&](int s) { return gbase + s * (KSLOT + VSLOT) + KSLOT; };
-
-  // Registers -> LDS: K row-major [key][KLD], V row-major [key][D] with
-  // swizzled chunks, 16 bytes per store.  One store per piece so that the
-  // fused step can spread them over its MFMA slots: pieces 0..KCH-1 store
-  // K, the rest V.
-  constexpr int kStorePieces = 2 * St::KCH;
-  auto sstore_piece = [&](const St& st, half_t* k_l, half_t* v_l, int piece) {
-    const int j = piece % St::KCH;
-    const int c8 = gtid + kGroup * j;
-    const int r = c8 / (D / 8), c = c8 % (D / 8);
-    if (piece < St::KCH)
-      *reinterpret_cast<half8v*>(&k_l[r * KLD + 8 * c]) = st.k[j];
-    else
-      *reinterpret_cast<half8v*>(&v_l[v_store_at<D>(r, c)]) = st.v[j];
-  };
-  auto sstore = [&](const St& st, half_t* k_l, half_t* v_l) {
-#pragma unroll
-    for (int piece = 0; piece < kStorePieces; ++piece) sstore_piece(st, k_l, v_l, piece);
+    for (int j = 0; j < LCH; ++j) {
+      const int x = LCH * wave + j;
+      lds_dma16(rk, __builtin_amdgcn_readfirstlane(lds_addr(kslot(s) + x * 8 * D)), kgo[j]);
+      lds_dma16(rv, __builtin_amdgcn_readfirstlane(lds_addr(vslot(s) + x * 8 * D)), vgo[j]);
+    }
   };
 
   float m_run = -INFINITY;  // running max (log2 units); -inf: the row has seen no key yet
@@ -182,13 +191,19 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   for (int u = 0; u < DT; ++u) vtr[u] = v_tr_offset<D>(lane, u);
   auto vfrag = [&](const half_t* v_l, int u, int cc) { return v_frag_tr<D>(v_l, vtr[u], cc); };
 
+  // This lane's K fragment offsets (halves) per k-step: row krow (+32 t,
+  // which keeps the swizzle), chunk 2 ks + g.
+  int koff[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = krow * D + 8 * ((2 * ks + g) ^ kswz(krow));
+
   auto qk = [&](float16v(&s)[NT], const half_t* k_l) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const half_t* kp = &k_l[(32 * t + krow) * KLD + 8 * g];
-      s[t] = mfma32x32x16(load_half8(kp), qf[0], float16v{});
+      s[t] = mfma32x32x16(load_half8(k_l + koff[0] + 32 * t * D), qf[0], float16v{});
 #pragma unroll
-      for (int ks = 1; ks < KS; ++ks) s[t] = mfma32x32x16(load_half8(kp + 16 * ks), qf[ks], s[t]);
+      for (int ks = 1; ks < KS; ++ks)
+        s[t] = mfma32x32x16(load_half8(k_l + koff[ks] + 32 * t * D), qf[ks], s[t]);
     }
   };
 
@@ -231,20 +246,18 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // cvt + dot2 of slot j-1) so that no VALU op waits on the one before it.
   // sched_barrier pins that order.  Returns the lane's sum of fp16 pcur.
   auto fused = [&](const float16v(&s)[NT], float16v(&sn)[NT], const half_t* k_l,
-                   const half_t* v_l, const half8v(&pprev)[2 * NT], half8v(&pcur)[2 * NT],
-                   int i) {
+                   const half_t* v_l, const half8v(&pprev)[2 * NT], half8v(&pcur)[2 * NT]) {
     constexpr int NQ = KS * NT;       // score MFMAs
     constexpr int NP = DT * 2 * NT;   // P V MFMAs
     constexpr int NJ = NQ + NP;       // slots
     constexpr int SPJ = 32 / NJ;      // scores per slot
     constexpr int AHEAD = 4;
     static_assert(NQ == NP && 32 % NJ == 0 && SPJ == 2, "slot split");
-    const half_t* kp = &k_l[krow * KLD + 8 * g];
     // Fragment of slot j: even j -> K (tile q % NT, k-step q / NT),
     // odd j -> V^T (tile q % DT, key chunk q / DT), q = j / 2.
     auto frag = [&](int j) {
       const int q = j / 2;
-      return (j % 2 == 0) ? load_half8(kp + 32 * (q % NT) * KLD + 16 * (q / NT))
+      return (j % 2 == 0) ? load_half8(k_l + koff[q / NT] + 32 * (q % NT) * D)
                           : vfrag(v_l, q % DT, q / DT);
     };
     auto score = [&](int sc) {  // score sc (0..31) of this lane
@@ -285,12 +298,6 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
         pcur[cc][e + 1] = h[1];
         dot2_acc(acc[cc], h);
       }
-      // Block i+2 into LDS (its slot is not read in this step) and the loads
-      // of block i+3, in the second half of the slots so that the loads
-      // issued a step ago have landed.
-      if (j >= NJ - kStorePieces - 2 && j < NJ - 2)
-        sstore_piece(st, kslot((i + 2) & 3), vslot((i + 2) & 3), j - (NJ - kStorePieces - 2));
-      if (j == NJ - 2) gload(st, i + 3);
       __builtin_amdgcn_sched_barrier(0);
     }
     {
@@ -368,49 +375,50 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       for (int cc = 0; cc < 2 * NT; ++cc) o[u] = mfma32x32x16(vfrag(v_l, u, cc), pb[cc], o[u]);
   };
 
-  // One block step i: scores of block i+1 into sn, softmax of block i
-  // (scores in s, P into pcur), P V of block i-1 (P in pprev), block i+2
-  // into LDS and the loads of block i+3 (inside the fused stretch), barrier.  Block j lives in LDS slot j % 4,
-  // so the four blocks a step touches (i-1, i, i+1, i+2) never share one.
+  // One block step i: loads of block i+2 straight into its LDS slot, then
+  // scores of block i+1 into sn, softmax of block i (scores in s, P into
+  // pcur) and P V of block i-1 (P in pprev) in the fused stretch, then a
+  // wait for the loads and the barrier that publishes block i+2.  Block j
+  // lives in LDS slot j % 4, so the four blocks a step touches (i-1, i, i+1,
+  // i+2) never share one; slot (i+2) % 4 last served block i-2, whose P V
+  // ran in step i-1.
   auto body = [&](int i, float16v(&s)[NT], float16v(&sn)[NT], half8v(&pprev)[2 * NT],
                   half8v(&pcur)[2 * NT]) {
     const int si = i & 3;
     if (i < my_n) {
+      if (i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
       const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
       // Some key of the block is past N or outside some query's window.
       const bool masked =
           (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
       // After the group's last block the next scores come from a stale
       // slot and are never used.
-      float ls = fused(s, sn, kslot((i + 1) & 3), vslot((i + 3) & 3), pprev, pcur, i);
+      float ls = fused(s, sn, kslot((i + 1) & 3), vslot((i + 3) & 3), pprev, pcur);
       // ls enters the condition so that the softmax cannot sink below it.
       if (__any(masked || !(ls <= thr))) ls = slow(si, kb0, masked, pcur);
       l_run += ls;
     }
-    // Steps past the group's last block store and load nothing: no later
-    // step reads those blocks, and the last block's V (read by the P V
-    // after the loop) stays in place.  (A store here would also let the
-    // compiler hoist the stores, and with them a wait for this step's
-    // loads, to the top of every step.)
+    // Steps past the group's last block load nothing: no later step reads
+    // those blocks, and the last block's V (read by the P V after the loop)
+    // stays in place.
+    wait_vmem();
     lds_barrier();
   };
 
-  // ---- prologue: blocks 0 and 1 into LDS, 2 in flight, scores of 0 ----
-  {
-    St st1;  // blocks 0 and 1 in one round trip to memory
-    gload(st, 0);
-    gload(st1, 1);
-    sstore(st, kslot(0), vslot(0));
-    sstore(st1, kslot(1), vslot(1));
-  }
-  gload(st, 2);
+  // ---- prologue: blocks 0 and 1 into LDS in one round trip, scores of 0 ----
+  if (my_n > 0) lds_load(0, 0);
+  if (my_n > 1) lds_load(1, 1);
+  wait_vmem();
   lds_barrier();
   float16v sa[NT], sb[NT];
-  qk(sa, kslot(0));
   half8v pa[2 * NT], pb2[2 * NT];
 
   // ---- step 0, peeled: block 0 is every row's first visible block, so its
-  // softmax is the slow path on the scores above; scores of block 1 ----
+  // softmax is the slow path on its exact scores; scores of block 1; loads
+  // of block 2.  (Scores of blocks a group does not have come from stale
+  // slots and are never used.) ----
+  if (my_n > 2) lds_load(2, 2);
+  qk(sa, kslot(0));
   if (my_n > 0) {
     const int kb0 = (blk0 + kg) * kKB;
     const bool masked =
@@ -418,8 +426,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     qk(sb, kslot(1));
     l_run += slow_scores(sa, kb0, masked, pb2);
   }
-  sstore(st, kslot(2), vslot(2));
-  gload(st, 3);
+  wait_vmem();
   lds_barrier();
 
   // Steps 1, 2, ...: unrolled by two so that the score and P arrays swap
