@@ -445,7 +445,45 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   }
 
   // ---- merge the key groups through LDS ----
-  if constexpr (KSPLIT > 1) {
+  // Two key groups and two 32-column tiles of O: group g finishes tile g.
+  // Each group publishes (m, l) and the tile the other group finishes, so
+  // both merge and store half of O.
+  constexpr bool kSplitMerge = KSPLIT == 2 && DT == 2;
+  if constexpr (kSplitMerge) {
+    // The partials below overwrite the start of the LDS, where the
+    // last-block P V above may still be reading V.
+    lds_barrier();
+    constexpr int SLOTS = 16 + 2;
+    static_assert(sizeof(smem) >= 8 * SLOTS * 64 * sizeof(float), "merge buffer");
+    float* const red = reinterpret_cast<float*>(smem) + lane;
+    float* mine = red + (size_t)(4 * kg + wave) * SLOTS * 64;
+    const float* other = red + (size_t)(4 * (1 - kg) + wave) * SLOTS * 64;
+    mine[0] = m_run;
+    mine[64] = l_run;
+    if (kg == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mine[(2 + r) * 64] = o[1][r];
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mine[(2 + r) * 64] = o[0][r];
+    }
+    lds_barrier();
+    const float m1 = other[0];
+    const float l1 = other[64];
+    const float mm = fmaxf(m_run, m1);
+    const float mu = (mm == -INFINITY) ? 0.f : mm;
+    const float a0 = fast_exp2(m_run - mu);
+    const float a1 = fast_exp2(m1 - mu);
+    m_run = mm;
+    l_run = l_run * a0 + l1 * a1;
+    if (kg == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[0][r] = o[0][r] * a0 + other[(2 + r) * 64] * a1;
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[1][r] = o[1][r] * a0 + other[(2 + r) * 64] * a1;
+    }
+  } else if constexpr (KSPLIT > 1) {
     // The partials below overwrite the start of the LDS, where group 0's
     // last-block P V above may still be reading V^T.
     lds_barrier();
@@ -491,6 +529,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
                                (uint32_t)qrows * p.stride_o * ES);
 #pragma unroll
   for (int u = 0; u < DT; ++u) {
+    if (kSplitMerge && u != kg) continue;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int col = 32 * u + 8 * b + 4 * g;
