@@ -581,11 +581,11 @@ bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32) {
 }
 
 bool fa2_fast_preferred(bool causal, int32_t N) {
-  // Measured on MI355X (B*H = 16..64, d = 64): the fast kernel is 2-9%
-  // faster from N = 2048 up without a mask; below that its deeper prologue
-  // costs more than its cheaper blocks save, and causal rows gain more from
-  // the generic kernel's per-wave skipping of invisible blocks.
-  return !causal && N >= 1536;
+  // Measured on MI355X (d = 64, B*H = 8..64): the fast kernel is ahead from
+  // N = 128 up without a mask (3-15%) and for causal rows from N = 1024
+  // (7-25%, growing with N); for shorter causal rows the generic kernel's
+  // per-wave skipping of invisible blocks wins (N = 256: 8.1 vs 8.9 us).
+  return !causal || N >= 1024;
 }
 
 hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, int ksplit,

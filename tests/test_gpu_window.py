@@ -74,8 +74,11 @@ def test_window_zero_is_identity(gpu):
     assert (out.cpu() - v.float()).abs().max().item() <= 1e-6
 
 
-def test_full_window_equals_plain_and_causal(gpu):
-    """(N, N) gives the unmasked kernel's result, (N, 0) the causal one."""
+def test_full_window_equals_plain_and_causal(gpu, monkeypatch):
+    """(N, N) gives the unmasked kernel's result, (N, 0) the causal one.
+    Windows run the generic kernel, so the plain and causal calls are pinned
+    to it too (the fast kernel rounds differently, within the 2e-3 bar)."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "0")
     n, h, d = 1000, 2, 64
     q, k, v = I.fa2_inputs(1, h, n, d, seed=11)
     plain = neso_amd.attention(q.to(DEV), k.to(DEV), v.to(DEV))
