@@ -450,17 +450,19 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_kernel(W4Args a) {
 // flight from the start.  One persistent workgroup per CU owns row tiles
 // blockIdx.x + i * gridDim.x (16 rows each, i < T).  Its WV waves split K
 // (wave w takes chunk quads [w*QW, (w+1)*QW)) and issue all their weight
-// and scale loads for all T tiles before anything else waits (plain loads:
+// and scale loads for all T tiles, after X, before anything else waits (plain loads:
 // the non-temporal hint measured slower for these 64-byte row pieces).  X is copied
 // once per workgroup into LDS, already in MFMA A-fragment order (slot
 // (4q + t) * 64 + lane holds X[m][32(4q+t) + 8g + {0,4,1,5,2,6,3,7}] for
 // lane = m + 16g), so the per-tile A operand is one conflict-free
 // ds_read_b128 per MFMA.  MFMA, transpose and dequantisation are those of
 // w4a16_skinny_kernel.  The WV partial tiles are reduced through LDS.
+// (The slot's row index is XOR-swizzled; see the X loads below.)
 constexpr int kLdsQuads = 32;  // K <= 4096
 
 template <int WV, int T, int QWMAX>
 __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) {
+  static_assert(QWMAX <= 4, "a quad's scales come from one of the four lane groups");
   constexpr uint32_t kOut = 0x80000000u;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -478,9 +480,37 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
   __shared__ half8v xs[kLdsQuads * 4 * kWave];
   __shared__ float red[T][WV][4][kWave];
 
+  // X first: loads complete in issue order, so X (L2-resident) reaches LDS
+  // while the weight burst is still arriving; issued after the weights, it
+  // waited behind them (measured: 15.7 -> 14.2 us at M = 16).  Each wave
+  // instruction reads 1 KiB of one X row (piece e: row m, pieces pp of 8
+  // halves; 16 rows x 64 B per instruction measured 14.2 vs 12.9 us).  Piece
+  // (m, chunk ct, quarter g) goes to A-fragment slot ct*64 + 16g + m', with
+  // the row index swizzled, m' = m ^ (4 (ct % 4) + g), so that the 64
+  // same-row stores of an instruction and the 16-lane fragment reads both
+  // spread over all banks.
+  constexpr int kXPer = (kLdsQuads * 4 * kWave) / (WV * kWave);
+  const rsrc_t rx = make_rsrc(a.X, (uint32_t)((a.M - 1) * a.ldx + a.K) * 2u);
+  half8v xv[kXPer];
+  uint32_t xslot[kXPer];
+#pragma unroll
+  for (int i = 0; i < kXPer; ++i) {
+    const uint32_t e = threadIdx.x + i * WV * kWave;
+    const uint32_t m = e / (4 * 4 * kLdsQuads), pp = e % (4 * 4 * kLdsQuads);
+    const uint32_t ct = pp >> 2, g = pp & 3;
+    const uint32_t oob = ((int)ct < C && (int)m < a.M) ? 0u : kOut;
+    xv[i] = buf_load_half8(rx, ((m * (uint32_t)a.ldx + 8u * pp) * 2u) | oob);
+    xslot[i] = ct * 64 + 16 * g + (m ^ (4 * (ct & 3) + g));
+  }
+
   // All weight and scale loads of this wave, all tiles.
+  // Scales: one 8-byte load per lane and tile, lane (li, lg) taking quad
+  // q0 + lg of row li (32 contiguous bytes per row instead of 8, and no
+  // four lanes loading the same bytes); quad qi reaches lane (li, *) from
+  // lane (li, qi) by ds_bpermute (measured 12.9 -> 11.7 us at M = 16).
+  typedef uint32_t uint2v __attribute__((ext_vector_type(2)));
   uint4v w[T][QWMAX];
-  half4v sc[T][QWMAX];
+  uint2v scw[T];
 #pragma unroll
   for (int i = 0; i < T; ++i) {
     const int tile = blockIdx.x + i * gridDim.x;
@@ -496,30 +526,19 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
       const uint32_t wo = (li * (uint32_t)KW * 4u + c * 16u) | (live && (int)c < cend ? 0u : kOut);
       w[i][qi] = __builtin_bit_cast(
           uint4v, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 0));
-      const uint32_t so = ((li * (uint32_t)SG + cq) * 2u) | (live && (int)cq < cend ? 0u : kOut);
-      sc[i][qi] = __builtin_bit_cast(
-          half4v, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
     }
-  }
-
-  // X (L2-resident) after the weights, so the HBM requests leave first:
-  // piece p of the workgroup's share covers LDS slot p = (4q+t)*64 + m + 16g.
-  constexpr int kXPer = (kLdsQuads * 4 * kWave) / (WV * kWave);
-  const rsrc_t rx = make_rsrc(a.X, (uint32_t)((a.M - 1) * a.ldx + a.K) * 2u);
-  half8v xv[kXPer];
-#pragma unroll
-  for (int i = 0; i < kXPer; ++i) {
-    const uint32_t slot = threadIdx.x + i * WV * kWave;
-    const uint32_t ct = slot >> 6, ln = slot & 63, m = ln & 15, g = ln >> 4;
-    const uint32_t oob = ((int)ct < C && (int)m < a.M) ? 0u : kOut;
-    xv[i] = buf_load_half8(rx, ((m * (uint32_t)a.ldx + 32u * ct + 8u * g) * 2u) | oob);
+    {
+      const uint32_t cq = 4 * (q0 + lg);
+      const uint32_t so = ((li * (uint32_t)SG + cq) * 2u) | (lg < QW && (int)cq < cend ? 0u : kOut);
+      scw[i] = __builtin_bit_cast(uint2v, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
+    }
   }
 
   // X into LDS in A-fragment order.
 #pragma unroll
   for (int i = 0; i < kXPer; ++i) {
     const half8v x = xv[i];
-    xs[threadIdx.x + i * WV * kWave] = half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+    xs[xslot[i]] = half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
   }
   lds_barrier();
 
@@ -532,11 +551,15 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
       if (qi >= QW) break;  // uniform
       const int q = q0 + qi;
       uint32_t wt[4] = {w[i][qi][0], w[i][qi][1], w[i][qi][2], w[i][qi][3]};
+      const int src = (li + 16 * qi) * 4;
+      const half4v sq = __builtin_bit_cast(
+          half4v, uint2v{(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)scw[i][0]),
+                         (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)scw[i][1])});
       transpose_rows4(wt[0], wt[1], wt[2], wt[3]);
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const half8v xa = xs[(4 * q + t) * kWave + lane];
-        const half_t s = sc[i][qi][t];
+        const half8v xa = xs[(4 * q + t) * kWave + 16 * lg + (li ^ (4 * t + lg))];
+        const half_t s = sq[t];
         const half2v s1 = {s, s};
         const half_t s16v = s * (half_t)0.0625f;
         const half2v s16 = {s16v, s16v};
