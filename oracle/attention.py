@@ -18,7 +18,8 @@ import torch
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, *,
               causal: bool = False, logit_bias: torch.Tensor | None = None,
               window: tuple[int, int] | None = None,
-              dtype: torch.dtype = torch.float32, chunk_rows: int = 1024) -> torch.Tensor:
+              dtype: torch.dtype = torch.float32, chunk_rows: int = 1024,
+              query_rows: torch.Tensor | None = None) -> torch.Tensor:
     """Closed form O = softmax(Q K^T * scale [+ logit_bias], mask) V on the CPU.
 
     Follows tests/test_flash_attention.py:296-339 (scores = q.k * scale, max
@@ -30,21 +31,29 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float, *
     masked logits get -inf here, -1e9 in the reference: identical results
     while every row keeps its diagonal, which non-negative windows do).
     Inputs are upcast to ``dtype``; rows are processed in chunks so the score
-    matrix stays bounded.  Returns ``dtype`` [..., N, d].
+    matrix stays bounded.  Returns ``dtype`` [..., N, d], or, with
+    ``query_rows`` (1-D indices), only those query rows [..., len, d]
+    (masks use the rows' positions; for parity checks at full sizes).
     """
     q = q.to("cpu", dtype)
     k = k.to("cpu", dtype)
     v = v.to("cpu", dtype)
     n = q.shape[-2]
+    rows_all = torch.arange(n) if query_rows is None else query_rows.to("cpu", torch.long)
+    if query_rows is not None:
+        q = q[..., rows_all, :]
+        if logit_bias is not None:
+            logit_bias = logit_bias[..., rows_all, :]
+    nq = q.shape[-2]
     out = torch.empty(q.shape, dtype=dtype)
     kt = k.transpose(-1, -2)
-    for r0 in range(0, n, chunk_rows):
-        r1 = min(n, r0 + chunk_rows)
+    for r0 in range(0, nq, chunk_rows):
+        r1 = min(nq, r0 + chunk_rows)
         s = torch.matmul(q[..., r0:r1, :], kt) * scale
         if logit_bias is not None:
             s = s + logit_bias[..., r0:r1, :].to(dtype)
         if causal or window is not None:
-            rows = torch.arange(r0, r1).unsqueeze(1)
+            rows = rows_all[r0:r1].unsqueeze(1)
             cols = torch.arange(n).unsqueeze(0)
             left, right = window if window is not None else (n, 0)
             s = s.masked_fill((cols > rows + right) | (cols < rows - left), float("-inf"))

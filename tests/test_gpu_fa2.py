@@ -88,6 +88,22 @@ def test_baseline_d128_causal(gpu):
         assert err <= TOL, ((b, h), err)
 
 
+def test_baseline_d128_causal_all_slices_sampled_rows(gpu):
+    """Config 3 at full size on all 64 (b, h) slices: 48 query rows each
+    (first and last rows, both sides of the 64-key and 128-query block
+    boundaries, random rows) against the oracle restricted to those rows."""
+    cfg = I.FA2_D128
+    q, k, v = I.fa2_inputs(**cfg, seed=1)
+    out = gpu_attention(q, k, v, causal=True)
+    n = cfg["N"]
+    fixed = torch.tensor([0, 1, 63, 64, 127, 128, 129, 2047, 2048, n - 65, n - 64, n - 2, n - 1])
+    rnd = torch.randint(0, n, (35,), generator=torch.Generator().manual_seed(4))
+    rows = torch.unique(torch.cat([fixed, rnd]))
+    ref = A.attention(q, k, v, 1 / math.sqrt(cfg["d"]), causal=True, query_rows=rows)
+    err = (out[:, :, rows, :] - ref).abs().max().item()
+    assert err <= TOL, err
+
+
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize("d", [32, 64, 128])
 @pytest.mark.parametrize("n", [1, 7, 100, 191, 1500])

@@ -35,6 +35,18 @@ def test_closed_form_matches_sdpa(n, d, causal):
     assert torch.allclose(out, ref, atol=1e-10, rtol=0)
 
 
+@pytest.mark.parametrize("causal,window", [(False, None), (True, None), (False, (9, 4))])
+def test_query_rows_subset(causal, window):
+    """query_rows gives exactly those rows of the full result (SDPA-checked
+    above), with causal and window masks at the rows' own positions."""
+    q, k, v = I.fa2_inputs(1, 3, 200, 64, seed=21)
+    rows = torch.tensor([0, 1, 63, 64, 117, 198, 199])
+    full = A.attention(q, k, v, 0.125, causal=causal, window=window, dtype=torch.float64)
+    sub = A.attention(q, k, v, 0.125, causal=causal, window=window, dtype=torch.float64,
+                      query_rows=rows)
+    assert torch.equal(sub, full[..., rows, :])
+
+
 @pytest.mark.parametrize("n,d", [(64, 32), (128, 64), (256, 64), (128, 128)])
 def test_golden_reference_rows(golden_dir, n, d):
     """tests/test_flash_attention.py:268-275 inputs, :296-339 expected rows."""
