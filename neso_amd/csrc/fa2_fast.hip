@@ -42,9 +42,16 @@ namespace neso {
 namespace {
 
 constexpr int kBM = 128;          // queries per workgroup
-constexpr int kKB = 64;           // keys per block
 constexpr int kGroup = 256;       // threads per key group (4 waves)
 constexpr float kPSumMax = 4096.f;  // fast-path bound on a lane's block sum of P
+
+// Keys per block: 64 for head_dim 64, 32 for head_dim 128.  Either way a
+// block step carries 16 MFMAs per wave (8 for its scores, 8 for its P V)
+// and a K + V slot is 16 KiB, so two key groups of four slots fit in LDS.
+template <int D>
+constexpr int fast_kb() {
+  return D == 128 ? 32 : 64;
+}
 
 // LDS halves of one key group: a 4-slot ring, each slot K [KB][D] then
 // V [KB][D], both row-major with 16-byte chunks swizzled (no padding: the
@@ -52,15 +59,20 @@ constexpr float kPSumMax = 4096.f;  // fast-path bound on a lane's block sum of 
 constexpr int kSlots = 4;
 template <int D>
 constexpr int fast_group_lds_halves() {
-  return kSlots * 2 * kKB * D;
+  return kSlots * 2 * fast_kb<D>() * D;
 }
 
-// Chunk swizzle of the K rows (D = 64, 8 chunks per row): chunk c of key
-// row r sits at chunk c ^ kswz(r).  A K fragment read takes one chunk from
-// each of 16 rows per 16-lane pass, rows 0..15 of a 32-row tile in
-// kRowPerm order; a 128-byte row covers half the banks, so rows of equal
-// parity need 8 distinct chunk positions, which bits 1..3 of r give.
-__device__ __forceinline__ int kswz(int r) { return (r >> 1) & 7; }
+// Chunk swizzle of the K rows: chunk c of key row r sits at chunk
+// c ^ kswz(r).  A K fragment read takes one chunk from each of 16 rows per
+// 16-lane pass, rows 0..15 of a 32-row tile in kRowPerm order.  D = 64: a
+// 128-byte row covers half the banks, so rows of equal parity need 8
+// distinct chunk positions, which bits 1..3 of r give.  D = 128: a row
+// covers all banks, so the 16 rows need 16 positions, bits 0..3 of r.
+template <int D>
+__device__ __forceinline__ int kswz(int r) {
+  static_assert(D == 64 || D == 128, "head dim");
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+}
 
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
@@ -87,6 +99,7 @@ __device__ __forceinline__ uint32_t lds_addr(const half_t* p) {
 
 template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT>
 __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
+  constexpr int kKB = fast_kb<D>();  // keys per block
   constexpr int NT = kKB / 32;  // 32-key tiles per block
   constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
@@ -94,7 +107,9 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   constexpr int VSLOT = kKB * D;
   constexpr int GLDS = fast_group_lds_halves<D>();
   constexpr int LCH = kKB * D / 8 / 64 / 4;  // 1 KiB load instructions per wave and matrix
-  static_assert(D == 64 && LCH >= 1 && kKB * D * 2 == 4 * LCH * 1024, "tile split");
+  constexpr int CPR = D / 8;      // 16-byte chunks per K/V row
+  constexpr int RPI = 64 / CPR;   // rows per 1 KiB load instruction
+  static_assert(LCH >= 1 && kKB * D * 2 == 4 * LCH * 1024 && RPI * D == 512, "tile split");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
 
   const int tid = threadIdx.x;
@@ -148,15 +163,15 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   auto vslot = [&](int s) { return gbase + s * (KSLOT + VSLOT) + KSLOT; };
 
   // Global -> LDS directly (buffer_load_dwordx4 ... lds).  One instruction
-  // fills 1 KiB of LDS, lane l's 16 bytes at byte 16 l, i.e. 8 rows of a
+  // fills 1 KiB of LDS, lane l's 16 bytes at byte 16 l, i.e. RPI rows of a
   // block; so lane l loads the chunk that the swizzled layout puts at its
-  // position: row 8x + l / 8 (x = instruction of the group), position l % 8,
-  // chunk (l % 8) ^ swizzle(row).  Rows past N read as zeros.
+  // position: row RPI x + l / CPR (x = instruction of the group), position
+  // l % CPR, chunk (l % CPR) ^ swizzle(row).  Rows past N read as zeros.
   uint32_t kgo[LCH], vgo[LCH];
 #pragma unroll
   for (int j = 0; j < LCH; ++j) {
-    const int row = 8 * (LCH * wave + j) + (lane >> 3), pos = lane & 7;
-    kgo[j] = (row * p.stride_kv + 8 * (pos ^ kswz(row))) * 2;
+    const int row = RPI * (LCH * wave + j) + lane / CPR, pos = lane % CPR;
+    kgo[j] = (row * p.stride_kv + 8 * (pos ^ kswz<D>(row))) * 2;
     vgo[j] = (row * p.stride_kv + 8 * (pos ^ vswz<D>(row))) * 2;
   }
   auto lds_load = [&](int i, int s) {
@@ -169,8 +184,8 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 #pragma unroll
     for (int j = 0; j < LCH; ++j) {
       const int x = LCH * wave + j;
-      lds_dma16(rk, __builtin_amdgcn_readfirstlane(lds_addr(kslot(s) + x * 8 * D)), kgo[j]);
-      lds_dma16(rv, __builtin_amdgcn_readfirstlane(lds_addr(vslot(s) + x * 8 * D)), vgo[j]);
+      lds_dma16(rk, __builtin_amdgcn_readfirstlane(lds_addr(kslot(s) + x * RPI * D)), kgo[j]);
+      lds_dma16(rv, __builtin_amdgcn_readfirstlane(lds_addr(vslot(s) + x * RPI * D)), vgo[j]);
     }
   };
 
@@ -195,7 +210,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // which keeps the swizzle), chunk 2 ks + g.
   int koff[KS];
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) koff[ks] = krow * D + 8 * ((2 * ks + g) ^ kswz(krow));
+  for (int ks = 0; ks < KS; ++ks) koff[ks] = krow * D + 8 * ((2 * ks + g) ^ kswz<D>(krow));
 
   auto qk = [&](float16v(&s)[NT], const half_t* k_l) {
 #pragma unroll
@@ -244,15 +259,17 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // steps; fragments are read AHEAD slots early; every slot carries the
   // VALU work of SPJ scores, staggered (fma of slot j+1, exp of slot j,
   // cvt + dot2 of slot j-1) so that no VALU op waits on the one before it.
-  // sched_barrier pins that order.  Returns the lane's sum of fp16 pcur.
+  // sched_barrier pins that order.  With one score per slot (head_dim 128)
+  // a pair of scores is converted every second slot.  Returns the lane's
+  // sum of fp16 pcur.
   auto fused = [&](const float16v(&s)[NT], float16v(&sn)[NT], const half_t* k_l,
                    const half_t* v_l, const half8v(&pprev)[2 * NT], half8v(&pcur)[2 * NT]) {
     constexpr int NQ = KS * NT;       // score MFMAs
     constexpr int NP = DT * 2 * NT;   // P V MFMAs
     constexpr int NJ = NQ + NP;       // slots
-    constexpr int SPJ = 32 / NJ;      // scores per slot
+    constexpr int SPJ = 16 * NT / NJ;  // scores per slot
     constexpr int AHEAD = 4;
-    static_assert(NQ == NP && 32 % NJ == 0 && SPJ == 2, "slot split");
+    static_assert(NQ == NP && 16 * NT == SPJ * NJ && (SPJ == 1 || SPJ == 2), "slot split");
     // Fragment of slot j: even j -> K (tile q % NT, k-step q / NT),
     // odd j -> V^T (tile q % DT, key chunk q / DT), q = j / 2.
     auto frag = [&](int j) {
@@ -260,7 +277,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       return (j % 2 == 0) ? load_half8(k_l + koff[q / NT] + 32 * (q % NT) * D)
                           : vfrag(v_l, q % DT, q / DT);
     };
-    auto score = [&](int sc) {  // score sc (0..31) of this lane
+    auto score = [&](int sc) {  // score sc (0..16 NT - 1) of this lane
       const int cc = sc / 8;
       return s[cc >> 1][8 * (cc & 1) + sc % 8];
     };
@@ -270,9 +287,17 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     float acc[2 * NT];
 #pragma unroll
     for (int cc = 0; cc < 2 * NT; ++cc) acc[cc] = 0.f;
-    float ev[NJ][2], pv[NJ][2];
-    ev[0][0] = __builtin_fmaf(score(0), c, -m_use);
-    ev[0][1] = __builtin_fmaf(score(1), c, -m_use);
+    float ev[NJ][SPJ], pv[NJ][SPJ];
+    // Scores sc, sc + 1 into pcur (fp16) and the lane's sum.
+    auto pack = [&](int sc, float x0, float x1) {
+      const int cc = sc / 8, e = sc % 8;
+      const half2v h = {(half_t)x0, (half_t)x1};
+      pcur[cc][e] = h[0];
+      pcur[cc][e + 1] = h[1];
+      dot2_acc(acc[cc], h);
+    };
+#pragma unroll
+    for (int e = 0; e < SPJ; ++e) ev[0][e] = __builtin_fmaf(score(e), c, -m_use);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -286,27 +311,19 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       }
       if (j + AHEAD < NJ) fr[j + AHEAD] = frag(j + AHEAD);
       if (j + 1 < NJ) {
-        ev[j + 1][0] = __builtin_fmaf(score(2 * j + 2), c, -m_use);
-        ev[j + 1][1] = __builtin_fmaf(score(2 * j + 3), c, -m_use);
+#pragma unroll
+        for (int e = 0; e < SPJ; ++e) ev[j + 1][e] = __builtin_fmaf(score(SPJ * (j + 1) + e), c, -m_use);
       }
-      pv[j][0] = fast_exp2(ev[j][0]);
-      pv[j][1] = fast_exp2(ev[j][1]);
-      if (j >= 1) {
-        const int sc = 2 * (j - 1), cc = sc / 8, e = sc % 8;
-        const half2v h = {(half_t)pv[j - 1][0], (half_t)pv[j - 1][1]};
-        pcur[cc][e] = h[0];
-        pcur[cc][e + 1] = h[1];
-        dot2_acc(acc[cc], h);
-      }
+#pragma unroll
+      for (int e = 0; e < SPJ; ++e) pv[j][e] = fast_exp2(ev[j][e]);
+      if (SPJ == 2 && j >= 1) pack(2 * (j - 1), pv[max(j - 1, 0)][0], pv[max(j - 1, 0)][SPJ - 1]);
+      if (SPJ == 1 && j >= 2 && j % 2 == 0) pack(j - 2, pv[max(j - 2, 0)][0], pv[max(j - 1, 0)][0]);
       __builtin_amdgcn_sched_barrier(0);
     }
-    {
-      const int sc = 2 * (NJ - 1), cc = sc / 8, e = sc % 8;
-      const half2v h = {(half_t)pv[NJ - 1][0], (half_t)pv[NJ - 1][1]};
-      pcur[cc][e] = h[0];
-      pcur[cc][e + 1] = h[1];
-      dot2_acc(acc[cc], h);
-    }
+    if (SPJ == 2)
+      pack(2 * (NJ - 1), pv[NJ - 1][0], pv[NJ - 1][SPJ - 1]);
+    else
+      pack(NJ - 2, pv[NJ - 2][0], pv[NJ - 1][0]);
 #pragma unroll
     for (int w = 1; w < 2 * NT; w *= 2)
 #pragma unroll
@@ -445,27 +462,26 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   }
 
   // ---- merge the key groups through LDS ----
-  // Two key groups and two 32-column tiles of O: group g finishes tile g.
-  // Each group publishes (m, l) and the tile the other group finishes, so
-  // both merge and store half of O.
-  constexpr bool kSplitMerge = KSPLIT == 2 && DT == 2;
+  // Two key groups and an even number of 32-column tiles of O: group g
+  // finishes the tiles u with u % 2 == g.  Each group publishes (m, l) and
+  // the tiles the other group finishes, so both merge and store half of O.
+  constexpr bool kSplitMerge = KSPLIT == 2 && DT % 2 == 0;
   if constexpr (kSplitMerge) {
     // The partials below overwrite the start of the LDS, where the
     // last-block P V above may still be reading V.
     lds_barrier();
-    constexpr int SLOTS = 16 + 2;
+    constexpr int SLOTS = 16 * (DT / 2) + 2;
     static_assert(sizeof(smem) >= 8 * SLOTS * 64 * sizeof(float), "merge buffer");
     float* const red = reinterpret_cast<float*>(smem) + lane;
     float* mine = red + (size_t)(4 * kg + wave) * SLOTS * 64;
     const float* other = red + (size_t)(4 * (1 - kg) + wave) * SLOTS * 64;
     mine[0] = m_run;
     mine[64] = l_run;
-    if (kg == 0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mine[(2 + r) * 64] = o[1][r];
-    } else {
+    for (int u = 0; u < DT; ++u) {
+      if ((u & 1) == kg) continue;  // kg is wave-uniform: a scalar branch
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mine[(2 + r) * 64] = o[0][r];
+      for (int r = 0; r < 16; ++r) mine[(2 + 16 * (u / 2) + r) * 64] = o[u][r];
     }
     lds_barrier();
     const float m1 = other[0];
@@ -476,12 +492,11 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     const float a1 = fast_exp2(m1 - mu);
     m_run = mm;
     l_run = l_run * a0 + l1 * a1;
-    if (kg == 0) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[0][r] = o[0][r] * a0 + other[(2 + r) * 64] * a1;
-    } else {
+    for (int u = 0; u < DT; ++u) {
+      if ((u & 1) != kg) continue;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[1][r] = o[1][r] * a0 + other[(2 + r) * 64] * a1;
+      for (int r = 0; r < 16; ++r) o[u][r] = o[u][r] * a0 + other[(2 + 16 * (u / 2) + r) * 64] * a1;
     }
   } else if constexpr (KSPLIT > 1) {
     // The partials below overwrite the start of the LDS, where group 0's
@@ -529,7 +544,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
                                (uint32_t)qrows * p.stride_o * ES);
 #pragma unroll
   for (int u = 0; u < DT; ++u) {
-    if (kSplitMerge && u != kg) continue;
+    if (kSplitMerge && (u & 1) != kg) continue;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int col = 32 * u + 8 * b + 4 * g;
@@ -570,6 +585,9 @@ hipError_t launch_fast_d(const Fa2Args& a, int d, bool causal, int ksplit, hipSt
     case 64:
       return causal ? launch_fast_t<64, true, OUT_F16>(a, ksplit, s)
                     : launch_fast_t<64, false, OUT_F16>(a, ksplit, s);
+    case 128:
+      return causal ? launch_fast_t<128, true, OUT_F16>(a, ksplit, s)
+                    : launch_fast_t<128, false, OUT_F16>(a, ksplit, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -577,7 +595,7 @@ hipError_t launch_fast_d(const Fa2Args& a, int d, bool causal, int ksplit, hipSt
 }  // namespace
 
 bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32) {
-  return head_dim == 64 && bias_kind == kBiasNone && !in_f32;
+  return (head_dim == 64 || head_dim == 128) && bias_kind == kBiasNone && !in_f32;
 }
 
 bool fa2_fast_preferred(bool causal, int32_t N) {

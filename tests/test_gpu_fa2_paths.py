@@ -1,8 +1,8 @@
 """Both FA2 kernels for fp16 Q/K/V, and the fast kernel's rescale paths, vs the CPU oracle.
 
-head_dim 64 without a bias runs the fast kernel where it is the faster one
-(unmasked, N >= 1536); ``NESO_AMD_FA2_FAST=2`` forces it wherever it applies
-and ``NESO_AMD_FA2_FAST=0`` forces the generic kernel.  Both must meet the
+head_dim 64 and 128 without a bias run the fast kernel where it is the
+faster one; ``NESO_AMD_FA2_FAST=2`` forces it wherever it applies and
+``NESO_AMD_FA2_FAST=0`` forces the generic kernel.  Both must meet the
 attention bar (max abs error <= 2e-3 against the fp32 CPU softmax(QK^T s) V)
 for every key split, ragged and block-aligned lengths, causal or not.
 
@@ -46,59 +46,67 @@ def check(q, k, v, causal=False, scale=None, tol=TOL):
 @pytest.mark.parametrize("path", ["fast", "generic"])
 @pytest.mark.parametrize("ksplit", [1, 2])
 @pytest.mark.parametrize("causal", [False, True])
-@pytest.mark.parametrize("n", [1, 63, 64, 65, 128, 192, 320, 1000])
-def test_paths_and_splits(gpu, monkeypatch, path, ksplit, causal, n):
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("n", [1, 31, 32, 33, 63, 64, 65, 128, 192, 320, 1000])
+def test_paths_and_splits(gpu, monkeypatch, path, ksplit, causal, d, n):
     """Key groups with equal and unequal block counts (odd block totals),
-    single-block groups and tails shorter than a block."""
+    single-block groups and tails shorter than a block (blocks are 64 keys
+    at d = 64 and 32 keys at d = 128 in the fast kernel)."""
     monkeypatch.setenv("NESO_AMD_FA2_FAST", "2" if path == "fast" else "0")
     monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
-    q, k, v = I.fa2_inputs(1, 2, n, 64, seed=n + 7 * ksplit)
+    q, k, v = I.fa2_inputs(1, 2, n, d, seed=n + 7 * ksplit + d)
     check(q, k, v, causal)
 
 
-def _stepped_keys(n, steps, seed):
-    """K rows scaled by a factor that changes per 64-key block."""
-    q, k, v = I.fa2_inputs(1, 2, n, 64, seed=seed)
+def _stepped_keys(n, steps, seed, d=64, block=64):
+    """K rows scaled by a factor that changes per key block."""
+    q, k, v = I.fa2_inputs(1, 2, n, d, seed=seed)
     k = k.float()
-    for b in range(0, n, 64):
-        k[:, :, b:b + 64] *= steps[(b // 64) % len(steps)]
+    for b in range(0, n, block):
+        k[:, :, b:b + block] *= steps[(b // block) % len(steps)]
     return q, k.half(), v
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("ksplit", [1, 2])
 @pytest.mark.parametrize("causal", [False, True])
-def test_running_max_jumps_up(gpu, monkeypatch, ksplit, causal):
+def test_running_max_jumps_up(gpu, monkeypatch, ksplit, causal, d):
     """Each later block's logits are far above the running max: P of the new
     block would overflow fp16 without the slow path's rescale."""
     monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
     monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
-    q, k, v = _stepped_keys(768, [0.5, 1.5, 3.0, 6.0, 9.0, 12.0], seed=31)
+    q, k, v = _stepped_keys(768, [0.5, 1.5, 3.0, 6.0, 9.0, 12.0], seed=31, d=d, block=128 // (d // 32))
     check(q, k, v, causal)
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("ksplit", [1, 2])
-def test_running_max_falls(gpu, monkeypatch, ksplit):
+def test_running_max_falls(gpu, monkeypatch, ksplit, d):
     """The first block holds the largest logits; later blocks contribute
     little and must not disturb the result (no rescale needed)."""
     monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
     monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
-    q, k, v = _stepped_keys(768, [12.0, 4.0, 1.0, 0.25, 0.0, 0.1], seed=32)
+    q, k, v = _stepped_keys(768, [12.0, 4.0, 1.0, 0.25, 0.0, 0.1], seed=32, d=d,
+                            block=128 // (d // 32))
     check(q, k, v)
 
 
-def test_alternating_magnitudes(gpu, monkeypatch):
+@pytest.mark.parametrize("d", [64, 128])
+def test_alternating_magnitudes(gpu, monkeypatch, d):
     """Large and small logit blocks alternate: the running max rises in
     steps and the fast path's bound is exceeded repeatedly."""
     monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
-    q, k, v = _stepped_keys(1024, [0.2, 8.0, 0.2, 11.0, 0.2, 14.0, 0.2, 16.0], seed=33)
+    q, k, v = _stepped_keys(1024, [0.2, 8.0, 0.2, 11.0, 0.2, 14.0, 0.2, 16.0], seed=33, d=d,
+                            block=128 // (d // 32))
     check(q, k, v)
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("scale", [4.0, -4.0, 1e-6])
-def test_extreme_scales(gpu, monkeypatch, scale):
+def test_extreme_scales(gpu, monkeypatch, scale, d):
     """|scale * log2(e)| far above 1 (logits of hundreds) and nearly 0."""
     monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
-    q, k, v = I.fa2_inputs(1, 2, 256, 64, seed=34)
+    q, k, v = I.fa2_inputs(1, 2, 256, d, seed=34)
     check(q, k, v, scale=scale)
 
 
