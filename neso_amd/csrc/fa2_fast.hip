@@ -599,11 +599,16 @@ bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32) {
   return (head_dim == 64 || head_dim == 128) && bias_kind == kBiasNone && !in_f32;
 }
 
-bool fa2_fast_preferred(bool causal, int32_t N) {
+bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid) {
   // Measured on MI355X (d = 64, B*H = 8..64): the fast kernel is ahead from
   // N = 128 up without a mask (3-15%) and for causal rows from N = 1024
   // (7-25%, growing with N); for shorter causal rows the generic kernel's
   // per-wave skipping of invisible blocks wins (N = 256: 8.1 vs 8.9 us).
+  // On a small grid (128-query workgroups <= half the compute units) the
+  // generic kernel's 64-query workgroups with four key groups win at d = 64
+  // from N = 512 (7-19%: H16 N1024 12.0 vs 13.4 us, H4 N2048 causal 18.3
+  // vs 22.5 us); at d = 128 the fast kernel stays ahead (5-12%).
+  if (head_dim == 64 && small_grid && N >= 512) return false;
   return !causal || N >= 1024;
 }
 

@@ -45,8 +45,7 @@ namespace neso {
 
 namespace {
 
-constexpr int kBM = 128;       // queries per workgroup
-constexpr int kGroup = 256;    // threads per key group (4 waves)
+constexpr int kBM = 128;       // queries per workgroup at four query waves
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.f;  // rescale threshold (log2 units)
 
@@ -65,10 +64,10 @@ struct Piece8<true> {
   float4v f[2];
 };
 
-template <int D, bool F32IN>
+template <int D, bool F32IN, int GT>
 struct Staging {
   static constexpr int kKB = key_block<D>();
-  static constexpr int KCH = kKB * D / 8 / kGroup;   // 8-element K (and V) pieces per thread
+  static constexpr int KCH = kKB * D / 8 / GT;   // 8-element K (and V) pieces per thread
   Piece8<F32IN> k[KCH];
   Piece8<F32IN> v[KCH];
   float b;
@@ -86,15 +85,18 @@ __device__ __forceinline__ void split_f16(const float4v (&f)[2], half8v& hi, hal
   }
 }
 
-template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int KSPLIT, bool F32IN>
-__global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
+template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int KSPLIT, bool F32IN, int QW>
+__global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
+  constexpr int kBM = 32 * QW;      // queries per workgroup (QW waves of 32)
+  constexpr int kGroup = 64 * QW;   // threads per key group
   constexpr int kKB = key_block<D>();
   constexpr int NT = kKB / 32; // 32-key tiles per block
   constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;   // 32-row tiles of O^T
   constexpr int KLD = D + 8;   // LDS row stride of K (halves)
   constexpr int BAND = kBM + kKB - 1;  // bias-table entries per block
-  using St = Staging<D, F32IN>;
+  using St = Staging<D, F32IN, kGroup>;
+  static_assert(BIAS != kBiasTableF32 || kGroup >= BAND, "one bias-band entry per thread");
   using InT = typename std::conditional<F32IN, float, half_t>::type;
   constexpr int IES = sizeof(InT);  // bytes per input element
   static_assert(St::KCH >= 1 && kKB * D / 8 % kGroup == 0, "K tile split");
@@ -428,7 +430,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   // order.  Lane layout is identical across groups (same query slice).
   if constexpr (KSPLIT > 1) {
     constexpr int SLOTS = 16 * DT + 2;
-    constexpr int PART = 4 * SLOTS * 64;  // floats per published group
+    constexpr int PART = QW * SLOTS * 64;  // floats per published group
     static_assert(sizeof(smem) >= (size_t)(KSPLIT - 1) * PART * sizeof(float), "merge buffer");
     float* red = reinterpret_cast<float*>(smem) + (size_t)wave * SLOTS * 64 + lane;
     if (kg > 0) {
@@ -486,33 +488,42 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
 }
 
 // Static LDS of one workgroup with K key groups.
-template <int D, int BIAS, bool F32IN>
+template <int D, int BIAS, bool F32IN, int QW>
 constexpr int fa2_lds_bytes(int K) {
   constexpr int kb = key_block<D>();
   const int slot = (kb * (D + 8) + kb * D) * 2 * (F32IN ? 2 : 1);
-  const int bias = BIAS == kBiasTableF32 ? (kBM + kb) * 4 : 4;
+  const int bias = BIAS == kBiasTableF32 ? (32 * QW + kb) * 4 : 4;
   return K * 2 * (slot + bias);
 }
 
-template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int K, bool F32IN>
-bool launch_fa2_k(const Fa2Args& a, hipStream_t stream) {
-  if constexpr (fa2_lds_bytes<D, BIAS, F32IN>(K) <= 160 * 1024) {
-    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, K, F32IN>),
-                       dim3(a.num_qblocks * a.batch_heads), dim3(K * kGroup), 0, stream, a);
+template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int K, bool F32IN, int QW>
+bool launch_fa2_k(Fa2Args a, hipStream_t stream) {
+  if constexpr (fa2_lds_bytes<D, BIAS, F32IN, QW>(K) <= 160 * 1024) {
+    a.num_qblocks = (a.N + 32 * QW - 1) / (32 * QW);
+    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, K, F32IN, QW>),
+                       dim3(a.num_qblocks * a.batch_heads), dim3(K * 64 * QW), 0, stream, a);
     return true;
   }
   return false;
 }
 
-template <int D, bool CAUSAL, int BIAS, bool OUT_F16, bool F32IN = false>
-hipError_t launch_fa2_t(const Fa2Args& a, int ksplit, hipStream_t stream) {
+template <int D, bool CAUSAL, int BIAS, bool OUT_F16, bool F32IN, int QW>
+hipError_t launch_fa2_q(const Fa2Args& a, int ksplit, hipStream_t stream) {
   // Use the requested key split, or the largest smaller one whose LDS fits.
   bool done = false;
-  if (ksplit >= 4) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 4, F32IN>(a, stream);
-  if (!done && ksplit >= 3) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 3, F32IN>(a, stream);
-  if (!done && ksplit >= 2) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 2, F32IN>(a, stream);
-  if (!done) launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 1, F32IN>(a, stream);
+  if (ksplit >= 4) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 4, F32IN, QW>(a, stream);
+  if (!done && ksplit >= 3) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 3, F32IN, QW>(a, stream);
+  if (!done && ksplit >= 2) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 2, F32IN, QW>(a, stream);
+  if (!done) launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 1, F32IN, QW>(a, stream);
   return hipGetLastError();
+}
+
+// Query waves per key group: 4 (128-query workgroups), or 2 (64-query
+// workgroups) when a.qwaves says so (see launch_fa2).
+template <int D, bool CAUSAL, int BIAS, bool OUT_F16, bool F32IN = false>
+hipError_t launch_fa2_t(const Fa2Args& a, int ksplit, hipStream_t stream) {
+  return a.qwaves == 2 ? launch_fa2_q<D, CAUSAL, BIAS, OUT_F16, F32IN, 2>(a, ksplit, stream)
+                       : launch_fa2_q<D, CAUSAL, BIAS, OUT_F16, F32IN, 4>(a, ksplit, stream);
 }
 
 template <int D, int BIAS, bool OUT_F16>
@@ -550,7 +561,7 @@ hipError_t launch_fa2_d(const Fa2Args& a, int d, bool causal, int ksplit, hipStr
 
 }  // namespace
 
-int fa2_query_block() { return kBM; }
+int fa2_query_block() { return kBM; }  // the largest query block of any FA2 kernel
 
 hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool out_f16,
                       hipStream_t stream, bool in_f32) {
@@ -558,10 +569,19 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
   // Split the keys of a workgroup over two wave groups when the grid alone
   // gives fewer than two workgroups per compute unit.
   const int64_t wgs = (int64_t)a.num_qblocks * a.batch_heads;
-  const int ksplit = (a.ksplit > 0) ? a.ksplit : (wgs < 2 * (int64_t)device_cu_count() ? 2 : 1);
+  const int64_t cus = device_cu_count();
+  int ksplit = (a.ksplit > 0) ? a.ksplit : (wgs < 2 * cus ? 2 : 1);
+  // Small grid: 128-query workgroups fill at most half the compute units.
+  const bool small = 2 * wgs <= cus;
   if (a.allow_fast && fa2_fast_supported(head_dim, bias_kind, in_f32) &&
-      (a.allow_fast == 2 || fa2_fast_preferred(causal, a.N)))
+      (a.allow_fast == 2 || fa2_fast_preferred(causal, a.N, head_dim, small)))
     return launch_fa2_fast(a, head_dim, causal, out_f16, ksplit, stream);
+  // Generic kernel on a small grid: 64-query workgroups (two query waves per
+  // key group) and four key groups double the grid, still one round of
+  // workgroups, with eight waves each.  With more workgroups the doubled
+  // grid takes two rounds (H12 N2048 d64: 34.4 us, the fast kernel 21.5).
+  if (a.qwaves != 2 && a.qwaves != 4) a.qwaves = small ? 2 : 4;
+  if (a.qwaves == 2 && a.ksplit <= 0) ksplit = 4;
   if (in_f32) {
     if (bias_kind != kBiasNone || out_f16) return hipErrorInvalidValue;
     return launch_fa2_f32in(a, head_dim, causal, ksplit, stream);

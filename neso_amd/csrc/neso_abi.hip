@@ -57,6 +57,15 @@ int env_allow_fast() {
   return v[0] == '2' ? 2 : 1;
 }
 
+// Query waves per key group of the generic FA2 kernel (tests cover both):
+// NESO_AMD_FA2_QW=2 or 4; unset chooses from the grid size.
+int env_qwaves() {
+  const char* v = getenv("NESO_AMD_FA2_QW");
+  if (!v) return 0;
+  const int k = atoi(v);
+  return (k == 2 || k == 4) ? k : 0;
+}
+
 int check_head_dim(int32_t d) {
   if (d == 32 || d == 64 || d == 128) return NESO_OK;
   return fail(NESO_EUNSUPPORTED, "head_dim %d not supported (32, 64, 128)", d);
@@ -248,6 +257,7 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
   a.scale_log2 = scale * 1.4426950408889634f;
   a.ksplit = env_ksplit();
   a.allow_fast = env_allow_fast();
+  a.qwaves = env_qwaves();
   // Causal is the window (N, 0); windows wider than N are clamped to N.
   a.win_left = win_left < 0 ? N : (win_left < N ? win_left : N);
   a.win_right = win_right < 0 ? 0 : (win_right < N ? win_right : N);

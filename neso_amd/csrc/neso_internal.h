@@ -38,6 +38,9 @@ struct Fa2Args {
   // (fa2_fast.hip) where it is measured faster, 2 = the fast kernel
   // wherever it applies, 0 = always the generic kernel.
   int32_t allow_fast;
+  // Query waves per key group of the generic kernel (its query block is 32
+  // rows per wave): 4 or 2; 0 = chosen from the grid size.
+  int32_t qwaves;
 };
 
 // Compute units of the current device (cached per device).
@@ -47,7 +50,7 @@ int fa2_query_block();
 // The fast kernel covers fp16 Q/K/V without a bias at head_dim 64, and is
 // the faster one for unmasked attention from N ~ 2048 up.
 bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32);
-bool fa2_fast_preferred(bool causal, int32_t N);
+bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid);
 hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, int ksplit,
                            hipStream_t stream);
 hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool out_f16,
