@@ -64,7 +64,7 @@ __device__ __forceinline__ void unpack_word(uint32_t w, const Nibbles& k, half2v
 }
 
 // ---------------------------------------------------------------------------
-// GEMV regime (M <= 4): a persistent stream of weight rows.
+// GEMV regime (M <= 3 by default, up to 4): a persistent stream of weight rows.
 //
 // Wave w handles rows w, w + T, w + 2T, ... (T = waves in the grid), so at
 // any moment the grid streams one contiguous stretch of W.  Lane l owns the
@@ -1224,7 +1224,12 @@ int w4a16_gemv_max_k() { return 32 * 256; }
 constexpr int kSkinnyWaves = NESO_SKINNY_WAVES;
 
 hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
-  if (a.M <= 4 && a.K <= w4a16_gemv_max_k()) {
+  // GEMV regime up to M = 3.  At M = 4 the skinny MFMA kernel is faster
+  // (K = 4096, N = 11008: 11.5 against 13.8 us; M = 3: 11.1 GEMV, 11.4
+  // MFMA).  NESO_AMD_W4_GEMV_MAX_M = 0..4 overrides the largest GEMV M.
+  const char* gemv_env = getenv("NESO_AMD_W4_GEMV_MAX_M");
+  const int gemv_max_m = gemv_env ? atoi(gemv_env) : 3;
+  if (a.M <= gemv_max_m && a.K <= w4a16_gemv_max_k()) {
     switch (a.M) {
       case 1: return launch_gemv_mr<1>(a, s);
       case 2: return launch_gemv_mr<2>(a, s);

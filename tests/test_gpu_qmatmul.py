@@ -74,6 +74,20 @@ def test_gemv_chunks_per_lane(gpu, m, k, n):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
+@pytest.mark.parametrize("gemv_max_m", ["0", "4"])
+@pytest.mark.parametrize("m", [1, 2, 3, 4])
+@pytest.mark.parametrize("n,k", [(300, 4096), (129, 2080)])
+def test_small_m_both_regimes(gpu, monkeypatch, gemv_max_m, m, n, k):
+    """M = 1..4 through the GEMV kernel (NESO_AMD_W4_GEMV_MAX_M = 4) and
+    through the MFMA kernels (= 0); by default M <= 3 takes the GEMV."""
+    monkeypatch.setenv("NESO_AMD_W4_GEMV_MAX_M", gemv_max_m)
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n + k)
+    words = Q.pack_int4(codes.numpy())
+    y = gpu_w4(x, words, scales)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
+    assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
+
+
 @pytest.mark.parametrize("group,zero", [(64, 8), (128, 7), (32, 0), (4096, 15)])
 @pytest.mark.parametrize("m", [1, 16])
 def test_group_and_zero_point(gpu, group, zero, m):
@@ -89,14 +103,14 @@ def test_zero_point_codes_give_zero(gpu, m):
     """Codes equal to the zero point dequantise to 0, so Y = 0.
 
     The MFMA regime subtracts the zero point per element (exact zeros).  The
-    GEMV regime (M <= 4) folds it into a per-chunk correction computed from
+    GEMV regime (M <= 3) folds it into a per-chunk correction computed from
     X, so it returns 0 up to fp32 rounding: |Y| <= 1e-3 here, against
     typical |Y| ~ 4 for these inputs with random codes.
     """
     x, _, scales = I.qmatmul_inputs(m, 4096, 512, seed=1)
     eights = Q.pack_int4(np.full((512, 4096), 8, np.uint8))
     y = gpu_w4(x, eights, scales)
-    if m <= 4:
+    if m <= 3:
         assert y.float().abs().max().item() <= 1e-3
     else:
         assert torch.count_nonzero(y).item() == 0
