@@ -64,7 +64,7 @@ __device__ __forceinline__ void unpack_word(uint32_t w, const Nibbles& k, half2v
 }
 
 // ---------------------------------------------------------------------------
-// GEMV regime (M <= 3 by default, up to 4): a persistent stream of weight rows.
+// GEMV regime (M <= 2 by default, up to 4): a persistent stream of weight rows.
 //
 // Wave w handles rows w, w + T, w + 2T, ... (T = waves in the grid), so at
 // any moment the grid streams one contiguous stretch of W.  Lane l owns the
@@ -446,12 +446,12 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_kernel(W4Args a) {
 // ---------------------------------------------------------------------------
 // Skinny-M regime with X resident in LDS (M <= 16, K <= 4096, group 32).
 //
-// The workload is one burst of N*K/2 bytes: every weight load should be in
-// flight from the start.  One persistent workgroup per CU owns row tiles
-// blockIdx.x + i * gridDim.x (16 rows each, i < T).  Its WV waves split K
-// (wave w takes chunk quads [w*QW, (w+1)*QW)) and issue all their weight
-// and scale loads for all T tiles, after X, before anything else waits (plain loads:
-// the non-temporal hint measured slower for these 64-byte row pieces).  X is copied
+// The workload is one burst of N*K/2 bytes.  One persistent workgroup per
+// CU owns row tiles blockIdx.x + i * gridDim.x (16 rows each, i < T).  Its
+// WV waves split K (wave w takes chunk quads [w*QW, (w+1)*QW)) and request
+// the weights and scales of tile i + 1 before computing tile i, tile 0
+// right after X (plain loads: the non-temporal hint measured slower for
+// these 64-byte row pieces).  X is copied
 // once per workgroup into LDS, already in MFMA A-fragment order (slot
 // (4q + t) * 64 + lane holds X[m][32(4q+t) + 8g + {0,4,1,5,2,6,3,7}] for
 // lane = m + 16g), so the per-tile A operand is one conflict-free
@@ -503,7 +503,7 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
     xslot[i] = ct * 64 + 16 * g + (m ^ (4 * (ct & 3) + g));
   }
 
-  // All weight and scale loads of this wave, all tiles.
+  // Weight and scale loads of this wave for tile i.
   // Scales: one 8-byte load per lane and tile, lane (li, lg) taking quad
   // q0 + lg of row li (32 contiguous bytes per row instead of 8, and no
   // four lanes loading the same bytes); quad qi reaches lane (li, *) from
@@ -511,8 +511,7 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
   typedef uint32_t uint2v __attribute__((ext_vector_type(2)));
   uint4v w[T][QWMAX];
   uint2v scw[T];
-#pragma unroll
-  for (int i = 0; i < T; ++i) {
+  auto load_tile = [&](int i) {
     const int tile = blockIdx.x + i * gridDim.x;
     const int n0 = tile * 16;
     const int nrows = tile < ntiles ? min(16, a.N - n0) : 0;
@@ -532,7 +531,12 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
       const uint32_t so = ((li * (uint32_t)SG + cq) * 2u) | (lg < QW && (int)cq < cend ? 0u : kOut);
       scw[i] = __builtin_bit_cast(uint2v, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
     }
-  }
+  };
+  // Tile 0 now; tile i + 1 is requested when tile i's compute starts.  With
+  // every tile requested up front, the wave stalls at the load instructions
+  // once the CU's outstanding-request capacity is full, and X, compute and
+  // the weight stream run one after another (M = 16: 12.0 -> 9.3 us).
+  load_tile(0);
 
   // X into LDS in A-fragment order.
 #pragma unroll
@@ -545,6 +549,7 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
   float4v acc[T];
 #pragma unroll
   for (int i = 0; i < T; ++i) {
+    if (i + 1 < T) load_tile(i + 1);
     acc[i] = float4v{};
 #pragma unroll
     for (int qi = 0; qi < QWMAX; ++qi) {
@@ -1224,11 +1229,12 @@ int w4a16_gemv_max_k() { return 32 * 256; }
 constexpr int kSkinnyWaves = NESO_SKINNY_WAVES;
 
 hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
-  // GEMV regime up to M = 3.  At M = 4 the skinny MFMA kernel is faster
-  // (K = 4096, N = 11008: 11.5 against 13.8 us; M = 3: 11.1 GEMV, 11.4
-  // MFMA).  NESO_AMD_W4_GEMV_MAX_M = 0..4 overrides the largest GEMV M.
+  // GEMV regime up to M = 2.  From M = 3 the skinny MFMA kernel is faster
+  // (K = 4096, N = 11008, GEMV / MFMA: M = 1 6.6 / 8.7 us, M = 2 8.6 / 8.7,
+  // M = 3 11.1 / 8.7, M = 4 13.8 / 8.7).  NESO_AMD_W4_GEMV_MAX_M = 0..4
+  // overrides the largest GEMV M.
   const char* gemv_env = getenv("NESO_AMD_W4_GEMV_MAX_M");
-  const int gemv_max_m = gemv_env ? atoi(gemv_env) : 3;
+  const int gemv_max_m = gemv_env ? atoi(gemv_env) : 2;
   if (a.M <= gemv_max_m && a.K <= w4a16_gemv_max_k()) {
     switch (a.M) {
       case 1: return launch_gemv_mr<1>(a, s);
