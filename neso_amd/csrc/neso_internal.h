@@ -71,6 +71,10 @@ struct W4Args {
 };
 
 hipError_t launch_w4a16(const W4Args& a, hipStream_t stream);
+// Skinny-M kernel with X in LDS (qmatmul_skinny.hip): M <= 16, group 32,
+// K % 128 == 0, K <= w4a16_skinny_lds_max_k().
+int w4a16_skinny_lds_max_k();
+hipError_t launch_w4a16_skinny_lds(const W4Args& a, hipStream_t stream);
 
 // C[M][N] (f32) = A[M][K] (f16) * f16(B[K][N] int8) [* scale[n]].
 struct W8Args {

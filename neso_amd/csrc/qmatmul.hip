@@ -19,49 +19,13 @@
 
 #include "common.h"
 #include "neso_internal.h"
+#include "qmatmul_common.h"
 
 namespace neso {
 
 namespace {
 
 constexpr int kThreads = 256;
-
-__device__ __forceinline__ half2v as_half2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
-
-// 32-bit constants the compiler cannot fold back into literals: gfx9 VOP3
-// encodings take no literal and read at most one SGPR, so v_and_or_b32
-// needs its two constants as one SGPR and one VGPR.
-__device__ __forceinline__ uint32_t sgpr_const(uint32_t v) {
-  uint32_t r;
-  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
-  return r;
-}
-__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
-  uint32_t r;
-  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
-  return r;
-}
-
-// Nibble masks and the f16 exponent pattern, held in registers so that
-// (w & mask) | magic is one v_and_or_b32.
-struct Nibbles {
-  uint32_t lo, hi, mag;
-};
-__device__ __forceinline__ Nibbles nibble_consts() {
-  return Nibbles{sgpr_const(0x000F000Fu), sgpr_const(0x00F000F0u), vgpr_const(0x64006400u)};
-}
-
-// Four f16 pairs of one packed word, shifted by the zero point:
-//   r[0] = (c0 - z, c4 - z)        r[1] = 16 * (c1 - z, c5 - z)
-//   r[2] = (c2 - z, c6 - z)        r[3] = 16 * (c3 - z, c7 - z)
-__device__ __forceinline__ void unpack_word(uint32_t w, const Nibbles& k, half2v z1, half2v z16,
-                                            half2v r[4]) {
-  const uint32_t w8 = w >> 8;
-  r[0] = as_half2((w & k.lo) | k.mag) - z1;
-  r[1] = as_half2((w & k.hi) | k.mag) - z16;
-  r[2] = as_half2((w8 & k.lo) | k.mag) - z1;
-  r[3] = as_half2((w8 & k.hi) | k.mag) - z16;
-}
 
 // ---------------------------------------------------------------------------
 // GEMV regime (M <= 2 by default, up to 4): a persistent stream of weight rows.
@@ -277,23 +241,6 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
 // dequantised and scaled in fp16 before the MFMA: (c - z) * s, one rounding.
 // Out-of-range rows and chunks are zero-filled by the buffer bounds check
 // (chunks past the wave's range get an out-of-range offset).
-// Word j of register w_j in 16-lane row g (chunk g, word j) becomes word g
-// of chunk j: a 4x4 transpose between the registers and the four rows.
-// v_permlane32_swap exchanges the upper 32 lanes of its first operand with
-// the lower 32 lanes of its second; v_permlane16_swap exchanges the odd rows
-// of its first operand with the even rows of its second.
-__device__ __forceinline__ void transpose_rows4(uint32_t& w0, uint32_t& w1, uint32_t& w2,
-                                                uint32_t& w3) {
-  const auto a = __builtin_amdgcn_permlane32_swap(w0, w2, false, false);
-  const auto b = __builtin_amdgcn_permlane32_swap(w1, w3, false, false);
-  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
-  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
-  w0 = c[0];
-  w1 = c[1];
-  w2 = d[0];
-  w3 = d[1];
-}
-
 template <int MT, int NT, int WV, bool G32>
 __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_kernel(W4Args a) {
   constexpr int QB = 2;                   // quads per batch
@@ -440,156 +387,6 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_kernel(W4Args a) {
     const int m = m0 + 16 * mt + 4 * (ln >> 4) + r;
     const int n = n0 + 16 * nt + (ln & 15);
     if (m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (half_t)v;
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Skinny-M regime with X resident in LDS (M <= 16, K <= 4096, group 32).
-//
-// The workload is one burst of N*K/2 bytes.  One persistent workgroup per
-// CU owns row tiles blockIdx.x + i * gridDim.x (16 rows each, i < T).  Its
-// WV waves split K (wave w takes chunk quads [w*QW, (w+1)*QW)) and request
-// the weights and scales of tile i + 1 before computing tile i, tile 0
-// right after X (plain loads: the non-temporal hint measured slower for
-// these 64-byte row pieces).  X is copied
-// once per workgroup into LDS, already in MFMA A-fragment order (slot
-// (4q + t) * 64 + lane holds X[m][32(4q+t) + 8g + {0,4,1,5,2,6,3,7}] for
-// lane = m + 16g), so the per-tile A operand is one conflict-free
-// ds_read_b128 per MFMA.  MFMA, transpose and dequantisation are those of
-// w4a16_skinny_kernel.  The WV partial tiles are reduced through LDS.
-// (The slot's row index is XOR-swizzled; see the X loads below.)
-constexpr int kLdsQuads = 32;  // K <= 4096
-
-template <int WV, int T, int QWMAX>
-__global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) {
-  static_assert(QWMAX <= 4, "a quad's scales come from one of the four lane groups");
-  constexpr uint32_t kOut = 0x80000000u;
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int li = lane & 15, lg = lane >> 4;
-  const int KW = a.K >> 3, SG = a.K >> 5, C = a.K >> 5;
-  const int Q = (C + 3) >> 2;
-  const int QW = (Q + WV - 1) / WV;
-  const int q0 = wave * QW;
-  const int cend = min(4 * min(q0 + QW, Q), C);
-  const int ntiles = (a.N + 15) >> 4;
-  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
-  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
-  const Nibbles nib = nibble_consts();
-
-  __shared__ half8v xs[kLdsQuads * 4 * kWave];
-  __shared__ float red[T][WV][4][kWave];
-
-  // X first: loads complete in issue order, so X (L2-resident) reaches LDS
-  // while the weight burst is still arriving; issued after the weights, it
-  // waited behind them (measured: 15.7 -> 14.2 us at M = 16).  Each wave
-  // instruction reads 1 KiB of one X row (piece e: row m, pieces pp of 8
-  // halves; 16 rows x 64 B per instruction measured 14.2 vs 12.9 us).  Piece
-  // (m, chunk ct, quarter g) goes to A-fragment slot ct*64 + 16g + m', with
-  // the row index swizzled, m' = m ^ (4 (ct % 4) + g), so that the 64
-  // same-row stores of an instruction and the 16-lane fragment reads both
-  // spread over all banks.
-  constexpr int kXPer = (kLdsQuads * 4 * kWave) / (WV * kWave);
-  const rsrc_t rx = make_rsrc(a.X, (uint32_t)((a.M - 1) * a.ldx + a.K) * 2u);
-  half8v xv[kXPer];
-  uint32_t xslot[kXPer];
-#pragma unroll
-  for (int i = 0; i < kXPer; ++i) {
-    const uint32_t e = threadIdx.x + i * WV * kWave;
-    const uint32_t m = e / (4 * 4 * kLdsQuads), pp = e % (4 * 4 * kLdsQuads);
-    const uint32_t ct = pp >> 2, g = pp & 3;
-    const uint32_t oob = ((int)ct < C && (int)m < a.M) ? 0u : kOut;
-    xv[i] = buf_load_half8(rx, ((m * (uint32_t)a.ldx + 8u * pp) * 2u) | oob);
-    xslot[i] = ct * 64 + 16 * g + (m ^ (4 * (ct & 3) + g));
-  }
-
-  // Weight and scale loads of this wave for tile i.
-  // Scales: one 8-byte load per lane and tile, lane (li, lg) taking quad
-  // q0 + lg of row li (32 contiguous bytes per row instead of 8, and no
-  // four lanes loading the same bytes); quad qi reaches lane (li, *) from
-  // lane (li, qi) by ds_bpermute (measured 12.9 -> 11.7 us at M = 16).
-  typedef uint32_t uint2v __attribute__((ext_vector_type(2)));
-  uint4v w[T][QWMAX];
-  uint2v scw[T];
-  auto load_tile = [&](int i) {
-    const int tile = blockIdx.x + i * gridDim.x;
-    const int n0 = tile * 16;
-    const int nrows = tile < ntiles ? min(16, a.N - n0) : 0;
-    const rsrc_t rw = make_rsrc(a.W + (int64_t)(nrows ? n0 : 0) * KW, (uint32_t)nrows * KW * 4u);
-    const rsrc_t rs = make_rsrc(a.S + (int64_t)(nrows ? n0 : 0) * SG, (uint32_t)nrows * SG * 2u);
-#pragma unroll
-    for (int qi = 0; qi < QWMAX; ++qi) {
-      const uint32_t cq = 4 * (q0 + qi);
-      const uint32_t c = cq + lg;
-      const bool live = qi < QW;
-      const uint32_t wo = (li * (uint32_t)KW * 4u + c * 16u) | (live && (int)c < cend ? 0u : kOut);
-      w[i][qi] = __builtin_bit_cast(
-          uint4v, __builtin_amdgcn_raw_buffer_load_b128(rw, wo, 0, 0));
-    }
-    {
-      const uint32_t cq = 4 * (q0 + lg);
-      const uint32_t so = ((li * (uint32_t)SG + cq) * 2u) | (lg < QW && (int)cq < cend ? 0u : kOut);
-      scw[i] = __builtin_bit_cast(uint2v, __builtin_amdgcn_raw_buffer_load_b64(rs, so, 0, 0));
-    }
-  };
-  // Tile 0 now; tile i + 1 is requested when tile i's compute starts.  With
-  // every tile requested up front, the wave stalls at the load instructions
-  // once the CU's outstanding-request capacity is full, and X, compute and
-  // the weight stream run one after another (M = 16: 12.0 -> 9.3 us).
-  load_tile(0);
-
-  // X into LDS in A-fragment order.
-#pragma unroll
-  for (int i = 0; i < kXPer; ++i) {
-    const half8v x = xv[i];
-    xs[xslot[i]] = half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
-  }
-  lds_barrier();
-
-  float4v acc[T];
-#pragma unroll
-  for (int i = 0; i < T; ++i) {
-    if (i + 1 < T) load_tile(i + 1);
-    acc[i] = float4v{};
-#pragma unroll
-    for (int qi = 0; qi < QWMAX; ++qi) {
-      if (qi >= QW) break;  // uniform
-      const int q = q0 + qi;
-      uint32_t wt[4] = {w[i][qi][0], w[i][qi][1], w[i][qi][2], w[i][qi][3]};
-      const int src = (li + 16 * qi) * 4;
-      const half4v sq = __builtin_bit_cast(
-          half4v, uint2v{(uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)scw[i][0]),
-                         (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)scw[i][1])});
-      transpose_rows4(wt[0], wt[1], wt[2], wt[3]);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const half8v xa = xs[(4 * q + t) * kWave + 16 * lg + (li ^ (4 * t + lg))];
-        const half_t s = sq[t];
-        const half2v s1 = {s, s};
-        const half_t s16v = s * (half_t)0.0625f;
-        const half2v s16 = {s16v, s16v};
-        half2v r[4];
-        unpack_word(wt[t], nib, z1, z16, r);
-        const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
-        const half8v bv = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
-        acc[i] = mfma16x16x32(xa, bv, acc[i]);
-      }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) red[i][wave][r][lane] = acc[i][r];
-  }
-  lds_barrier();
-
-  // acc[i] register r of lane l is D[4(l/16) + r][l%16] of tile i.
-  for (int e = threadIdx.x; e < T * 4 * kWave; e += WV * kWave) {
-    const int i = e / (4 * kWave), r = (e / kWave) & 3, ln = e & 63;
-    const int tile = blockIdx.x + i * gridDim.x;
-    float v = 0.f;
-#pragma unroll
-    for (int wv = 0; wv < WV; ++wv) v += red[i][wv][r][ln];
-    const int m = 4 * (ln >> 4) + r;
-    const int n = tile * 16 + (ln & 15);
-    if (tile < ntiles && m < a.M && n < a.N) a.Y[(int64_t)m * a.ldy + n] = (half_t)v;
   }
 }
 
@@ -1253,21 +1050,10 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
   // stay below 2^31 bytes (the out-of-range marker).
   const bool skinny_fits = (int64_t)32 * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
                            (int64_t)32 * a.K / 2 < ((int64_t)1 << 31);
-  if (a.M <= 16 && a.group == 32 && a.K % 128 == 0 && a.K <= 32 * 4 * kLdsQuads) {
-    // X in LDS, one persistent workgroup per CU, 8 waves splitting K.
-    const int ntiles = (a.N + 15) / 16;
-    const int cus = device_cu_count();
-    int T = (ntiles + cus - 1) / cus;
-    if (T > 4) T = 4;
-    const dim3 grid((ntiles + T - 1) / T);
-    constexpr int WV = 8, QWMAX = (kLdsQuads + WV - 1) / WV;
-    switch (T) {
-      case 1: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 1, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
-      case 2: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 2, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
-      case 3: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 3, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
-      default: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 4, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
-    }
-    return hipGetLastError();
+  if (a.M <= 16 && a.group == 32 && a.K % 128 == 0 && a.K <= w4a16_skinny_lds_max_k()) {
+    // X in LDS, one persistent workgroup per CU, 8 waves splitting K
+    // (qmatmul_skinny.hip).
+    return launch_w4a16_skinny_lds(a, s);
   }
   if (a.M <= 64 && skinny_fits) {
     // One 8-byte load fetches the scales of a chunk quad when every chunk

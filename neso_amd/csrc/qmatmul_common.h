@@ -1,0 +1,66 @@
+// Helpers shared by the int4 matmul translation units (qmatmul.hip and
+// qmatmul_skinny.hip): f16 exponent-trick dequantisation and the 4x4
+// transpose across 16-lane rows.
+#pragma once
+
+#include "common.h"
+
+namespace neso {
+namespace {
+
+__device__ __forceinline__ half2v as_half2(uint32_t u) { return __builtin_bit_cast(half2v, u); }
+
+// 32-bit constants the compiler cannot fold back into literals: gfx9 VOP3
+// encodings take no literal and read at most one SGPR, so v_and_or_b32
+// needs its two constants as one SGPR and one VGPR.
+__device__ __forceinline__ uint32_t sgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
+  return r;
+}
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+  return r;
+}
+
+// Nibble masks and the f16 exponent pattern, held in registers so that
+// (w & mask) | magic is one v_and_or_b32.
+struct Nibbles {
+  uint32_t lo, hi, mag;
+};
+__device__ __forceinline__ Nibbles nibble_consts() {
+  return Nibbles{sgpr_const(0x000F000Fu), sgpr_const(0x00F000F0u), vgpr_const(0x64006400u)};
+}
+
+// Four f16 pairs of one packed word, shifted by the zero point:
+//   r[0] = (c0 - z, c4 - z)        r[1] = 16 * (c1 - z, c5 - z)
+//   r[2] = (c2 - z, c6 - z)        r[3] = 16 * (c3 - z, c7 - z)
+__device__ __forceinline__ void unpack_word(uint32_t w, const Nibbles& k, half2v z1, half2v z16,
+                                            half2v r[4]) {
+  const uint32_t w8 = w >> 8;
+  r[0] = as_half2((w & k.lo) | k.mag) - z1;
+  r[1] = as_half2((w & k.hi) | k.mag) - z16;
+  r[2] = as_half2((w8 & k.lo) | k.mag) - z1;
+  r[3] = as_half2((w8 & k.hi) | k.mag) - z16;
+}
+
+// Word j of register w_j in 16-lane row g (chunk g, word j) becomes word g
+// of chunk j: a 4x4 transpose between the registers and the four rows.
+// v_permlane32_swap exchanges the upper 32 lanes of its first operand with
+// the lower 32 lanes of its second; v_permlane16_swap exchanges the odd rows
+// of its first operand with the even rows of its second.
+__device__ __forceinline__ void transpose_rows4(uint32_t& w0, uint32_t& w1, uint32_t& w2,
+                                                uint32_t& w3) {
+  const auto a = __builtin_amdgcn_permlane32_swap(w0, w2, false, false);
+  const auto b = __builtin_amdgcn_permlane32_swap(w1, w3, false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[0], b[0], false, false);
+  const auto d = __builtin_amdgcn_permlane16_swap(a[1], b[1], false, false);
+  w0 = c[0];
+  w1 = c[1];
+  w2 = d[0];
+  w3 = d[1];
+}
+
+}  // namespace
+}  // namespace neso
