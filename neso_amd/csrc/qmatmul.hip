@@ -223,7 +223,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// Skinny-M regime (5 <= M <= 64): split-K MFMA.
+// Skinny-M regime (3 <= M <= 64 by default): split-K MFMA.
 //
 // A workgroup owns 16*NT rows of W (output columns n) and 16*MT rows of X.
 // Its WV waves split K into contiguous ranges of chunk quads (a quad = 4
