@@ -98,8 +98,10 @@ __device__ __forceinline__ uint32_t lds_addr(const half_t* p) {
   return (uint32_t)(size_t)(__attribute__((address_space(3))) const half_t*)p;
 }
 
-template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT>
+// PAIR (causal only): each workgroup takes two query blocks, see below.
+template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT, bool PAIR = false>
 __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
+  static_assert(!PAIR || CAUSAL, "paired query blocks are for causal grids");
   constexpr int kKB = fast_kb<D>();  // keys per block
   constexpr int NT = kKB / 32;  // 32-key tiles per block
   constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
@@ -121,10 +123,16 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   const int g = lane >> 5;
   const int ql = lane & 31;
 
+  // Workgroup x of head bh takes query block nqb - 1 - x (causal: longest
+  // rows first) or x.  With PAIR it then also takes block x, so that every
+  // workgroup does the work of nqb + 1 blocks' rows.
   const uint32_t wg = xcd_swizzle(blockIdx.x, gridDim.x);
-  const int bh = wg / p.num_qblocks;
-  int qblk = wg % p.num_qblocks;
-  if (CAUSAL) qblk = p.num_qblocks - 1 - qblk;  // longest rows first
+  const int nqb = p.num_qblocks;
+  const int wph = PAIR ? (nqb + 1) / 2 : nqb;  // workgroups per head
+  const int bh = wg / wph;
+  const int x = wg % wph;
+
+  auto run = [&](const int qblk) {
   const int N = p.N;
   const int q0 = qblk * kBM;
   const int qw0 = q0 + wave * 32;
@@ -559,11 +567,32 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       }
     }
   }
+  };  // run
+
+  if constexpr (PAIR) {
+    // One copy of the body: a loop of one or two passes.
+    const int npass = x != nqb - 1 - x ? 2 : 1;
+#pragma nounroll
+    for (int pass = 0; pass < npass; ++pass) {
+      if (pass) lds_barrier();  // the merge before read partials that this block's loads overwrite
+      run(pass ? x : nqb - 1 - x);
+    }
+  } else {
+    run(CAUSAL ? nqb - 1 - x : x);
+  }
 }
 
 template <int D, bool CAUSAL, bool OUT_F16, int K>
 bool launch_fast_k(const Fa2Args& a, hipStream_t stream) {
   if constexpr (K * fast_group_lds_halves<D>() * 2 <= 160 * 1024) {
+    if constexpr (CAUSAL) {
+      if (a.pair_qblocks) {
+        hipLaunchKernelGGL((fa2_fast_kernel<D, true, OUT_F16, K, true>),
+                           dim3((a.num_qblocks + 1) / 2 * a.batch_heads), dim3(K * kGroup), 0,
+                           stream, a);
+        return true;
+      }
+    }
     hipLaunchKernelGGL((fa2_fast_kernel<D, CAUSAL, OUT_F16, K>),
                        dim3(a.num_qblocks * a.batch_heads), dim3(K * kGroup), 0, stream, a);
     return true;
@@ -615,6 +644,8 @@ bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid) {
 hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, int ksplit,
                            hipStream_t stream) {
   a.num_qblocks = (a.N + kBM - 1) / kBM;
+  // Paired query blocks (causal kernels only; any window is correct).
+  a.pair_qblocks = (causal && a.pair_qblocks == 1) ? 1 : 0;
   return out_f16 ? launch_fast_d<true>(a, head_dim, causal, ksplit, stream)
                  : launch_fast_d<false>(a, head_dim, causal, ksplit, stream);
 }

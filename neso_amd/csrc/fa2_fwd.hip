@@ -582,8 +582,21 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
   // Small grid: 128-query workgroups fill at most half the compute units.
   const bool small = 2 * wgs <= cus;
   if (a.allow_fast && fa2_fast_supported(head_dim, bias_kind, in_f32) &&
-      (a.allow_fast == 2 || fa2_fast_preferred(causal, a.N, head_dim, small)))
+      (a.allow_fast == 2 || fa2_fast_preferred(causal, a.N, head_dim, small))) {
+    // Causal grids of at least two workgroups per CU: each workgroup takes a
+    // long and a short query block (pair_qblocks), which evens out the work,
+    // and the key split then follows the halved grid (fast kernel, measured:
+    // d128 B2 H32 N4096 356.6 -> 331.6 us, d64 B1 H32 N4096 102.3 -> 92.1
+    // us, d64 B1 H16 N4096 51.7 -> 49.4 us; at 256 workgroups pairing
+    // would idle half the CUs).  NESO_AMD_FA2_PAIR = 0 / 1 forces it.
+    if (a.pair_qblocks < 0)
+      a.pair_qblocks = (full_causal && wgs >= 2 * cus) ? 1 : 0;
+    if (causal && a.pair_qblocks == 1 && a.ksplit <= 0) {
+      const int64_t pwgs = (int64_t)((a.num_qblocks + 1) / 2) * a.batch_heads;
+      ksplit = pwgs < 2 * cus ? 2 : 1;
+    }
     return launch_fa2_fast(a, head_dim, causal, out_f16, ksplit, stream);
+  }
   // Generic kernel on a small grid: 64-query workgroups (two query waves per
   // key group) and four key groups double the grid, still one round of
   // workgroups, with eight waves each.  With more workgroups the doubled

@@ -66,6 +66,15 @@ int env_qwaves() {
   return (k == 2 || k == 4) ? k : 0;
 }
 
+// Paired query blocks for causal calls on the generic FA2 kernel:
+// NESO_AMD_FA2_PAIR=1 forces them, 0 forbids them; unset lets the launcher
+// choose.
+int env_pair() {
+  const char* v = getenv("NESO_AMD_FA2_PAIR");
+  if (!v) return -1;
+  return atoi(v) ? 1 : 0;
+}
+
 int check_head_dim(int32_t d) {
   if (d == 32 || d == 64 || d == 128) return NESO_OK;
   return fail(NESO_EUNSUPPORTED, "head_dim %d not supported (32, 64, 128)", d);
@@ -258,6 +267,7 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
   a.ksplit = env_ksplit();
   a.allow_fast = env_allow_fast();
   a.qwaves = env_qwaves();
+  a.pair_qblocks = env_pair();
   // Causal is the window (N, 0); windows wider than N are clamped to N.
   a.win_left = win_left < 0 ? N : (win_left < N ? win_left : N);
   a.win_right = win_right < 0 ? 0 : (win_right < N ? win_right : N);

@@ -119,3 +119,30 @@ def test_fast_equals_generic(gpu, monkeypatch):
     monkeypatch.setenv("NESO_AMD_FA2_FAST", "0")
     generic = run(q, k, v)
     assert (fast - generic).abs().max().item() <= 1e-3
+
+
+@pytest.mark.parametrize("ksplit", [1, 2])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("n", [1, 128, 129, 384, 1000, 1500])
+def test_fast_paired_causal_blocks(gpu, monkeypatch, ksplit, d, n):
+    """Fast kernel, causal, with paired query blocks (workgroup x takes
+    blocks nqb-1-x and x; an odd middle block once)."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
+    monkeypatch.setenv("NESO_AMD_FA2_PAIR", "1")
+    q, k, v = I.fa2_inputs(1, 3, n, d, seed=n + d + ksplit)
+    check(q, k, v, causal=True)
+
+
+@pytest.mark.parametrize("n,wl,wr", [(300, 100, 37), (1500, 128, 128), (1000, 1000, 0)])
+def test_fast_paired_windows(gpu, monkeypatch, n, wl, wr):
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_PAIR", "1")
+    heads, d = 2, 64
+    q, k, v = (t[0].permute(1, 0, 2).contiguous() for t in I.fa2_inputs(1, heads, n, d, seed=n))
+    dev = torch.device("cuda:0")
+    out = neso_amd.window_attention(q.to(dev), k.to(dev), v.to(dev), wl, wr,
+                                    out_dtype=torch.float32).cpu()
+    qh, kh, vh = (t.permute(1, 0, 2) for t in (q, k, v))
+    ref = A.attention(qh, kh, vh, 1 / math.sqrt(d), window=(wl, wr)).permute(1, 0, 2)
+    assert (out - ref).abs().max().item() <= TOL
