@@ -236,7 +236,7 @@ def main():
                      "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("fa2_headline"),
-                     "kernel": "fa2_fast_kernel<64,false,false,2>",
+                     "kernel": "fa2_fast_kernel<64,false,false,2,false>",
                      "algorithmic_flop_per_launch": flop},
     }
 
