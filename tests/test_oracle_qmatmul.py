@@ -116,7 +116,7 @@ def test_rel_err_metric():
 
 
 def test_algorithmic_bytes_baseline():
-    # M=1, K=4096, N=11008 -> 25,392,640 bytes.
+    # M=1, K=4096, N=11008: K*N/2 + (K/32)*N*2 + M*K*2 + M*N*2 = 25,392,640 bytes.
     assert Q.algorithmic_bytes(1, 11008, 4096) == 25_392_640
 
 
