@@ -415,6 +415,7 @@ static int w8a16_common(const void* A, const int8_t* B, float* C, const void* sc
   if (!aligned2(A) || (scale && !aligned2(scale)) || (reinterpret_cast<uintptr_t>(C) & 3u))
     return fail(NESO_EINVAL, "%s: misaligned A/C/scale", name);
   if (M == 0 || N == 0) return ok();
+  if (K == 0) return fail(NESO_EINVAL, "%s: K=0 with non-empty output", name);
   neso::W8Args a{};
   a.A = static_cast<const neso::half_t*>(A);
   a.B = B;

@@ -844,7 +844,10 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
   const int mrows = min(kW8BM, a.M - m0);
   constexpr uint32_t kOut = 0x80000000u;
   const rsrc_t ra = make_rsrc(a.A + (int64_t)m0 * a.lda, (uint32_t)((mrows - 1) * a.lda + a.K) * 2u);
-  const rsrc_t rb = make_rsrc(a.B + n0, (uint32_t)((a.K - 1) * (int64_t)a.ldb + min(kW8BN, a.N - n0)));
+  // K >= 1 (the ABI rejects K = 0 with a non-empty output); the extent is
+  // clamped at 0 anyway so a bad call cannot wrap it to ~4 GiB.
+  const rsrc_t rb = make_rsrc(
+      a.B + n0, (uint32_t)max((int64_t)0, (a.K - 1) * (int64_t)a.ldb + min(kW8BN, a.N - n0)));
   // A: rows (tid >> 2) + 64j, 16-byte piece tid & 3 of the step.
   const int ar = tid >> 2, ap = tid & 3;
   // B: column chunk c (8 columns), k pair kp.
@@ -1036,8 +1039,11 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
   // (K = 4096, N = 11008, GEMV / MFMA: M = 1 6.6 / 8.7 us, M = 2 8.6 / 8.7,
   // M = 3 11.1 / 8.7, M = 4 13.8 / 8.7).  NESO_AMD_W4_GEMV_MAX_M = 0..4
   // overrides the largest GEMV M.
+  // Values outside 0..4 fall back to the default: the GEMV kernels hold
+  // at most four rows of X.
   const char* gemv_env = getenv("NESO_AMD_W4_GEMV_MAX_M");
-  const int gemv_max_m = gemv_env ? atoi(gemv_env) : 2;
+  const int gemv_env_m = gemv_env ? atoi(gemv_env) : -1;
+  const int gemv_max_m = (gemv_env_m >= 0 && gemv_env_m <= 4) ? gemv_env_m : 2;
   if (a.M <= gemv_max_m && a.K <= w4a16_gemv_max_k()) {
     switch (a.M) {
       case 1: return launch_gemv_mr<1>(a, s);

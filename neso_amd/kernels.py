@@ -56,6 +56,27 @@ def _ptr(x: Any, name: str, dtype: torch.dtype | tuple[torch.dtype, ...] | None)
     return x.data_ptr()
 
 
+def _extent(x: Any, name: str, elems: int) -> None:
+    """Raise ValueError if tensor ``x`` cannot hold ``elems`` elements from its
+    first element on (the extent the declared sizes and strides imply).
+
+    The kernels bound their loads by the declared sizes, not by the tensor,
+    so a short tensor would be read or written past its allocation.  Raw
+    integer addresses are the caller's responsibility.
+    """
+    if not isinstance(x, torch.Tensor) or elems <= 0:
+        return
+    avail = x.untyped_storage().nbytes() - x.storage_offset() * x.element_size()
+    if elems * x.element_size() > avail:
+        raise ValueError(f"{name}: the declared sizes and strides span {elems} elements but the "
+                         f"tensor holds {avail // x.element_size()} from its first element")
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
 def _stream(stream: Any, *tensors: Any) -> int:
     if stream is not None:
         return int(stream.cuda_stream) if hasattr(stream, "cuda_stream") else int(stream)
@@ -87,6 +108,12 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
         qkv_dtype = "f32" if isinstance(Q, torch.Tensor) and Q.dtype == torch.float32 else "f16"
     if qkv_dtype not in ("f16", "f32"):
         raise ValueError(f"qkv_dtype must be 'f16' or 'f32', got {qkv_dtype!r}")
+    if N > 0 and batch_heads > 0:
+        span_q = (batch_heads - 1) * stride_bh_qo + (N - 1) * stride_qo + head_dim
+        span_kv = (batch_heads - 1) * stride_bh_kv + (N - 1) * stride_kv + head_dim
+        for t, nm, sp in ((Q, "Q", span_q), (K, "K", span_kv), (V, "V", span_kv),
+                          (O, "O", span_q)):
+            _extent(t, nm, sp)
     lib = _lib.load()
     dt = torch.float32 if qkv_dtype == "f32" else torch.float16
     fn = lib.neso_flash_attention_f32_fwd if qkv_dtype == "f32" else lib.neso_flash_attention_fwd
@@ -120,6 +147,10 @@ def flash_attention_window_fwd(Q, K, V, O, seq_len: int, stride_h: int, stride_m
         out_dtype = _lib.NESO_OUT_F32 if O.dtype == torch.float32 else _lib.NESO_OUT_F16
     else:
         out_dtype = _lib.NESO_OUT_F16
+    if seq_len > 0 and num_heads > 0:
+        span = (seq_len - 1) * stride_m + (num_heads - 1) * stride_h + head_dim
+        for t, nm in ((Q, "Q"), (K, "K"), (V, "V"), (O, "O")):
+            _extent(t, nm, span)
     lib = _lib.load()
     st = lib.neso_flash_attention_window_fwd(
         _ptr(Q, "Q", torch.float16), _ptr(K, "K", torch.float16), _ptr(V, "V", torch.float16),
@@ -151,6 +182,12 @@ def rel_pos_fa2_fwd(Q, K, V, bias, O, T: int, stride: int, scale: float, stride_
     else:
         out_dtype = _lib.NESO_OUT_F16
     bias_dtype = torch.float16 if bias_mode == _lib.NESO_BIAS_DENSE_SCALED_F16 else torch.float32
+    if T > 0 and num_heads > 0:
+        span = (num_heads - 1) * stride_h + (T - 1) * stride + head_dim
+        for t, nm in ((Q, "Q"), (K, "K"), (V, "V"), (O, "O")):
+            _extent(t, nm, span)
+        per_head = T * T if bias_mode == _lib.NESO_BIAS_DENSE_SCALED_F16 else 2 * T - 1
+        _extent(bias, "bias", (num_heads - 1) * bias_stride_h + per_head)
     lib = _lib.load()
     st = lib.neso_rel_pos_fa2_fwd(
         _ptr(Q, "Q", torch.float16), _ptr(K, "K", torch.float16), _ptr(V, "V", torch.float16),
@@ -163,6 +200,11 @@ def rel_pos_fa2_fwd(Q, K, V, bias, O, T: int, stride: int, scale: float, stride_
 def w4a16_matmul(X, W, scales, Y, M: int, N: int, K: int, stride_xm: int, stride_ym: int,
                  group_size: int = 32, zero_point: int = 8, *, stream=None) -> None:
     """Y[M, N] fp16 = X[M, K] fp16 @ dequant(W)^T, W int32 [N, K/8] (int4, low nibble first)."""
+    if M > 0 and N > 0 and K > 0 and group_size > 0:
+        _extent(X, "X", (M - 1) * stride_xm + K)
+        _extent(W, "W", N * (K // 8))
+        _extent(scales, "scales", N * (K // group_size))
+        _extent(Y, "Y", (M - 1) * stride_ym + N)
     lib = _lib.load()
     st = lib.neso_w4a16_matmul(
         _ptr(X, "X", torch.float16), _ptr(W, "W", torch.int32), _ptr(scales, "scales", torch.float16),
@@ -171,9 +213,18 @@ def w4a16_matmul(X, W, scales, Y, M: int, N: int, K: int, stride_xm: int, stride
     _lib.check(st)
 
 
+def _w8_extents(A, B, C, scale, K, stride_am, stride_bk, stride_cm, M, N) -> None:
+    if M > 0 and N > 0 and K > 0:
+        _extent(A, "A", (M - 1) * stride_am + K)
+        _extent(B, "B", (K - 1) * stride_bk + N)
+        _extent(C, "C", (M - 1) * stride_cm + N)
+        _extent(scale, "scale", N)
+
+
 def w8a16_matmul(A, B, C, K: int, stride_am: int, stride_bk: int, stride_cm: int, *, M: int,
                  N: int, stream=None) -> None:
     """C fp32 = A fp16 @ f16(B int8 [K, N]) (tests/test_quantized_matmul.py:77-80 order)."""
+    _w8_extents(A, B, C, None, K, stride_am, stride_bk, stride_cm, M, N)
     lib = _lib.load()
     st = lib.neso_w8a16_matmul(
         _ptr(A, "A", torch.float16), _ptr(B, "B", torch.int8), _ptr(C, "C", torch.float32), int(K),
@@ -184,6 +235,7 @@ def w8a16_matmul(A, B, C, K: int, stride_am: int, stride_bk: int, stride_cm: int
 def w8a16_scaled_matmul(A, B, C, scale, K: int, stride_am: int, stride_bk: int, stride_cm: int,
                         *, M: int, N: int, stream=None) -> None:
     """C = (A @ f16(B)) * scale[n] (tests/test_quantized_matmul.py:189-192 order)."""
+    _w8_extents(A, B, C, scale, K, stride_am, stride_bk, stride_cm, M, N)
     lib = _lib.load()
     st = lib.neso_w8a16_scaled_matmul(
         _ptr(A, "A", torch.float16), _ptr(B, "B", torch.int8), _ptr(C, "C", torch.float32),
@@ -228,6 +280,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
     bh = q.numel() // max(n * d, 1) if n * d else 0
     if out is None:
         out = torch.empty(q.shape, dtype=torch.float32, device=q.device)
+    _require(out.shape == q.shape and out.is_contiguous() and out.dtype == torch.float32,
+             f"out must be a contiguous fp32 tensor of shape {tuple(q.shape)}")
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     flash_attention_fwd(q, k, v, out, n, d, d, scale, head_dim=d, batch_heads=bh,
                         stride_bh_qo=n * d, stride_bh_kv=n * d, causal=causal)
@@ -238,9 +292,21 @@ def rel_pos_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: 
                       scale: float | None = None, out_dtype: torch.dtype = torch.float32,
                       out: torch.Tensor | None = None) -> torch.Tensor:
     """softmax(Q K^T * scale + table[h, i - j + N - 1]) V for [H, N, d] fp16, table f32 [H, 2N-1]."""
+    _require(q.dim() == 3, f"q must be [H, N, d], got {tuple(q.shape)}")
+    _require(k.shape == q.shape and v.shape == q.shape,
+             f"k {tuple(k.shape)} and v {tuple(v.shape)} must match q {tuple(q.shape)}")
+    _require(q.is_contiguous() and k.is_contiguous() and v.is_contiguous(),
+             "q, k, v must be contiguous")
+    _require(q.dtype == k.dtype == v.dtype == torch.float16, "q, k, v must be fp16")
     h, n, d = (int(s) for s in q.shape)
     if table.shape != (h, 2 * n - 1):
         raise ValueError(f"table must be [H, 2N-1] = [{h}, {2 * n - 1}], got {tuple(table.shape)}")
+    _require(table.is_contiguous() and table.dtype == torch.float32,
+             "table must be a contiguous fp32 tensor")
+    _require(out_dtype in (torch.float16, torch.float32), "out_dtype must be fp16 or fp32")
+    if out is not None:
+        _require(out.shape == q.shape and out.is_contiguous() and out.dtype == out_dtype,
+                 f"out must be a contiguous {out_dtype} tensor of shape {tuple(q.shape)}")
     if out is None:
         out = torch.empty((h, n, d), dtype=out_dtype, device=q.device)
     scale = 1.0 / math.sqrt(d) if scale is None else scale
@@ -262,6 +328,9 @@ def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_l
     n, h, d = (int(x) for x in q.shape)
     if out is None:
         out = torch.empty((n, h, d), dtype=out_dtype, device=q.device)
+    _require(out.shape == q.shape and out.is_contiguous()
+             and out.dtype in (torch.float16, torch.float32),
+             f"out must be a contiguous fp16 or fp32 tensor of shape {tuple(q.shape)}")
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     flash_attention_window_fwd(q, k, v, out, n, d, h * d, scale, window_left, window_right,
                                num_heads=h, head_dim=d)
@@ -272,8 +341,23 @@ def w4a16_linear(x: torch.Tensor, w_packed: torch.Tensor, scales: torch.Tensor, 
                  group_size: int = 32, zero_point: int = 8,
                  out: torch.Tensor | None = None) -> torch.Tensor:
     """x [M, K] fp16 @ dequant(w_packed [N, K/8] int32, scales [N, K/group])^T -> fp16 [M, N]."""
+    _require(x.dim() == 2 and x.stride(1) == 1, "x must be [M, K] with unit column stride")
     m, k = (int(s) for s in x.shape)
+    _require(w_packed.dim() == 2 and w_packed.is_contiguous() and w_packed.dtype == torch.int32,
+             "w_packed must be a contiguous int32 [N, K/8] tensor")
     n = int(w_packed.shape[0])
+    _require(k % 8 == 0 and int(w_packed.shape[1]) == k // 8,
+             f"w_packed must be [N, K/8] = [{n}, {k // 8}], got {tuple(w_packed.shape)}")
+    _require(group_size > 0 and k % group_size == 0,
+             f"group_size {group_size} must divide K = {k}")
+    _require(scales.dim() == 2 and scales.is_contiguous() and scales.dtype == torch.float16
+             and tuple(scales.shape) == (n, k // group_size),
+             f"scales must be a contiguous fp16 [N, K/group] = [{n}, {k // group_size}] tensor, "
+             f"got {tuple(scales.shape)} {scales.dtype}")
+    if out is not None:
+        _require(out.dim() == 2 and tuple(out.shape) == (m, n) and out.stride(1) == 1
+                 and out.dtype == torch.float16,
+                 f"out must be fp16 [M, N] = [{m}, {n}] with unit column stride")
     if out is None:
         out = torch.empty((m, n), dtype=torch.float16, device=x.device)
     w4a16_matmul(x, w_packed, scales, out, m, n, k, x.stride(0), out.stride(0), group_size,

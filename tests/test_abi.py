@@ -183,6 +183,14 @@ def test_w8a16_validation(lib, scaled):
         bad = list(good)
         bad[3] = None
         assert fn(*bad) == _lib.NESO_EINVAL
+    # K = 0 with a non-empty output is rejected before any launch (the
+    # kernel's B extent would otherwise be negative); with M = 0 it is a no-op.
+    bad = list(good)
+    bad[-7], bad[-3] = 0, 64  # K = 0, M = 64
+    assert fn(*bad) == _lib.NESO_EINVAL
+    assert b"K=0" in lib.neso_last_error()
+    bad[-3] = 0
+    assert fn(*bad) == _lib.NESO_OK
 
 
 def test_python_wrappers_raise():
@@ -211,3 +219,44 @@ def test_ctypes_signatures_are_c_types():
     for name, (res, args) in _lib.SIGNATURES.items():
         for a in args:
             assert issubclass(a, ctypes._SimpleCData), (name, a)
+
+
+def test_tensor_wrappers_validate_before_launch():
+    """Shape, dtype and extent errors raise ValueError before the ABI is called
+    (CPU tensors here: the shape message must come first, not "no CPU path")."""
+    f16 = torch.float16
+    x = torch.zeros(2, 64, dtype=f16)
+    w = torch.zeros(16, 8, dtype=torch.int32)
+    s = torch.zeros(16, 2, dtype=f16)
+    neso_amd_err = "w_packed must be"
+    with pytest.raises(ValueError, match=neso_amd_err):
+        neso_amd.w4a16_linear(x, torch.zeros(16, 4, dtype=torch.int32), s)
+    with pytest.raises(ValueError, match="scales must be"):
+        # scales made for group 128 passed with the default group 32
+        neso_amd.w4a16_linear(x, w, torch.zeros(16, 1, dtype=f16))
+    with pytest.raises(ValueError, match="group_size"):
+        neso_amd.w4a16_linear(x, w, s, group_size=48)
+    with pytest.raises(ValueError, match="out must be"):
+        neso_amd.w4a16_linear(x, w, s, out=torch.zeros(2, 8, dtype=f16))
+    q = torch.zeros(2, 16, 64, dtype=f16)
+    table = torch.zeros(2, 31, dtype=torch.float32)
+    with pytest.raises(ValueError, match="must match q"):
+        neso_amd.rel_pos_attention(q, torch.zeros(2, 8, 64, dtype=f16), q, table)
+    with pytest.raises(ValueError, match="table must be"):
+        neso_amd.rel_pos_attention(q, q, q, torch.zeros(2, 30, dtype=torch.float32))
+    with pytest.raises(ValueError, match="fp32"):
+        neso_amd.rel_pos_attention(q, q, q, table.double())
+    with pytest.raises(ValueError, match="out must be"):
+        neso_amd.attention(q, q, q, out=torch.zeros(2, 16, 64, dtype=f16))
+    # Reference-order launchers: a tensor shorter than the declared extent.
+    with pytest.raises(ValueError, match="span"):
+        neso_amd.flash_attention_fwd(q, q, q, torch.zeros(2, 16, 64), 16, 64, 64, 0.125,
+                                     batch_heads=3, stride_bh_qo=1024, stride_bh_kv=1024)
+    with pytest.raises(ValueError, match="span"):
+        neso_amd.w4a16_matmul(x, w, s, torch.zeros(1, 16, dtype=f16), 2, 16, 64, 64, 16)
+    with pytest.raises(ValueError, match="span"):
+        neso_amd.w8a16_matmul(x, torch.zeros(64, 8, dtype=torch.int8),
+                              torch.zeros(2, 16), 64, 64, 16, 16, M=2, N=16)
+    with pytest.raises(ValueError, match="span"):
+        neso_amd.rel_pos_fa2_fwd(q, q, q, torch.zeros(2, 16, 15, dtype=f16), q, 16, 64, 0.125,
+                                 1024, 256, num_heads=2)
