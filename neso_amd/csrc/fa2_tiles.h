@@ -87,4 +87,40 @@ __device__ __forceinline__ half8v v_frag_tr(const half_t* v_l, int off, int cc) 
   return half8v{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 }
 
+// Chunk swizzle of the K rows: chunk c of key row r sits at chunk
+// c ^ kswz(r).  A K fragment read takes one chunk from each of 16 rows per
+// 16-lane pass, rows 0..15 of a 32-row tile in kRowPerm order.  D = 64: a
+// 128-byte row covers half the banks, so rows of equal parity need 8
+// distinct chunk positions, which bits 1..3 of r give.  D = 128: a row
+// covers all banks, so the 16 rows need 16 positions, bits 0..3 of r.
+template <int D>
+__device__ __forceinline__ int kswz(int r) {
+  static_assert(D == 64 || D == 128, "head dim");
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+}
+
+// s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+
+// 16 bytes per lane from the buffer into LDS (buffer_load_dwordx4 ... lds):
+// lane l's bytes land at LDS byte address lds + 16 l.  Written as asm so
+// that the compiler does not make the kernel's LDS reads wait for it (it
+// cannot tell that they read other slots); the kernel orders these writes
+// itself with s_waitcnt vmcnt(0) and a barrier before the slot is read.
+// Vector loads only; M0 holds the LDS base (one wait state after writing
+// it).  The compiler treats M0 as reserved and ignores the clobber; these
+// kernels use M0 nowhere else (checked in their ISA).
+__device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds, uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(lds), "v"(voff), "s"(r)
+      : "m0");
+}
+__device__ __forceinline__ uint32_t lds_addr(const half_t* p) {
+  return (uint32_t)(size_t)(__attribute__((address_space(3))) const half_t*)p;
+}
+
 }  // namespace neso
