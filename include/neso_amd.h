@@ -37,6 +37,10 @@ extern "C" {
 #define NESO_OUT_F16 0
 #define NESO_OUT_F32 1
 
+/* element type of Q, K, V and O for neso_flash_attention_io_fwd */
+#define NESO_IO_F16 0
+#define NESO_IO_F32 1
+
 /* Version of this ABI (bumped on any signature change). */
 int neso_abi_version(void);
 
@@ -93,6 +97,23 @@ int neso_flash_attention_f32_fwd(const float* Q, const float* K, const float* V,
                                  int32_t N, int32_t stride_qo, int32_t stride_kv, float scale,
                                  int32_t head_dim, int32_t batch_heads, int64_t stride_bh_qo,
                                  int64_t stride_bh_kv, int32_t causal, void* stream);
+
+/*
+ * Flash-Attention-2 forward with O in the input type.  Replaces the
+ * hand-written `flash_attention_fwd(Q, K, V, O, N, d_head, scale)` kernel of
+ * bench/bench_flash_attention.py:142-152 (buffers 0-3, scalars 4-6, io_type
+ * half or float for all four buffers; O row r at r * d_head, :361).  The
+ * first seven parameters keep that order and meaning:
+ *   Q, K, V, O  [N][d_head] rows of io_dtype, row stride d_head
+ *   N           sequence length; d_head 32, 64 or 128; scale as the reference
+ * Appended: io_dtype (NESO_IO_F16: fp16 Q/K/V/O, fp32 softmax and
+ * accumulation, O rounded to fp16 once at the end; NESO_IO_F32: fp32
+ * Q/K/V/O through the split-precision kernel of neso_flash_attention_f32_fwd),
+ * batch_heads (contiguous [batch_heads][N][d_head] slices, >= 1) and stream.
+ */
+int neso_flash_attention_io_fwd(const void* Q, const void* K, const void* V, void* O, int32_t N,
+                                int32_t d_head, float scale, int32_t io_dtype,
+                                int32_t batch_heads, void* stream);
 
 /*
  * Sliding-window attention.  Replaces the windowed `flash_attention_fwd`

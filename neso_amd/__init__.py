@@ -11,6 +11,8 @@ from ._lib import (  # noqa: F401
     NESO_EINVAL,
     NESO_ELAUNCH,
     NESO_EUNSUPPORTED,
+    NESO_IO_F16,
+    NESO_IO_F32,
     NESO_OK,
     NESO_OUT_F16,
     NESO_OUT_F32,
@@ -21,6 +23,7 @@ from .kernels import (  # noqa: F401
     KERNELS,
     attention,
     flash_attention_fwd,
+    flash_attention_io_fwd,
     flash_attention_window_fwd,
     launch,
     rel_pos_attention,

@@ -24,6 +24,8 @@ NESO_BIAS_DENSE_SCALED_F16 = 0
 NESO_BIAS_TABLE_F32 = 1
 NESO_OUT_F16 = 0
 NESO_OUT_F32 = 1
+NESO_IO_F16 = 0
+NESO_IO_F32 = 1
 
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
@@ -43,6 +45,10 @@ SIGNATURES = {
     "neso_flash_attention_f32_fwd": (
         ctypes.c_int,
         [_p, _p, _p, _p, _i32, _i32, _i32, _f32, _i32, _i32, _i64, _i64, _i32, _p],
+    ),
+    "neso_flash_attention_io_fwd": (
+        ctypes.c_int,
+        [_p, _p, _p, _p, _i32, _i32, _f32, _i32, _i32, _p],
     ),
     "neso_flash_attention_window_fwd": (
         ctypes.c_int,

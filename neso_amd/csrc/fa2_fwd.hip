@@ -50,9 +50,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLazyLog2 = 8.f;  // rescale threshold (log2 units)
 
 // Keys per LDS block.  64 measured faster than 128 at d = 64 on MI355X
-// (fewer live registers; the extra barriers are not the bottleneck).
-template <int D>
-constexpr int key_block() { return 64; }
+// (fewer live registers; the extra barriers are not the bottleneck).  fp32
+// input at d = 128 uses 32: its slots hold the hi and lo halves of K and V,
+// and two 32-key slots per key group keep two key groups within the LDS
+// (and the fp32 staging registers within the register file).
+template <int D, bool F32IN = false>
+constexpr int key_block() { return (F32IN && D == 128) ? 32 : 64; }
 
 // One 8-element row piece of K or V in registers: f16, or f32 (two float4).
 template <bool F32IN>
@@ -66,7 +69,7 @@ struct Piece8<true> {
 
 template <int D, bool F32IN, int GT>
 struct Staging {
-  static constexpr int kKB = key_block<D>();
+  static constexpr int kKB = key_block<D, F32IN>();
   static constexpr int KCH = kKB * D / 8 / GT;   // 8-element K (and V) pieces per thread
   Piece8<F32IN> k[KCH];
   Piece8<F32IN> v[KCH];
@@ -89,7 +92,7 @@ template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int KSPLIT, bool F32IN, in
 __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   constexpr int kBM = 32 * QW;      // queries per workgroup (QW waves of 32)
   constexpr int kGroup = 64 * QW;   // threads per key group
-  constexpr int kKB = key_block<D>();
+  constexpr int kKB = key_block<D, F32IN>();
   constexpr int NT = kKB / 32; // 32-key tiles per block
   constexpr int KS = D / 16;   // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;   // 32-row tiles of O^T
@@ -490,7 +493,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
 // Static LDS of one workgroup with K key groups.
 template <int D, int BIAS, bool F32IN, int QW>
 constexpr int fa2_lds_bytes(int K) {
-  constexpr int kb = key_block<D>();
+  constexpr int kb = key_block<D, F32IN>();
   const int slot = (kb * (D + 8) + kb * D) * 2 * (F32IN ? 2 : 1);
   const int bias = BIAS == kBiasTableF32 ? (32 * QW + kb) * 4 : 4;
   return K * 2 * (slot + bias);
@@ -536,7 +539,7 @@ hipError_t launch_fa2_c(const Fa2Args& a, bool causal, int ksplit, hipStream_t s
   return launch_fa2_t<D, false, BIAS, OUT_F16>(a, ksplit, s);
 }
 
-// f32 Q/K/V (split into f16 hi + lo), no bias, f32 output, d <= 64.
+// f32 Q/K/V (split into f16 hi + lo), no bias, f32 output.
 hipError_t launch_fa2_f32in(const Fa2Args& a, int d, bool causal, int ksplit, hipStream_t s) {
   switch (d) {
     case 32:
@@ -545,6 +548,9 @@ hipError_t launch_fa2_f32in(const Fa2Args& a, int d, bool causal, int ksplit, hi
     case 64:
       return causal ? launch_fa2_t<64, true, kBiasNone, false, true>(a, ksplit, s)
                     : launch_fa2_t<64, false, kBiasNone, false, true>(a, ksplit, s);
+    case 128:
+      return causal ? launch_fa2_t<128, true, kBiasNone, false, true>(a, ksplit, s)
+                    : launch_fa2_t<128, false, kBiasNone, false, true>(a, ksplit, s);
     default: return hipErrorInvalidValue;
   }
 }

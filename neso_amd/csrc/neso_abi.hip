@@ -122,6 +122,18 @@ const char kManifest[] = R"JSON({
      "threadgroup_size": 256, "block_m": 128, "head_dims": [32, 64],
      "precision": "f32 inputs split into f16 hi + lo, three f16 MFMAs per product, f32 accumulation",
      "grid": ["cdiv(N, 128) * batch_heads", "1", "1"]},
+    {"name": "neso_flash_attention_io_fwd", "replaces": "flash_attention_fwd(Q, K, V, O, N, d_head, scale) (bench/bench_flash_attention.py:142-152)",
+     "params": [
+      {"index": 0, "name": "Q", "type": "const fp16*|const fp32*", "is_pointer": true},
+      {"index": 1, "name": "K", "type": "const fp16*|const fp32*", "is_pointer": true},
+      {"index": 2, "name": "V", "type": "const fp16*|const fp32*", "is_pointer": true},
+      {"index": 3, "name": "O", "type": "fp16*|fp32*", "is_pointer": true},
+      {"index": 4, "name": "N", "type": "int32", "is_pointer": false},
+      {"index": 5, "name": "d_head", "type": "int32", "is_pointer": false},
+      {"index": 6, "name": "scale", "type": "fp32", "is_pointer": false},
+      {"index": 7, "name": "io_dtype", "type": "int32", "is_pointer": false},
+      {"index": 8, "name": "batch_heads", "type": "int32", "is_pointer": false},
+      {"index": 9, "name": "stream", "type": "hipStream_t", "is_pointer": true}]},
     {"name": "neso_flash_attention_window_fwd", "replaces": "flash_attention_fwd with window_left/right (debug/fa2_correctness_legacy.py:92-102)",
      "params": [
       {"index": 0, "name": "Q", "type": "const fp16*", "is_pointer": true},
@@ -216,9 +228,6 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
   if (heads < 0) return fail(NESO_EINVAL, "%s: batch_heads=%d < 0", name, heads);
   int st = check_head_dim(head_dim);
   if (st != NESO_OK) return st;
-  if (in_f32 && head_dim > 64)
-    return fail(NESO_EUNSUPPORTED, "%s: f32 Q/K/V supports head_dim 32 and 64, got %d", name,
-                head_dim);
   if (!isfinite(scale)) return fail(NESO_EINVAL, "%s: scale is not finite", name);
   if (causal != 0 && causal != 1) return fail(NESO_EINVAL, "%s: causal=%d", name, causal);
   if (stride_q < head_dim || stride_kv < head_dim || stride_o < head_dim)
@@ -333,6 +342,19 @@ int neso_flash_attention_f32_fwd(const float* Q, const float* K, const float* V,
   return fa2_common(Q, K, V, O, nullptr, N, stride_qo, stride_kv, stride_qo, scale, head_dim,
                     batch_heads, stride_bh_qo, stride_bh_kv, stride_bh_qo, 0, causal,
                     neso::kBiasNone, false, stream, "flash_attention_f32_fwd", -1, -1, true);
+}
+
+int neso_flash_attention_io_fwd(const void* Q, const void* K, const void* V, void* O, int32_t N,
+                                int32_t d_head, float scale, int32_t io_dtype,
+                                int32_t batch_heads, void* stream) {
+  const char* name = "flash_attention_io_fwd";
+  if (io_dtype != NESO_IO_F16 && io_dtype != NESO_IO_F32)
+    return fail(NESO_EINVAL, "%s: io_dtype=%d", name, io_dtype);
+  const bool f32 = io_dtype == NESO_IO_F32;
+  // Rows are d_head apart and slices N rows apart (the reference's layout).
+  const int64_t slice = (int64_t)N * d_head;
+  return fa2_common(Q, K, V, O, nullptr, N, d_head, d_head, d_head, scale, d_head, batch_heads,
+                    slice, slice, slice, 0, 0, neso::kBiasNone, !f32, stream, name, -1, -1, f32);
 }
 
 int neso_flash_attention_window_fwd(const void* Q, const void* K, const void* V, void* O,

@@ -25,6 +25,7 @@ from . import _lib
 
 __all__ = [
     "flash_attention_fwd",
+    "flash_attention_io_fwd",
     "flash_attention_window_fwd",
     "rel_pos_fa2_fwd",
     "w4a16_matmul",
@@ -122,6 +123,35 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
         _ptr(O, "O", torch.float32), int(N), int(stride_qo), int(stride_kv), float(scale),
         int(head_dim), int(batch_heads), int(stride_bh_qo), int(stride_bh_kv), int(bool(causal)),
         _stream(stream, Q, O))
+    _lib.check(st)
+
+
+def flash_attention_io_fwd(Q, K, V, O, N: int, d_head: int, scale: float, *,
+                           batch_heads: int = 1, io_dtype: str | None = None,
+                           stream=None) -> None:
+    """FA2 forward with O in the input type, O = softmax(Q K^T * scale) V.
+
+    Positional arguments as the hand-written reference kernel
+    (bench/bench_flash_attention.py:142-152): Q, K, V, O [N, d_head] rows of
+    one type (``io_type`` half or float there), N, d_head, scale.  Keyword
+    extensions: ``batch_heads`` contiguous [batch_heads, N, d_head] slices in
+    one launch; ``io_dtype`` 'f16' or 'f32' (inferred from Q for tensors).
+    """
+    if io_dtype is None:
+        if not isinstance(Q, torch.Tensor):
+            raise ValueError("io_dtype is required when Q is a raw address")
+        io_dtype = "f32" if Q.dtype == torch.float32 else "f16"
+    if io_dtype not in ("f16", "f32"):
+        raise ValueError(f"io_dtype must be 'f16' or 'f32', got {io_dtype!r}")
+    if N > 0 and batch_heads > 0:
+        for t, nm in ((Q, "Q"), (K, "K"), (V, "V"), (O, "O")):
+            _extent(t, nm, batch_heads * N * d_head)
+    dt = torch.float32 if io_dtype == "f32" else torch.float16
+    lib = _lib.load()
+    st = lib.neso_flash_attention_io_fwd(
+        _ptr(Q, "Q", dt), _ptr(K, "K", dt), _ptr(V, "V", dt), _ptr(O, "O", dt), int(N),
+        int(d_head), float(scale), _lib.NESO_IO_F32 if io_dtype == "f32" else _lib.NESO_IO_F16,
+        int(batch_heads), _stream(stream, Q, O))
     _lib.check(st)
 
 
@@ -246,6 +276,7 @@ def w8a16_scaled_matmul(A, B, C, scale, K: int, stride_am: int, stride_bk: int, 
 
 KERNELS = {
     "flash_attention_fwd": flash_attention_fwd,
+    "flash_attention_io_fwd": flash_attention_io_fwd,
     "flash_attention_window_fwd": flash_attention_window_fwd,
     "rel_pos_fa2_fwd": rel_pos_fa2_fwd,
     "w4a16_matmul": w4a16_matmul,

@@ -204,7 +204,7 @@ def qmm_int4_kat() -> None:
 
 def main() -> int:
     fa2_kat()
-    for n, d in ((64, 32), (128, 64), (256, 64), (128, 128)):
+    for n, d in ((64, 32), (128, 64), (256, 64), (128, 128), (256, 128), (512, 128)):
         fa2_ref_rows(n, d)
     relpos_ref(32, 64, 2)
     relpos_ref(64, 64, 4)

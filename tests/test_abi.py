@@ -109,7 +109,8 @@ def fa2_f32(lib, **kw):
 
 
 @pytest.mark.parametrize("kw,status", [
-    (dict(head_dim=128, stride_qo=128, stride_kv=128), _lib.NESO_EUNSUPPORTED),
+    (dict(head_dim=128, stride_qo=128, stride_kv=128), _lib.NESO_OK),
+    (dict(head_dim=96, stride_qo=96, stride_kv=96), _lib.NESO_EUNSUPPORTED),
     (dict(stride_qo=66), _lib.NESO_EINVAL),          # f32 rows need multiples of 4
     (dict(stride_qo=68, stride_kv=68), _lib.NESO_OK),  # ... not of 8
     (dict(stride_bh_kv=6), _lib.NESO_EINVAL),
@@ -119,6 +120,28 @@ def fa2_f32(lib, **kw):
 ])
 def test_fa2_f32_validation(lib, kw, status):
     assert fa2_f32(lib, **kw) == status
+
+
+def fa2_io(lib, **kw):
+    args = dict(Q=A16, K=A16, V=A16, O=A16, N=0, d_head=64, scale=0.125, io_dtype=0,
+                batch_heads=1, stream=None)
+    args.update(kw)
+    return lib.neso_flash_attention_io_fwd(*args.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(), _lib.NESO_OK),
+    (dict(io_dtype=1), _lib.NESO_OK),
+    (dict(io_dtype=2), _lib.NESO_EINVAL),
+    (dict(O=None), _lib.NESO_EINVAL),
+    (dict(d_head=96), _lib.NESO_EUNSUPPORTED),
+    (dict(d_head=128, io_dtype=1), _lib.NESO_OK),
+    (dict(O=A16 + 8), _lib.NESO_EINVAL),
+    (dict(N=-3), _lib.NESO_EINVAL),
+    (dict(batch_heads=-1), _lib.NESO_EINVAL),
+])
+def test_fa2_io_validation(lib, kw, status):
+    assert fa2_io(lib, **kw) == status
 
 
 def relpos(lib, **kw):

@@ -41,7 +41,8 @@ def test_harness_kat(gpu, golden_dir):
     assert err <= 1e-5, err
 
 
-@pytest.mark.parametrize("n,d", [(64, 32), (128, 64), (256, 64), (128, 128)])
+@pytest.mark.parametrize("n,d", [(64, 32), (128, 64), (256, 64), (128, 128), (256, 128),
+                                 (512, 128)])
 def test_reference_rows(gpu, golden_dir, n, d):
     """Reference generator (tests/test_flash_attention.py:268-275), rows 0 and N/2."""
     z = np.load(golden_dir / f"fa2_ref_N{n}_d{d}.npz")

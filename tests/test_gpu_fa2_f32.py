@@ -35,7 +35,8 @@ def _run(q, k, v, causal=False, scale=None):
     return out.cpu()
 
 
-@pytest.mark.parametrize("n,d", [(64, 32), (128, 64), (256, 64)])
+@pytest.mark.parametrize("n,d", [(64, 32), (128, 64), (256, 64), (128, 128), (256, 128),
+                                 (512, 128)])
 def test_reference_rows(gpu, golden_dir, n, d):
     """Reference generator (random.seed(42), gauss(0, 0.5)) packed as f32, rows 0 and N/2."""
     z = np.load(golden_dir / f"fa2_ref_N{n}_d{d}.npz")
@@ -54,7 +55,13 @@ def test_reference_rows(gpu, golden_dir, n, d):
 
 @pytest.mark.parametrize("b,h,n,d,causal", [
     (1, 1, 1, 32, False), (1, 2, 77, 64, True), (2, 3, 300, 32, False), (1, 4, 1000, 64, True),
-    (1, 3, 129, 64, False), (1, 8, 2048, 64, False), (1, 2, 2048, 32, True)])
+    (1, 3, 129, 64, False), (1, 8, 2048, 64, False), (1, 2, 2048, 32, True),
+    # head_dim 128 (32-key blocks): the reference's d = 128 lengths
+    # (tests/test_flash_attention.py:405-418), ragged tails, causal, and
+    # grids that take both the 128- and the 64-query workgroups.
+    (1, 1, 128, 128, False), (1, 1, 256, 128, False), (1, 1, 512, 128, False),
+    (1, 2, 1, 128, False), (1, 3, 33, 128, True), (2, 2, 300, 128, False),
+    (1, 4, 777, 128, True), (1, 16, 2048, 128, False), (1, 64, 1024, 128, True)])
 def test_vs_fp64_oracle(gpu, b, h, n, d, causal):
     q, k, v = _inputs(b, h, n, d, seed=n + d)
     out = _run(q, k, v, causal=causal)
@@ -63,10 +70,11 @@ def test_vs_fp64_oracle(gpu, b, h, n, d, causal):
     assert err <= TOL32, err
 
 
-def test_split_beats_fp16_rounding(gpu):
+@pytest.mark.parametrize("d", [64, 128])
+def test_split_beats_fp16_rounding(gpu, d):
     """The f32 kernel must be far more accurate than rounding the inputs to fp16."""
-    q, k, v = _inputs(1, 2, 512, 64, seed=5)
-    ref = A.attention(q, k, v, 0.125, dtype=torch.float64)
+    q, k, v = _inputs(1, 2, 512, d, seed=5)
+    ref = A.attention(q, k, v, 1 / math.sqrt(d), dtype=torch.float64)
     err32 = (_run(q, k, v).double() - ref).abs().max().item()
     err16 = (_run(q.half(), k.half(), v.half()).double() - ref).abs().max().item()
     assert err16 > 1e-4  # fp16 rounding of the inputs alone is visible
@@ -109,8 +117,8 @@ def test_padded_strides_and_slices(gpu):
 def test_f32_errors(gpu):
     x = torch.zeros(128, 128, device=DEV)
     o = torch.zeros(128, 128, device=DEV)
-    with pytest.raises(neso_amd.NesoArgumentError):  # head_dim 128 has no f32 kernel
-        neso_amd.flash_attention_fwd(x, x, x, o, 128, 128, 128, 0.1, head_dim=128)
+    with pytest.raises(neso_amd.NesoArgumentError):  # head_dim 96 has no kernel
+        neso_amd.flash_attention_fwd(x, x, x, o, 128, 96, 96, 0.1, head_dim=96)
     y = torch.zeros(64 * 66, device=DEV)
     with pytest.raises(neso_amd.NesoArgumentError):  # row stride 66 is not a multiple of 4
         neso_amd.flash_attention_fwd(y, y, y, y, 64, 66, 66, 0.1, head_dim=64)

@@ -47,7 +47,8 @@ def test_query_rows_subset(causal, window):
     assert torch.equal(sub, full[..., rows, :])
 
 
-@pytest.mark.parametrize("n,d", [(64, 32), (128, 64), (256, 64), (128, 128)])
+@pytest.mark.parametrize("n,d", [(64, 32), (128, 64), (256, 64), (128, 128), (256, 128),
+                                 (512, 128)])
 def test_golden_reference_rows(golden_dir, n, d):
     """tests/test_flash_attention.py:268-275 inputs, :296-339 expected rows."""
     z = np.load(golden_dir / f"fa2_ref_N{n}_d{d}.npz")
