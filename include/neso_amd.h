@@ -56,6 +56,21 @@ const char* neso_last_error(void);
 const char* neso_kernel_manifest(void);
 
 /*
+ * Launch-plan recording (no GPU needed).  Between neso_plan_begin and
+ * neso_plan_end, calls made on this thread validate their arguments and
+ * choose their kernels exactly as usual, but record each kernel launch
+ * instead of issuing it; no HIP call is made.  cu_count > 0 stands in for
+ * the device's compute-unit count (0: the current device's).
+ * neso_plan_end returns JSON {"launches": [{"device_kernel", "template_args"
+ * (bools as 0/1), "grid": [x, y, z], "threadgroup_size", "num_warps"}]},
+ * valid until the next neso_plan_end on this thread.  It is how the
+ * manifest's per-variant geometry is checked against the launchers, the
+ * role of the reference's AOT metadata (src/neso/aot_compile.py:108-117).
+ */
+int neso_plan_begin(int32_t cu_count);
+const char* neso_plan_end(void);
+
+/*
  * Flash-Attention-2 forward.  Replaces the `flash_attention_fwd` kernel of
  * tests/test_flash_attention.py:149-153 (launched at :287-290 and by
  * macos/harness.rs:149-169 with buffers 0-3 = Q, K, V, O and scalars 4-7 =

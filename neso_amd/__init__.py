@@ -26,6 +26,8 @@ from .kernels import (  # noqa: F401
     flash_attention_io_fwd,
     flash_attention_window_fwd,
     launch,
+    launch_plan,
+    manifest,
     rel_pos_attention,
     rel_pos_fa2_fwd,
     w4a16_linear,

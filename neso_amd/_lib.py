@@ -38,6 +38,8 @@ SIGNATURES = {
     "neso_status_string": (ctypes.c_char_p, [ctypes.c_int]),
     "neso_last_error": (ctypes.c_char_p, []),
     "neso_kernel_manifest": (ctypes.c_char_p, []),
+    "neso_plan_begin": (ctypes.c_int, [_i32]),
+    "neso_plan_end": (ctypes.c_char_p, []),
     "neso_flash_attention_fwd": (
         ctypes.c_int,
         [_p, _p, _p, _p, _i32, _i32, _i32, _f32, _i32, _i32, _i64, _i64, _i32, _p],

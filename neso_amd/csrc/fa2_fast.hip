@@ -546,19 +546,21 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   }
 }
 
+// Launches with K key groups if their LDS fits (returns false otherwise).
 template <int D, bool CAUSAL, bool OUT_F16, int K>
-bool launch_fast_k(const Fa2Args& a, hipStream_t stream) {
+bool launch_fast_k(const Fa2Args& a, hipStream_t stream, hipError_t& err) {
   if constexpr (K * fast_group_lds_halves<D>() * 2 <= 160 * 1024) {
     if constexpr (CAUSAL) {
       if (a.pair_qblocks) {
-        hipLaunchKernelGGL((fa2_fast_kernel<D, true, OUT_F16, K, true>),
-                           dim3((a.num_qblocks + 1) / 2 * a.batch_heads), dim3(K * kGroup), 0,
-                           stream, a);
+        err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, true>>(
+            ktag("fa2_fast_kernel", D, true, OUT_F16, K, true),
+            dim3((a.num_qblocks + 1) / 2 * a.batch_heads), dim3(K * kGroup), stream, a);
         return true;
       }
     }
-    hipLaunchKernelGGL((fa2_fast_kernel<D, CAUSAL, OUT_F16, K>),
-                       dim3(a.num_qblocks * a.batch_heads), dim3(K * kGroup), 0, stream, a);
+    err = launch<&fa2_fast_kernel<D, CAUSAL, OUT_F16, K>>(
+        ktag("fa2_fast_kernel", D, CAUSAL, OUT_F16, K, false),
+        dim3(a.num_qblocks * a.batch_heads), dim3(K * kGroup), stream, a);
     return true;
   }
   return false;
@@ -566,11 +568,12 @@ bool launch_fast_k(const Fa2Args& a, hipStream_t stream) {
 
 template <int D, bool CAUSAL, bool OUT_F16>
 hipError_t launch_fast_t(const Fa2Args& a, int ksplit, hipStream_t stream) {
+  hipError_t err = hipSuccess;
   bool done = false;
-  if (ksplit >= 3) done = launch_fast_k<D, CAUSAL, OUT_F16, 3>(a, stream);
-  if (!done && ksplit >= 2) done = launch_fast_k<D, CAUSAL, OUT_F16, 2>(a, stream);
-  if (!done) launch_fast_k<D, CAUSAL, OUT_F16, 1>(a, stream);
-  return hipGetLastError();
+  if (ksplit >= 3) done = launch_fast_k<D, CAUSAL, OUT_F16, 3>(a, stream, err);
+  if (!done && ksplit >= 2) done = launch_fast_k<D, CAUSAL, OUT_F16, 2>(a, stream, err);
+  if (!done) launch_fast_k<D, CAUSAL, OUT_F16, 1>(a, stream, err);
+  return err;
 }
 
 template <bool OUT_F16>

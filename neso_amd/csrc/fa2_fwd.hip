@@ -499,12 +499,14 @@ constexpr int fa2_lds_bytes(int K) {
   return K * 2 * (slot + bias);
 }
 
+// Launches with K key groups if their LDS fits (returns false otherwise).
 template <int D, bool CAUSAL, int BIAS, bool OUT_F16, int K, bool F32IN, int QW>
-bool launch_fa2_k(Fa2Args a, hipStream_t stream) {
+bool launch_fa2_k(Fa2Args a, hipStream_t stream, hipError_t& err) {
   if constexpr (fa2_lds_bytes<D, BIAS, F32IN, QW>(K) <= 160 * 1024) {
     a.num_qblocks = (a.N + 32 * QW - 1) / (32 * QW);
-    hipLaunchKernelGGL((fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, K, F32IN, QW>),
-                       dim3(a.num_qblocks * a.batch_heads), dim3(K * 64 * QW), 0, stream, a);
+    err = launch<&fa2_fwd_kernel<D, CAUSAL, BIAS, OUT_F16, K, F32IN, QW>>(
+        ktag("fa2_fwd_kernel", D, CAUSAL, BIAS, OUT_F16, K, F32IN, QW),
+        dim3(a.num_qblocks * a.batch_heads), dim3(K * 64 * QW), stream, a);
     return true;
   }
   return false;
@@ -513,12 +515,15 @@ bool launch_fa2_k(Fa2Args a, hipStream_t stream) {
 template <int D, bool CAUSAL, int BIAS, bool OUT_F16, bool F32IN, int QW>
 hipError_t launch_fa2_q(const Fa2Args& a, int ksplit, hipStream_t stream) {
   // Use the requested key split, or the largest smaller one whose LDS fits.
+  hipError_t err = hipSuccess;
   bool done = false;
-  if (ksplit >= 4) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 4, F32IN, QW>(a, stream);
-  if (!done && ksplit >= 3) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 3, F32IN, QW>(a, stream);
-  if (!done && ksplit >= 2) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 2, F32IN, QW>(a, stream);
-  if (!done) launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 1, F32IN, QW>(a, stream);
-  return hipGetLastError();
+  if (ksplit >= 4) done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 4, F32IN, QW>(a, stream, err);
+  if (!done && ksplit >= 3)
+    done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 3, F32IN, QW>(a, stream, err);
+  if (!done && ksplit >= 2)
+    done = launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 2, F32IN, QW>(a, stream, err);
+  if (!done) launch_fa2_k<D, CAUSAL, BIAS, OUT_F16, 1, F32IN, QW>(a, stream, err);
+  return err;
 }
 
 // Query waves per key group: 4 (128-query workgroups), or 2 (64-query

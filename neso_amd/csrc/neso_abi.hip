@@ -9,8 +9,10 @@
 
 #include <algorithm>
 #include <atomic>
+#include <string>
 
 #include "../../include/neso_amd.h"
+#include "manifest.h"
 #include "neso_internal.h"
 
 namespace {
@@ -79,142 +81,6 @@ int check_head_dim(int32_t d) {
   if (d == 32 || d == 64 || d == 128) return NESO_OK;
   return fail(NESO_EUNSUPPORTED, "head_dim %d not supported (32, 64, 128)", d);
 }
-
-const char kManifest[] = R"JSON({
-  "library": "neso_amd",
-  "abi_version": 1,
-  "target": "gfx950",
-  "kernels": [
-    {"name": "neso_flash_attention_fwd", "replaces": "flash_attention_fwd (tests/test_flash_attention.py:149-153)",
-     "params": [
-      {"index": 0, "name": "Q", "type": "const fp16*", "is_pointer": true},
-      {"index": 1, "name": "K", "type": "const fp16*", "is_pointer": true},
-      {"index": 2, "name": "V", "type": "const fp16*", "is_pointer": true},
-      {"index": 3, "name": "O", "type": "fp32*", "is_pointer": true},
-      {"index": 4, "name": "N", "type": "int32", "is_pointer": false},
-      {"index": 5, "name": "stride_qo", "type": "int32", "is_pointer": false},
-      {"index": 6, "name": "stride_kv", "type": "int32", "is_pointer": false},
-      {"index": 7, "name": "scale", "type": "fp32", "is_pointer": false},
-      {"index": 8, "name": "head_dim", "type": "int32", "is_pointer": false},
-      {"index": 9, "name": "batch_heads", "type": "int32", "is_pointer": false},
-      {"index": 10, "name": "stride_bh_qo", "type": "int64", "is_pointer": false},
-      {"index": 11, "name": "stride_bh_kv", "type": "int64", "is_pointer": false},
-      {"index": 12, "name": "causal", "type": "int32", "is_pointer": false},
-      {"index": 13, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
-     "threadgroup_size": 256, "block_m": 128, "block_n": 64, "head_dims": [32, 64, 128],
-     "grid": ["cdiv(N, 128) * batch_heads", "1", "1"]},
-    {"name": "neso_flash_attention_f32_fwd", "replaces": "flash_attention_fwd with qkv_dtype='f32' (tests/test_flash_attention.py:79-89,250-290)",
-     "params": [
-      {"index": 0, "name": "Q", "type": "const fp32*", "is_pointer": true},
-      {"index": 1, "name": "K", "type": "const fp32*", "is_pointer": true},
-      {"index": 2, "name": "V", "type": "const fp32*", "is_pointer": true},
-      {"index": 3, "name": "O", "type": "fp32*", "is_pointer": true},
-      {"index": 4, "name": "N", "type": "int32", "is_pointer": false},
-      {"index": 5, "name": "stride_qo", "type": "int32", "is_pointer": false},
-      {"index": 6, "name": "stride_kv", "type": "int32", "is_pointer": false},
-      {"index": 7, "name": "scale", "type": "fp32", "is_pointer": false},
-      {"index": 8, "name": "head_dim", "type": "int32", "is_pointer": false},
-      {"index": 9, "name": "batch_heads", "type": "int32", "is_pointer": false},
-      {"index": 10, "name": "stride_bh_qo", "type": "int64", "is_pointer": false},
-      {"index": 11, "name": "stride_bh_kv", "type": "int64", "is_pointer": false},
-      {"index": 12, "name": "causal", "type": "int32", "is_pointer": false},
-      {"index": 13, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
-     "threadgroup_size": 256, "block_m": 128, "head_dims": [32, 64],
-     "precision": "f32 inputs split into f16 hi + lo, three f16 MFMAs per product, f32 accumulation",
-     "grid": ["cdiv(N, 128) * batch_heads", "1", "1"]},
-    {"name": "neso_flash_attention_io_fwd", "replaces": "flash_attention_fwd(Q, K, V, O, N, d_head, scale) (bench/bench_flash_attention.py:142-152)",
-     "params": [
-      {"index": 0, "name": "Q", "type": "const fp16*|const fp32*", "is_pointer": true},
-      {"index": 1, "name": "K", "type": "const fp16*|const fp32*", "is_pointer": true},
-      {"index": 2, "name": "V", "type": "const fp16*|const fp32*", "is_pointer": true},
-      {"index": 3, "name": "O", "type": "fp16*|fp32*", "is_pointer": true},
-      {"index": 4, "name": "N", "type": "int32", "is_pointer": false},
-      {"index": 5, "name": "d_head", "type": "int32", "is_pointer": false},
-      {"index": 6, "name": "scale", "type": "fp32", "is_pointer": false},
-      {"index": 7, "name": "io_dtype", "type": "int32", "is_pointer": false},
-      {"index": 8, "name": "batch_heads", "type": "int32", "is_pointer": false},
-      {"index": 9, "name": "stream", "type": "hipStream_t", "is_pointer": true}]},
-    {"name": "neso_flash_attention_window_fwd", "replaces": "flash_attention_fwd with window_left/right (debug/fa2_correctness_legacy.py:92-102)",
-     "params": [
-      {"index": 0, "name": "Q", "type": "const fp16*", "is_pointer": true},
-      {"index": 1, "name": "K", "type": "const fp16*", "is_pointer": true},
-      {"index": 2, "name": "V", "type": "const fp16*", "is_pointer": true},
-      {"index": 3, "name": "O", "type": "fp16*|fp32*", "is_pointer": true},
-      {"index": 4, "name": "seq_len", "type": "int32", "is_pointer": false},
-      {"index": 5, "name": "stride_h", "type": "int32", "is_pointer": false},
-      {"index": 6, "name": "stride_m", "type": "int32", "is_pointer": false},
-      {"index": 7, "name": "sm_scale", "type": "fp32", "is_pointer": false},
-      {"index": 8, "name": "window_left", "type": "int32", "is_pointer": false},
-      {"index": 9, "name": "window_right", "type": "int32", "is_pointer": false},
-      {"index": 10, "name": "num_heads", "type": "int32", "is_pointer": false},
-      {"index": 11, "name": "head_dim", "type": "int32", "is_pointer": false},
-      {"index": 12, "name": "out_dtype", "type": "int32", "is_pointer": false},
-      {"index": 13, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
-     "threadgroup_size": 256, "block_m": 128, "block_n": 64,
-     "grid": ["cdiv(seq_len, 128) * num_heads", "1", "1"]},
-    {"name": "neso_rel_pos_fa2_fwd", "replaces": "rel_pos_fa2_fwd (tests/test_rel_pos_fa2.py:157-163)",
-     "params": [
-      {"index": 0, "name": "Q", "type": "const fp16*", "is_pointer": true},
-      {"index": 1, "name": "K", "type": "const fp16*", "is_pointer": true},
-      {"index": 2, "name": "V", "type": "const fp16*", "is_pointer": true},
-      {"index": 3, "name": "bias", "type": "const fp16*|const fp32*", "is_pointer": true},
-      {"index": 4, "name": "O", "type": "fp16*|fp32*", "is_pointer": true},
-      {"index": 5, "name": "T", "type": "int32", "is_pointer": false},
-      {"index": 6, "name": "stride", "type": "int32", "is_pointer": false},
-      {"index": 7, "name": "scale", "type": "fp32", "is_pointer": false},
-      {"index": 8, "name": "stride_h", "type": "int32", "is_pointer": false},
-      {"index": 9, "name": "bias_stride_h", "type": "int32", "is_pointer": false},
-      {"index": 10, "name": "num_heads", "type": "int32", "is_pointer": false},
-      {"index": 11, "name": "head_dim", "type": "int32", "is_pointer": false},
-      {"index": 12, "name": "bias_mode", "type": "int32", "is_pointer": false},
-      {"index": 13, "name": "out_dtype", "type": "int32", "is_pointer": false},
-      {"index": 14, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
-     "threadgroup_size": 256, "block_m": 128, "block_n": 64,
-     "grid": ["cdiv(T, 128) * num_heads", "1", "1"]},
-    {"name": "neso_w4a16_matmul", "replaces": null,
-     "params": [
-      {"index": 0, "name": "X", "type": "const fp16*", "is_pointer": true},
-      {"index": 1, "name": "W", "type": "const int32*", "is_pointer": true},
-      {"index": 2, "name": "scales", "type": "const fp16*", "is_pointer": true},
-      {"index": 3, "name": "Y", "type": "fp16*", "is_pointer": true},
-      {"index": 4, "name": "M", "type": "int32", "is_pointer": false},
-      {"index": 5, "name": "N", "type": "int32", "is_pointer": false},
-      {"index": 6, "name": "K", "type": "int32", "is_pointer": false},
-      {"index": 7, "name": "stride_xm", "type": "int32", "is_pointer": false},
-      {"index": 8, "name": "stride_ym", "type": "int32", "is_pointer": false},
-      {"index": 9, "name": "group_size", "type": "int32", "is_pointer": false},
-      {"index": 10, "name": "zero_point", "type": "int32", "is_pointer": false},
-      {"index": 11, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
-     "threadgroup_size": 256},
-    {"name": "neso_w8a16_matmul", "replaces": "w8a16_matmul (tests/test_quantized_matmul.py:77-80)",
-     "params": [
-      {"index": 0, "name": "A", "type": "const fp16*", "is_pointer": true},
-      {"index": 1, "name": "B", "type": "const int8*", "is_pointer": true},
-      {"index": 2, "name": "C", "type": "fp32*", "is_pointer": true},
-      {"index": 3, "name": "K", "type": "int32", "is_pointer": false},
-      {"index": 4, "name": "stride_am", "type": "int32", "is_pointer": false},
-      {"index": 5, "name": "stride_bk", "type": "int32", "is_pointer": false},
-      {"index": 6, "name": "stride_cm", "type": "int32", "is_pointer": false},
-      {"index": 7, "name": "M", "type": "int32", "is_pointer": false},
-      {"index": 8, "name": "N", "type": "int32", "is_pointer": false},
-      {"index": 9, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
-     "threadgroup_size": 256},
-    {"name": "neso_w8a16_scaled_matmul", "replaces": "w8a16_scaled_matmul (tests/test_quantized_matmul.py:189-192)",
-     "params": [
-      {"index": 0, "name": "A", "type": "const fp16*", "is_pointer": true},
-      {"index": 1, "name": "B", "type": "const int8*", "is_pointer": true},
-      {"index": 2, "name": "C", "type": "fp32*", "is_pointer": true},
-      {"index": 3, "name": "scale", "type": "const fp16*", "is_pointer": true},
-      {"index": 4, "name": "K", "type": "int32", "is_pointer": false},
-      {"index": 5, "name": "stride_am", "type": "int32", "is_pointer": false},
-      {"index": 6, "name": "stride_bk", "type": "int32", "is_pointer": false},
-      {"index": 7, "name": "stride_cm", "type": "int32", "is_pointer": false},
-      {"index": 8, "name": "M", "type": "int32", "is_pointer": false},
-      {"index": 9, "name": "N", "type": "int32", "is_pointer": false},
-      {"index": 10, "name": "stream", "type": "hipStream_t", "is_pointer": true}],
-     "threadgroup_size": 256}
-  ]
-})JSON";
 
 // Shared by both attention entry points once their layouts are resolved.
 int fa2_common(const void* Q, const void* K, const void* V, void* O, const void* bias, int32_t N,
@@ -285,11 +151,36 @@ int fa2_common(const void* Q, const void* K, const void* V, void* O, const void*
                   name);
 }
 
+// Launch-plan recording state of the calling thread.
+struct PlanState {
+  bool active = false;
+  int cus = 0;  // compute units planned for; 0 = the current device's
+  int count = 0;
+  std::string json;
+};
+thread_local PlanState g_plan;
+
 }  // namespace
 
 namespace neso {
 
+bool plan_recording() { return g_plan.active; }
+
+void plan_add(const KernelTag& tag, dim3 grid, dim3 block) {
+  std::string targs;
+  for (int i = 0; i < tag.nargs; ++i) targs += (i ? ", " : "") + std::to_string(tag.args[i]);
+  char buf[320];
+  snprintf(buf, sizeof buf,
+           "%s{\"device_kernel\": \"%s\", \"template_args\": [%s], \"grid\": [%u, %u, %u], "
+           "\"threadgroup_size\": %u, \"num_warps\": %u}",
+           g_plan.count ? ", " : "", tag.name, targs.c_str(), grid.x, grid.y, grid.z,
+           block.x * block.y * block.z, block.x * block.y * block.z / 64);
+  g_plan.json += buf;
+  ++g_plan.count;
+}
+
 int device_cu_count() {
+  if (g_plan.active && g_plan.cus > 0) return g_plan.cus;
   constexpr int kMaxDevices = 64;
   static std::atomic<int> cache[kMaxDevices];
   int dev = 0;
@@ -310,7 +201,7 @@ int device_cu_count() {
 
 extern "C" {
 
-int neso_abi_version(void) { return 1; }
+int neso_abi_version(void) { return 2; }
 
 const char* neso_status_string(int status) {
   switch (status) {
@@ -324,7 +215,23 @@ const char* neso_status_string(int status) {
 
 const char* neso_last_error(void) { return g_last_error; }
 
-const char* neso_kernel_manifest(void) { return kManifest; }
+const char* neso_kernel_manifest(void) { return neso::kManifest; }
+
+int neso_plan_begin(int32_t cu_count) {
+  if (cu_count < 0) return fail(NESO_EINVAL, "plan_begin: cu_count=%d < 0", cu_count);
+  g_plan.active = true;
+  g_plan.cus = cu_count;
+  g_plan.count = 0;
+  g_plan.json.clear();
+  return ok();
+}
+
+const char* neso_plan_end(void) {
+  static thread_local std::string out;
+  out = "{\"launches\": [" + g_plan.json + "]}";
+  g_plan = PlanState{};
+  return out.c_str();
+}
 
 int neso_flash_attention_fwd(const void* Q, const void* K, const void* V, float* O, int32_t N,
                              int32_t stride_qo, int32_t stride_kv, float scale, int32_t head_dim,

@@ -46,8 +46,40 @@ struct Fa2Args {
   int32_t pair_qblocks;
 };
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device), or the count a
+// launch-plan recording stands in for.
 int device_cu_count();
+
+// ---- launches ----
+// Every kernel of the library is launched through launch<&kernel>(...).
+// While a launch plan is being recorded on the calling thread
+// (neso_plan_begin / neso_plan_end in the C ABI), the launch is recorded
+// instead of issued and no HIP call is made, so the host-side choice of
+// kernel, grid and workgroup size can be inspected without a GPU.
+bool plan_recording();
+
+// Name and template arguments of a launched kernel, for the plan record.
+struct KernelTag {
+  const char* name;
+  int args[8];
+  int nargs;
+};
+template <typename... T>
+KernelTag ktag(const char* name, T... v) {
+  static_assert(sizeof...(T) <= 8, "template arguments");
+  return KernelTag{name, {static_cast<int>(v)...}, (int)sizeof...(T)};
+}
+void plan_add(const KernelTag& tag, dim3 grid, dim3 block);
+
+template <auto F, typename... A>
+hipError_t launch(const KernelTag& tag, dim3 grid, dim3 block, hipStream_t stream, A... args) {
+  if (plan_recording()) {
+    plan_add(tag, grid, block);
+    return hipSuccess;
+  }
+  void* argv[] = {static_cast<void*>(&args)...};
+  return hipLaunchKernel(reinterpret_cast<const void*>(F), grid, block, argv, 0, stream);
+}
 
 int fa2_query_block();
 // The fast kernel covers fp16 Q/K/V without a bias at head_dim 64, and is

@@ -993,18 +993,19 @@ hipError_t launch_gemv_r(const W4Args& a, hipStream_t s) {
   const int cus = device_cu_count();
   if (blocks > cus) blocks = (blocks + cus - 1) / cus * cus;
   const int G = a.K / 32;
-  if (G <= 64) {
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 1, R, false>), dim3(blocks), dim3(kThreads), 0, s, a);
-  } else if (G <= 128 && a.group == 32 && G % 2 == 0) {  // whole 4-byte scale pairs
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 2, R, true>), dim3(blocks), dim3(kThreads), 0, s, a);
-  } else if (G <= 128) {
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 2, R, false>), dim3(blocks), dim3(kThreads), 0, s, a);
-  } else if (G <= 256) {
-    hipLaunchKernelGGL((w4a16_gemv_kernel<MR, 4, R, false>), dim3(blocks), dim3(kThreads), 0, s, a);
-  } else {
-    return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
+  if (G <= 64)
+    return launch<&w4a16_gemv_kernel<MR, 1, R, false>>(
+        ktag("w4a16_gemv_kernel", MR, 1, R, false), dim3(blocks), dim3(kThreads), s, a);
+  if (G <= 128 && a.group == 32 && G % 2 == 0)  // whole 4-byte scale pairs
+    return launch<&w4a16_gemv_kernel<MR, 2, R, true>>(
+        ktag("w4a16_gemv_kernel", MR, 2, R, true), dim3(blocks), dim3(kThreads), s, a);
+  if (G <= 128)
+    return launch<&w4a16_gemv_kernel<MR, 2, R, false>>(
+        ktag("w4a16_gemv_kernel", MR, 2, R, false), dim3(blocks), dim3(kThreads), s, a);
+  if (G <= 256)
+    return launch<&w4a16_gemv_kernel<MR, 4, R, false>>(
+        ktag("w4a16_gemv_kernel", MR, 4, R, false), dim3(blocks), dim3(kThreads), s, a);
+  return hipErrorInvalidValue;
 }
 
 template <int MR>
@@ -1065,24 +1066,19 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
     // One 8-byte load fetches the scales of a chunk quad when every chunk
     // has its own scale and rows hold whole quads (8-byte aligned).
     const bool g32 = a.group == 32 && a.K % 128 == 0;
+    const dim3 block(kSkinnyWaves * kWave);
     if (a.M <= 16) {
       const dim3 grid((a.N + 31) / 32, 1);
-      if (g32)
-        hipLaunchKernelGGL((w4a16_skinny_kernel<1, 2, kSkinnyWaves, true>), grid,
-                           dim3(kSkinnyWaves * kWave), 0, s, a);
-      else
-        hipLaunchKernelGGL((w4a16_skinny_kernel<1, 2, kSkinnyWaves, false>), grid,
-                           dim3(kSkinnyWaves * kWave), 0, s, a);
-    } else {
-      const dim3 grid((a.N + 31) / 32, (a.M + 31) / 32);
-      if (g32)
-        hipLaunchKernelGGL((w4a16_skinny_kernel<2, 2, kSkinnyWaves, true>), grid,
-                           dim3(kSkinnyWaves * kWave), 0, s, a);
-      else
-        hipLaunchKernelGGL((w4a16_skinny_kernel<2, 2, kSkinnyWaves, false>), grid,
-                           dim3(kSkinnyWaves * kWave), 0, s, a);
+      return g32 ? launch<&w4a16_skinny_kernel<1, 2, kSkinnyWaves, true>>(
+          ktag("w4a16_skinny_kernel", 1, 2, kSkinnyWaves, true), grid, block, s, a)
+                 : launch<&w4a16_skinny_kernel<1, 2, kSkinnyWaves, false>>(
+                     ktag("w4a16_skinny_kernel", 1, 2, kSkinnyWaves, false), grid, block, s, a);
     }
-    return hipGetLastError();
+    const dim3 grid((a.N + 31) / 32, (a.M + 31) / 32);
+    return g32 ? launch<&w4a16_skinny_kernel<2, 2, kSkinnyWaves, true>>(
+        ktag("w4a16_skinny_kernel", 2, 2, kSkinnyWaves, true), grid, block, s, a)
+               : launch<&w4a16_skinny_kernel<2, 2, kSkinnyWaves, false>>(
+                   ktag("w4a16_skinny_kernel", 2, 2, kSkinnyWaves, false), grid, block, s, a);
   }
 #ifndef NESO_GEMM_WN
 #define NESO_GEMM_WN 2
@@ -1106,23 +1102,21 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
                       : a.M < 192    ? 0
                                      : (tiles <= device_cu_count() ? 2 : 1);
   if (kgroups && tile_fits) {
-    if (kgroups == 2)
-      hipLaunchKernelGGL(w4a16_tile_gemm_kernel<2>, dim3(tiles), dim3(512), 0, s, a);
-    else
-      hipLaunchKernelGGL(w4a16_tile_gemm_kernel<1>, dim3(tiles), dim3(256), 0, s, a);
-    return hipGetLastError();
+    return kgroups == 2 ? launch<&w4a16_tile_gemm_kernel<2>>(
+        ktag("w4a16_tile_gemm_kernel", 2), dim3(tiles), dim3(512), s, a)
+                        : launch<&w4a16_tile_gemm_kernel<1>>(
+                            ktag("w4a16_tile_gemm_kernel", 1), dim3(tiles), dim3(256), s, a);
   }
   constexpr int WM = 2, WN = NESO_GEMM_WN, BN = NESO_GEMM_BN;
   if ((int64_t)kGBM * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
       (int64_t)BN * a.K / 2 < ((int64_t)1 << 31)) {
     const int tiles = ((a.M + kGBM - 1) / kGBM) * ((a.N + BN - 1) / BN);
-    hipLaunchKernelGGL((w4a16_gemm_kernel<WM, WN, BN>), dim3(tiles), dim3(WM * WN * kWave), 0, s, a);
-    return hipGetLastError();
+    return launch<&w4a16_gemm_kernel<WM, WN, BN>>(
+        ktag("w4a16_gemm_kernel", WM, WN, BN), dim3(tiles), dim3(WM * WN * kWave), s, a);
   }
   constexpr int TN = 2;
   const dim3 grid((a.N + 4 * 32 * TN - 1) / (4 * 32 * TN), (a.M + 31) / 32);
-  hipLaunchKernelGGL((w4a16_mfma_kernel<TN>), grid, dim3(kThreads), 0, s, a);
-  return hipGetLastError();
+  return launch<&w4a16_mfma_kernel<TN>>(ktag("w4a16_mfma_kernel", TN), grid, dim3(kThreads), s, a);
 }
 
 hipError_t launch_w8a16(const W8Args& a, hipStream_t s) {
@@ -1136,12 +1130,10 @@ hipError_t launch_w8a16(const W8Args& a, hipStream_t s) {
                      (int64_t)a.K * a.ldb < ((int64_t)1 << 31);
   if (tiled) {
     const dim3 grid((a.N + kW8BN - 1) / kW8BN, (a.M + kW8BM - 1) / kW8BM);
-    hipLaunchKernelGGL(w8a16_gemm_kernel, grid, dim3(kThreads), 0, s, a);
-    return hipGetLastError();
+    return launch<&w8a16_gemm_kernel>(ktag("w8a16_gemm_kernel"), grid, dim3(kThreads), s, a);
   }
   const dim3 grid((a.N + 127) / 128, (a.M + 31) / 32);
-  hipLaunchKernelGGL(w8a16_kernel, grid, dim3(kThreads), 0, s, a);
-  return hipGetLastError();
+  return launch<&w8a16_kernel>(ktag("w8a16_kernel"), grid, dim3(kThreads), s, a);
 }
 
 }  // namespace neso

@@ -169,13 +169,17 @@ hipError_t launch_w4a16_skinny_lds(const W4Args& a, hipStream_t s) {
   if (T > 4) T = 4;
   const dim3 grid((ntiles + T - 1) / T);
   constexpr int WV = 8, QWMAX = (kLdsQuads + WV - 1) / WV;
+  const dim3 block(WV * kWave);
   switch (T) {
-    case 1: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 1, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
-    case 2: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 2, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
-    case 3: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 3, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
-    default: hipLaunchKernelGGL((w4a16_skinny_lds_kernel<WV, 4, QWMAX>), grid, dim3(WV * kWave), 0, s, a); break;
+    case 1: return launch<&w4a16_skinny_lds_kernel<WV, 1, QWMAX>>(
+        ktag("w4a16_skinny_lds_kernel", WV, 1, QWMAX), grid, block, s, a);
+    case 2: return launch<&w4a16_skinny_lds_kernel<WV, 2, QWMAX>>(
+        ktag("w4a16_skinny_lds_kernel", WV, 2, QWMAX), grid, block, s, a);
+    case 3: return launch<&w4a16_skinny_lds_kernel<WV, 3, QWMAX>>(
+        ktag("w4a16_skinny_lds_kernel", WV, 3, QWMAX), grid, block, s, a);
+    default: return launch<&w4a16_skinny_lds_kernel<WV, 4, QWMAX>>(
+        ktag("w4a16_skinny_lds_kernel", WV, 4, QWMAX), grid, block, s, a);
   }
-  return hipGetLastError();
 }
 
 }  // namespace neso

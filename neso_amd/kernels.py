@@ -32,6 +32,8 @@ __all__ = [
     "w8a16_matmul",
     "w8a16_scaled_matmul",
     "launch",
+    "launch_plan",
+    "manifest",
     "KERNELS",
     "attention",
     "rel_pos_attention",
@@ -283,6 +285,31 @@ KERNELS = {
     "w8a16_matmul": w8a16_matmul,
     "w8a16_scaled_matmul": w8a16_scaled_matmul,
 }
+
+
+def manifest() -> dict:
+    """The library's kernel manifest (``neso_kernel_manifest``) as a dict: per
+    entry point the reference's AOT fields (src/neso/aot_compile.py:108-117)
+    and per device-kernel variant its launch geometry."""
+    import json
+    return json.loads(_lib.load().neso_kernel_manifest().decode())
+
+
+def launch_plan(name: str, *args, cu_count: int = 0, **kwargs) -> list[dict]:
+    """The kernel launches that ``launch(name, *args, **kwargs)`` would issue,
+    recorded instead of issued (``neso_plan_begin`` / ``neso_plan_end``): each
+    a dict with the device kernel, its template arguments, grid,
+    threadgroup size and warp count.  Needs no GPU; ``cu_count`` stands in
+    for the device's compute units (0: the current device's).  Tensors must
+    still be given on the GPU or as raw device addresses."""
+    import json
+    lib = _lib.load()
+    _lib.check(lib.neso_plan_begin(int(cu_count)))
+    try:
+        launch(name, *args, **kwargs)
+    finally:
+        plan = json.loads(lib.neso_plan_end().decode())
+    return plan["launches"]
 
 
 def launch(name: str, *args, **kwargs) -> None:

@@ -59,14 +59,117 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_manifest_matches_header(lib):
     man = json.loads(lib.neso_kernel_manifest().decode())
-    assert man["abi_version"] == lib.neso_abi_version() == 1
+    assert man["abi_version"] == lib.neso_abi_version() == 2
     funcs = header_functions()
     for k in man["kernels"]:
-        assert k["name"] in funcs
-        assert len(k["params"]) == funcs[k["name"]], k["name"]
+        # The reference's AOT metadata fields (src/neso/aot_compile.py:108-117).
+        assert {"kernel_name", "params", "constants", "threadgroup_size", "num_warps",
+                "grid"} <= set(k), k.get("kernel_name")
+        assert k["kernel_name"] in funcs
+        assert len(k["params"]) == funcs[k["kernel_name"]], k["kernel_name"]
         assert [p["index"] for p in k["params"]] == list(range(len(k["params"])))
-    kernels = {k["name"] for k in man["kernels"]}
+        for v in k["variants"]:
+            assert {"device_kernel", "template_params", "threadgroup_size", "num_warps",
+                    "grid", "constants"} <= set(v)
+            assert len(v["grid"]) == 3
+    kernels = {k["kernel_name"] for k in man["kernels"]}
     assert kernels == {n for n in funcs if n.endswith(("_fwd", "_matmul"))}
+
+
+def _cdiv(a, b):
+    return -(-a // b)
+
+
+def _eval(expr, env):
+    """A manifest geometry expression (Python syntax, the manifest's own text)."""
+    return eval(expr, {"__builtins__": {}}, {**env, "cdiv": _cdiv})
+
+
+def _plan(lib, fn, args, cus):
+    assert lib.neso_plan_begin(cus) == _lib.NESO_OK
+    try:
+        status = fn(*args)
+    finally:
+        plan = json.loads(lib.neso_plan_end().decode())
+    return status, plan["launches"]
+
+
+_P = A16
+PLAN_CASES = [
+    # (entry point, positional args, size variables)
+    ("neso_flash_attention_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 16, 2048 * 64, 2048 * 64, 0],
+     dict(N=2048, batch_heads=16)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [128, 64, 64, 0.125, 64, 8, 128 * 64, 128 * 64, 0],
+     dict(N=128, batch_heads=8)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [1024, 64, 64, 0.125, 64, 16, 1024 * 64, 1024 * 64, 1],
+     dict(N=1024, batch_heads=16)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [512, 64, 64, 0.125, 64, 16, 512 * 64, 512 * 64, 1],
+     dict(N=512, batch_heads=16)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [4096, 128, 128, 0.08, 128, 64, 4096 * 128, 4096 * 128, 1],
+     dict(N=4096, batch_heads=64)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 4, 2048 * 64, 2048 * 64, 1],
+     dict(N=2048, batch_heads=4)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [300, 32, 32, 0.17, 32, 3, 300 * 32, 300 * 32, 0],
+     dict(N=300, batch_heads=3)),
+    ("neso_flash_attention_f32_fwd", [_P] * 4 + [512, 128, 128, 0.08, 128, 2, 512 * 128, 512 * 128, 0],
+     dict(N=512, batch_heads=2)),
+    ("neso_flash_attention_f32_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 8, 2048 * 64, 2048 * 64, 1],
+     dict(N=2048, batch_heads=8)),
+    ("neso_flash_attention_io_fwd", [_P] * 4 + [1000, 128, 0.08, 0, 2], dict(N=1000, batch_heads=2)),
+    ("neso_flash_attention_io_fwd", [_P] * 4 + [256, 64, 0.125, 1, 1], dict(N=256, batch_heads=1)),
+    ("neso_flash_attention_window_fwd", [_P] * 4 + [400, 64, 192, 0.125, 5, 7, 3, 64, 1],
+     dict(N=400, batch_heads=3)),
+    ("neso_rel_pos_fa2_fwd", [_P] * 5 + [1500, 64, 0.125, 1500 * 64, 2999, 8, 64, 1, 1],
+     dict(N=1500, batch_heads=8)),
+    ("neso_rel_pos_fa2_fwd", [_P] * 5 + [64, 64, 0.125, 64 * 64, 64 * 64, 4, 64, 0, 0],
+     dict(N=64, batch_heads=4)),
+    ("neso_rel_pos_fa2_fwd", [_P] * 5 + [8192, 64, 0.125, 8192 * 64, 16383, 16, 64, 1, 1],
+     dict(N=8192, batch_heads=16)),
+    # X row stride 2^23: the tiled kernels' 32-bit buffer offsets would
+    # overflow, so the fallback kernel is chosen.
+    ("neso_w4a16_matmul", [_P] * 4 + [100, 11008, 4096, 1 << 23, 11008, 32, 8],
+     dict(M=100, N=11008, K=4096)),
+] + [
+    ("neso_w4a16_matmul", [_P] * 4 + [m, 11008, k, k, 11008, g, 8], dict(M=m, N=11008, K=k))
+    for m, k, g in ((1, 4096, 32), (2, 4096, 32), (1, 8192, 128), (3, 4096, 32), (16, 4096, 32),
+                    (16, 5120, 32), (48, 4096, 64), (128, 4096, 32), (256, 4096, 32),
+                    (1000, 4096, 32))
+] + [
+    ("neso_w8a16_matmul", [_P] * 3 + [4096, 4096, 4096, 4096, 4096, 4096],
+     dict(M=4096, N=4096, K=4096)),
+    ("neso_w8a16_scaled_matmul", [_P] * 4 + [100, 100, 100, 100, 64, 100],
+     dict(M=64, N=100, K=100)),
+]
+
+
+@pytest.mark.parametrize("cus", [256, 80])
+@pytest.mark.parametrize("case", range(len(PLAN_CASES)))
+def test_manifest_geometry_matches_launches(lib, case, cus):
+    """The launch each entry point chooses (recorded, not issued) is one of
+    its manifest variants, with the threadgroup size, warp count and grid
+    that the variant's formulas give for the call's sizes."""
+    name, args, sizes = PLAN_CASES[case]
+    man = {k["kernel_name"]: k for k in json.loads(lib.neso_kernel_manifest().decode())["kernels"]}
+    status, launches = _plan(lib, getattr(lib, name), args + [None], cus)
+    assert status == _lib.NESO_OK, lib.neso_last_error()
+    assert len(launches) == 1, launches
+    rec = launches[0]
+    entry = man[name]
+    variants = {v["device_kernel"]: v for v in entry["variants"]}
+    assert rec["device_kernel"] in variants, (name, rec)
+    v = variants[rec["device_kernel"]]
+    assert len(v["template_params"]) == len(rec["template_args"])
+    env = dict(zip(v["template_params"], rec["template_args"]), cus=cus, **sizes)
+    assert _eval(v["threadgroup_size"], env) == rec["threadgroup_size"]
+    assert _eval(v["num_warps"], env) == rec["num_warps"]
+    assert [_eval(g, env) for g in v["grid"]] == rec["grid"], (v["grid"], rec)
+
+
+def test_plan_records_nothing_on_rejected_calls(lib):
+    status, launches = _plan(lib, lib.neso_flash_attention_fwd,
+                             [A16] * 4 + [128, 64, 64, 0.125, 96, 1, 0, 0, 0, None], 256)
+    assert status == _lib.NESO_EUNSUPPORTED and launches == []
+    assert lib.neso_plan_begin(-1) == _lib.NESO_EINVAL
 
 
 def test_status_strings(lib):
@@ -283,3 +386,12 @@ def test_tensor_wrappers_validate_before_launch():
     with pytest.raises(ValueError, match="span"):
         neso_amd.rel_pos_fa2_fwd(q, q, q, torch.zeros(2, 16, 15, dtype=f16), q, 16, 64, 0.125,
                                  1024, 256, num_heads=2)
+
+
+def test_python_manifest_and_plan():
+    man = neso_amd.manifest()
+    assert {k["kernel_name"] for k in man["kernels"]} >= {"neso_flash_attention_fwd",
+                                                          "neso_w4a16_matmul"}
+    plan = neso_amd.launch_plan("w4a16_matmul", A16, A16, A16, A16, 1, 11008, 4096, 4096, 11008,
+                                cu_count=256)
+    assert [p["device_kernel"] for p in plan] == ["w4a16_gemv_kernel"]
