@@ -170,6 +170,24 @@ int neso_rel_pos_fa2_fwd(const void* Q, const void* K, const void* V, const void
                          int32_t bias_mode, int32_t out_dtype, void* stream);
 
 /*
+ * Relative-position bias precompute for the reference-signature kernel
+ * above.  Replaces the host-side `precompute_bias_and_qu(Q, K_rel, bias_u,
+ * bias_v, T, d, nh, scale)` of tests/test_rel_pos_fa2.py:286-311 (same
+ * leading arguments and order; `scale` is accepted and unused there too,
+ * the bias is returned unscaled).  Inputs fp32, contiguous:
+ *   Q [nh][T][d], K_rel [nh][2T-1][d], bias_u, bias_v [nh][d]
+ * Outputs fp16, contiguous, ready for neso_rel_pos_fa2_fwd with
+ * NESO_BIAS_DENSE_SCALED_F16:
+ *   Q_u [nh][T][d]      = Q + bias_u
+ *   rel_bias [nh][T][T] = (Q + bias_v)_i . K_rel[T-1-i+j]   (fp32 products
+ *                         and accumulation, rounded to fp16 once)
+ * d 32, 64 or 128; Q, K_rel, bias_v and Q_u 16-byte aligned.
+ */
+int neso_rel_pos_precompute(const float* Q, const float* K_rel, const float* bias_u,
+                            const float* bias_v, int32_t T, int32_t d, int32_t nh, float scale,
+                            void* Q_u, void* rel_bias, void* stream);
+
+/*
  * Weight-only int4 matmul, Y[M][N] fp16 = X[M][K] fp16 * dequant(W)^T.
  * No reference kernel packs int4 (the reference's W4A16 stores one int4
  * value per int8, tests/test_quantized_matmul.py:170-178); this is the

@@ -28,8 +28,10 @@ from .kernels import (  # noqa: F401
     launch,
     launch_plan,
     manifest,
+    precompute_bias_and_qu,
     rel_pos_attention,
     rel_pos_fa2_fwd,
+    rel_pos_precompute,
     w4a16_linear,
     w4a16_matmul,
     w8a16_matmul,

@@ -60,6 +60,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_p, _p, _p, _p, _p, _i32, _i32, _f32, _i32, _i32, _i32, _i32, _i32, _i32, _p],
     ),
+    "neso_rel_pos_precompute": (
+        ctypes.c_int,
+        [_p, _p, _p, _p, _i32, _i32, _i32, _f32, _p, _p, _p],
+    ),
     "neso_w4a16_matmul": (
         ctypes.c_int,
         [_p, _p, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32, _p],

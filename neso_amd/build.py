@@ -22,7 +22,8 @@ BUILD_DIR = PKG / "_build"
 LIB_PATH = PKG / "libneso_amd.so"
 ARCH = "gfx950"
 
-SOURCES = ["neso_abi.hip", "fa2_fwd.hip", "fa2_fast.hip", "qmatmul.hip", "qmatmul_skinny.hip"]
+SOURCES = ["neso_abi.hip", "fa2_fwd.hip", "fa2_fast.hip", "relpos_pre.hip", "qmatmul.hip",
+           "qmatmul_skinny.hip"]
 
 # Per-source options on top of COMMON_FLAGS.  The skinny int4 kernel runs
 # 3-4% faster without the scheduler's memory-operation clustering (M = 16:

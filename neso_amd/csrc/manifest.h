@@ -759,6 +759,117 @@ constexpr char kManifest[] = R"JSON({
    ]
   },
   {
+   "kernel_name": "neso_rel_pos_precompute",
+   "replaces": "precompute_bias_and_qu(Q, K_rel, bias_u, bias_v, T, d, nh, scale) (tests/test_rel_pos_fa2.py:286-311), host-side in the reference",
+   "params": [
+    {
+     "index": 0,
+     "name": "Q",
+     "type": "const fp32*",
+     "is_pointer": true
+    },
+    {
+     "index": 1,
+     "name": "K_rel",
+     "type": "const fp32*",
+     "is_pointer": true
+    },
+    {
+     "index": 2,
+     "name": "bias_u",
+     "type": "const fp32*",
+     "is_pointer": true
+    },
+    {
+     "index": 3,
+     "name": "bias_v",
+     "type": "const fp32*",
+     "is_pointer": true
+    },
+    {
+     "index": 4,
+     "name": "T",
+     "type": "int32",
+     "is_pointer": false
+    },
+    {
+     "index": 5,
+     "name": "d",
+     "type": "int32",
+     "is_pointer": false
+    },
+    {
+     "index": 6,
+     "name": "nh",
+     "type": "int32",
+     "is_pointer": false
+    },
+    {
+     "index": 7,
+     "name": "scale",
+     "type": "fp32",
+     "is_pointer": false
+    },
+    {
+     "index": 8,
+     "name": "Q_u",
+     "type": "fp16*",
+     "is_pointer": true
+    },
+    {
+     "index": 9,
+     "name": "rel_bias",
+     "type": "fp16*",
+     "is_pointer": true
+    },
+    {
+     "index": 10,
+     "name": "stream",
+     "type": "hipStream_t",
+     "is_pointer": true
+    }
+   ],
+   "constants": {
+    "wave_size": 64,
+    "head_dim": [
+     32,
+     64,
+     128
+    ],
+    "rel_bias": "unscaled, (Q + bias_v)_i . K_rel[T - 1 - i + j]"
+   },
+   "threadgroup_size": null,
+   "num_warps": null,
+   "grid": null,
+   "launch": "one variant per head_dim; geometry below",
+   "size_vars": {
+    "T": "T",
+    "nh": "nh"
+   },
+   "variants": [
+    {
+     "device_kernel": "relpos_precompute_kernel",
+     "source": "neso_amd/csrc/relpos_pre.hip",
+     "template_params": [
+      "D"
+     ],
+     "when": "always",
+     "threadgroup_size": "256",
+     "num_warps": "4",
+     "grid": [
+      "cdiv(T, 32)",
+      "nh",
+      "1"
+     ],
+     "constants": {
+      "block_m": "32",
+      "relative_positions_per_tile": "32",
+      "mfma": "v_mfma_f32_32x32x2f32"
+     }
+    }
+   ]
+  },
+  {
    "kernel_name": "neso_w4a16_matmul",
    "replaces": null,
    "params": [

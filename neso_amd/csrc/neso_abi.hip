@@ -299,6 +299,34 @@ int neso_rel_pos_fa2_fwd(const void* Q, const void* K, const void* V, const void
                     out_dtype == NESO_OUT_F16, stream, "rel_pos_fa2_fwd");
 }
 
+int neso_rel_pos_precompute(const float* Q, const float* K_rel, const float* bias_u,
+                            const float* bias_v, int32_t T, int32_t d, int32_t nh, float scale,
+                            void* Q_u, void* rel_bias, void* stream) {
+  const char* name = "rel_pos_precompute";
+  (void)scale;  // the reference's precompute leaves the bias unscaled too
+  if (!Q || !K_rel || !bias_u || !bias_v || !Q_u || !rel_bias)
+    return fail(NESO_EINVAL, "%s: null tensor pointer", name);
+  if (T < 0 || nh < 0) return fail(NESO_EINVAL, "%s: T=%d nh=%d", name, T, nh);
+  int st = check_head_dim(d);
+  if (st != NESO_OK) return st;
+  if (!aligned16(Q) || !aligned16(K_rel) || !aligned16(bias_v) || !aligned16(Q_u) ||
+      (reinterpret_cast<uintptr_t>(bias_u) & 3u) || !aligned2(rel_bias))
+    return fail(NESO_EINVAL, "%s: Q/K_rel/bias_v/Q_u must be 16-byte aligned", name);
+  if (T == 0 || nh == 0) return ok();
+  if ((int64_t)T * T > 0x7fffffff || (int64_t)(2 * T - 1) * d > 0x7fffffff)
+    return fail(NESO_EUNSUPPORTED, "%s: T=%d too large", name, T);
+  neso::RelPreArgs a{};
+  a.Q = Q;
+  a.K_rel = K_rel;
+  a.bias_u = bias_u;
+  a.bias_v = bias_v;
+  a.Q_u = static_cast<neso::half_t*>(Q_u);
+  a.rel_bias = static_cast<neso::half_t*>(rel_bias);
+  a.T = T;
+  a.heads = nh;
+  return launched(neso::launch_relpos_precompute(a, d, static_cast<hipStream_t>(stream)), name);
+}
+
 int neso_w4a16_matmul(const void* X, const int32_t* W, const void* scales, void* Y, int32_t M,
                       int32_t N, int32_t K, int32_t stride_xm, int32_t stride_ym,
                       int32_t group_size, int32_t zero_point, void* stream) {

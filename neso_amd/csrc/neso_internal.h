@@ -123,4 +123,21 @@ struct W8Args {
 
 hipError_t launch_w8a16(const W8Args& a, hipStream_t stream);
 
+// Rel-pos bias precompute: Q_u = Q + bias_u and the unscaled dense
+// rel_bias[h][i][j] = (Q + bias_v)[h][i] . K_rel[h][T-1-i+j], fp32 in, fp16
+// out, all contiguous ([heads][T][d], [heads][2T-1][d], [heads][d],
+// [heads][T][T]).
+struct RelPreArgs {
+  const float* Q;
+  const float* K_rel;
+  const float* bias_u;
+  const float* bias_v;
+  half_t* Q_u;
+  half_t* rel_bias;
+  int32_t T;
+  int32_t heads;
+};
+
+hipError_t launch_relpos_precompute(const RelPreArgs& a, int head_dim, hipStream_t stream);
+
 }  // namespace neso

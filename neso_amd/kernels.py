@@ -28,6 +28,8 @@ __all__ = [
     "flash_attention_io_fwd",
     "flash_attention_window_fwd",
     "rel_pos_fa2_fwd",
+    "rel_pos_precompute",
+    "precompute_bias_and_qu",
     "w4a16_matmul",
     "w8a16_matmul",
     "w8a16_scaled_matmul",
@@ -229,6 +231,33 @@ def rel_pos_fa2_fwd(Q, K, V, bias, O, T: int, stride: int, scale: float, stride_
     _lib.check(st)
 
 
+def rel_pos_precompute(Q, K_rel, bias_u, bias_v, T: int, d: int, nh: int, scale: float, Q_u,
+                       rel_bias, *, stream=None) -> None:
+    """Q_u = Q + bias_u and the unscaled dense rel_bias[h, i, j] = (Q + bias_v)_i .
+    K_rel[T - 1 - i + j] on the GPU.
+
+    Leading arguments as the reference's host precompute
+    ``precompute_bias_and_qu(Q, K_rel, bias_u, bias_v, T, d, nh, scale)``
+    (tests/test_rel_pos_fa2.py:286-311; ``scale`` unused, as there), then
+    the two outputs it returns: Q_u fp16 [nh, T, d] and rel_bias fp16
+    [nh, T, T], the inputs of :func:`rel_pos_fa2_fwd` in the dense mode.
+    Q, K_rel, bias_u, bias_v are contiguous fp32 [nh, T, d], [nh, 2T-1, d],
+    [nh, d], [nh, d].
+    """
+    if T > 0 and nh > 0:
+        for t, nm, n in ((Q, "Q", nh * T * d), (K_rel, "K_rel", nh * (2 * T - 1) * d),
+                         (bias_u, "bias_u", nh * d), (bias_v, "bias_v", nh * d),
+                         (Q_u, "Q_u", nh * T * d), (rel_bias, "rel_bias", nh * T * T)):
+            _extent(t, nm, n)
+    lib = _lib.load()
+    f32, f16 = torch.float32, torch.float16
+    st = lib.neso_rel_pos_precompute(
+        _ptr(Q, "Q", f32), _ptr(K_rel, "K_rel", f32), _ptr(bias_u, "bias_u", f32),
+        _ptr(bias_v, "bias_v", f32), int(T), int(d), int(nh), float(scale),
+        _ptr(Q_u, "Q_u", f16), _ptr(rel_bias, "rel_bias", f16), _stream(stream, Q, Q_u))
+    _lib.check(st)
+
+
 def w4a16_matmul(X, W, scales, Y, M: int, N: int, K: int, stride_xm: int, stride_ym: int,
                  group_size: int = 32, zero_point: int = 8, *, stream=None) -> None:
     """Y[M, N] fp16 = X[M, K] fp16 @ dequant(W)^T, W int32 [N, K/8] (int4, low nibble first)."""
@@ -281,6 +310,7 @@ KERNELS = {
     "flash_attention_io_fwd": flash_attention_io_fwd,
     "flash_attention_window_fwd": flash_attention_window_fwd,
     "rel_pos_fa2_fwd": rel_pos_fa2_fwd,
+    "rel_pos_precompute": rel_pos_precompute,
     "w4a16_matmul": w4a16_matmul,
     "w8a16_matmul": w8a16_matmul,
     "w8a16_scaled_matmul": w8a16_scaled_matmul,
@@ -371,6 +401,26 @@ def rel_pos_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, table: 
     rel_pos_fa2_fwd(q, k, v, table, out, n, d, scale, n * d, 2 * n - 1, num_heads=h, head_dim=d,
                     bias_mode=_lib.NESO_BIAS_TABLE_F32)
     return out
+
+
+def precompute_bias_and_qu(q: torch.Tensor, k_rel: torch.Tensor, bias_u: torch.Tensor,
+                           bias_v: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """GPU counterpart of the reference's ``precompute_bias_and_qu``
+    (tests/test_rel_pos_fa2.py:286-311) on fp32 tensors q [nh, T, d],
+    k_rel [nh, 2T-1, d], bias_u / bias_v [nh, d]; returns (Q_u fp16
+    [nh, T, d], rel_bias fp16 [nh, T, T]) for :func:`rel_pos_fa2_fwd`."""
+    _require(q.dim() == 3, f"q must be [nh, T, d], got {tuple(q.shape)}")
+    nh, t, d = (int(x) for x in q.shape)
+    _require(tuple(k_rel.shape) == (nh, 2 * t - 1, d),
+             f"k_rel must be [nh, 2T-1, d] = [{nh}, {2 * t - 1}, {d}], got {tuple(k_rel.shape)}")
+    for x, nm in ((bias_u, "bias_u"), (bias_v, "bias_v")):
+        _require(tuple(x.shape) == (nh, d), f"{nm} must be [nh, d] = [{nh}, {d}]")
+    for x, nm in ((q, "q"), (k_rel, "k_rel"), (bias_u, "bias_u"), (bias_v, "bias_v")):
+        _require(x.is_contiguous() and x.dtype == torch.float32, f"{nm} must be contiguous fp32")
+    q_u = torch.empty((nh, t, d), dtype=torch.float16, device=q.device)
+    rel_bias = torch.empty((nh, t, t), dtype=torch.float16, device=q.device)
+    rel_pos_precompute(q, k_rel, bias_u, bias_v, t, d, nh, 1.0 / math.sqrt(d), q_u, rel_bias)
+    return q_u, rel_bias
 
 
 def window_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, window_left: int,

@@ -73,7 +73,7 @@ def test_manifest_matches_header(lib):
                     "grid", "constants"} <= set(v)
             assert len(v["grid"]) == 3
     kernels = {k["kernel_name"] for k in man["kernels"]}
-    assert kernels == {n for n in funcs if n.endswith(("_fwd", "_matmul"))}
+    assert kernels == {n for n in funcs if n.endswith(("_fwd", "_matmul", "_precompute"))}
 
 
 def _cdiv(a, b):
@@ -125,6 +125,8 @@ PLAN_CASES = [
      dict(N=64, batch_heads=4)),
     ("neso_rel_pos_fa2_fwd", [_P] * 5 + [8192, 64, 0.125, 8192 * 64, 16383, 16, 64, 1, 1],
      dict(N=8192, batch_heads=16)),
+    ("neso_rel_pos_precompute", [_P] * 4 + [1500, 64, 8, 0.125, _P, _P], dict(T=1500, nh=8)),
+    ("neso_rel_pos_precompute", [_P] * 4 + [33, 128, 3, 0.1, _P, _P], dict(T=33, nh=3)),
     # X row stride 2^23: the tiled kernels' 32-bit buffer offsets would
     # overflow, so the fallback kernel is chosen.
     ("neso_w4a16_matmul", [_P] * 4 + [100, 11008, 4096, 1 << 23, 11008, 32, 8],
@@ -245,6 +247,27 @@ def fa2_io(lib, **kw):
 ])
 def test_fa2_io_validation(lib, kw, status):
     assert fa2_io(lib, **kw) == status
+
+
+def relpre(lib, **kw):
+    args = dict(Q=A16, K_rel=A16, bias_u=A16, bias_v=A16, T=0, d=64, nh=1, scale=0.125,
+                Q_u=A16, rel_bias=A16, stream=None)
+    args.update(kw)
+    return lib.neso_rel_pos_precompute(*args.values())
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(), _lib.NESO_OK),
+    (dict(Q=None), _lib.NESO_EINVAL),
+    (dict(rel_bias=None), _lib.NESO_EINVAL),
+    (dict(d=48), _lib.NESO_EUNSUPPORTED),
+    (dict(T=-1), _lib.NESO_EINVAL),
+    (dict(K_rel=A16 + 4), _lib.NESO_EINVAL),
+    (dict(rel_bias=A16 + 2), _lib.NESO_OK),  # fp16 output: 2-byte alignment
+    (dict(T=50000, nh=1), _lib.NESO_EUNSUPPORTED),  # T * T past 2^31
+])
+def test_relpos_precompute_validation(lib, kw, status):
+    assert relpre(lib, **kw) == status
 
 
 def relpos(lib, **kw):
