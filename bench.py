@@ -3,47 +3,61 @@
 
 A "step" is one FA2 forward launch over BASELINE's headline workload
 (B=1, H=16, N=2048, d=64, non-causal, fp16 in / fp32 out), inputs resident
-in HBM.  ``value`` = 4*B*H*N^2*d / (ms_per_step) in TFLOP/s.
+in HBM.  ``value`` = 4*B*H*N^2*d / ms_per_step in TFLOP/s, where
+``ms_per_step`` is the time of exactly ``--steps`` consecutive launches
+(captured in one HIP graph, replayed once between two HIP events on the
+replay stream, bracketed by device synchronisation) divided by ``--steps``;
+it includes the GPU's dispatch gap between consecutive kernels but not
+Python's launch cost.  ``timing`` adds the median (and 10th/90th
+percentiles) over 64 separately timed replays of a 16-launch graph, and the
+eager rate (launches one by one from Python, host-bound for short kernels).
 
-Launches are captured in a HIP graph (16 per graph) and the graph is
-replayed; HIP events recorded on the replay stream bracket the timed
-launches.  The per-launch time therefore includes the GPU's dispatch gap
-between consecutive kernels but not Python's launch cost, which exceeds the
-runtime of the smaller kernels (``eager_ms_per_step`` reports the eager
-rate for comparison).  The same line carries:
+The same line carries:
 
 * ``roofline`` for that kernel against dense-fp16 MFMA peak (2516.6 TFLOP/s
-  = 256 CU x 2.4 GHz x 4096 FLOP/clk);
+  = 256 CU x 2.4 GHz x 4096 FLOP/clk), with the HBM traffic per launch from
+  the committed counter summary;
 * ``cpu_baseline``: the CPU oracle (torch fp32, all host threads) on the
-  same workload, rank 0 only;
+  same workload, with the host CPU model;
 * ``qmatmul``: the int4 qmatmul at M=1, K=4096, N=11008 in HBM GB/s
   (algorithmic bytes K*N/2 + (K/32)*N*2 + M*K*2 + M*N*2), over 16 rotated
-  weight copies (> 256 MiB, so the Infinity Cache cannot hold them), with
-  its own roofline against 8 TB/s and its CPU baseline;
-* ``sweep``: the other BASELINE configs (FA2 N sweep, d=128 causal, rel-pos
-  N=1500, qmatmul M=16/256), one entry each.
+  weight copies (> 256 MiB, more than the Infinity Cache holds), with its
+  own roofline against 8 TB/s and its CPU baseline;
+* ``sweep``: every other BASELINE config (FA2 config 1 and the N sweep,
+  d=128 causal, rel-pos N=1500, qmatmul M=16/256), the fp32-input FA2 and
+  the reference-format W8A16 at 4096^3, each with its GPU rate, its
+  roofline fraction and its CPU baseline.
 
-``--calibrate-copy`` instead times a plain device-to-device copy of 256 MiB
-(torch's copy kernel), the reference for scaling the FETCH_SIZE/WRITE_SIZE
-counters to bytes.
+``--case NAME`` runs one workload only (for counter runs under rocprofv3);
+``--calibrate-copy`` times a plain 256 MiB device-to-device copy, the
+reference for scaling the FETCH_SIZE/WRITE_SIZE counters to bytes.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-sweep] [--no-cpu]
+       python bench.py --case fa2_headline|fa2_d128|relpos|w4a16_m1|... [--steps K]
        python bench.py --calibrate-copy
 """
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
+import platform
 import statistics
 import sys
 import time
 
 MFMA_F16_PEAK_TFLOPS = 2516.6  # 256 CUs * 2.4 GHz * 4096 dense fp16 FLOP/clk/CU
-FP32_MFMA_PEAK_TFLOPS = 157.3  # published dense fp32 MFMA peak
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 METRIC = "FA2 fwd TFLOP/s (d64,N2048) + % MFMA peak; int4 qmatmul HBM GB/s"
+GRAPH_LAUNCHES = 16
+MEDIAN_REPLAYS = 64
+ROTATE = 16  # weight copies for the qmatmul cases: 16 x 24.2 MB > 256 MB Infinity Cache
+
+# Seconds the GPU is kept busy with the timed workload before each
+# measurement.  An idle MI355X starts a burst of kernels at 1.5-1.7 GHz and
+# reaches its sustained ~2.2 GHz only after tens of milliseconds of load;
+# without this the first cases would be timed at the idle clock.
+CLOCK_RAMP_S = 0.3
 
 
 def parse():
@@ -53,6 +67,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--case", default=None, help="run one workload only (see CASES)")
     ap.add_argument("--calibrate-copy", action="store_true")
     ap.add_argument("--ramp", type=float, default=CLOCK_RAMP_S,
                     help="seconds of untimed load before each measurement (clock ramp); "
@@ -64,69 +79,107 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-GRAPH_LAUNCHES = 16
-
-
-# Seconds the GPU is kept busy with the timed workload before each
-# measurement.  An idle MI355X starts a burst of kernels at 1.5-1.7 GHz and
-# reaches its sustained ~2.2 GHz only after tens of milliseconds of load;
-# without this the first cases would be timed at the idle clock.
-CLOCK_RAMP_S = 0.3
-
-
-def ramp_clock(run_once, torch, seconds=None):
-    """Repeat ``run_once()`` (asynchronous GPU work) for ``seconds`` of wall time."""
-    seconds = CLOCK_RAMP_S if seconds is None else seconds
+def ramp_clock(run_once, torch):
+    """Repeat ``run_once()`` (asynchronous GPU work) for CLOCK_RAMP_S of wall time."""
     t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
+    while time.perf_counter() - t0 < CLOCK_RAMP_S:
         for _ in range(8):
             run_once()
         torch.cuda.synchronize()
 
 
-def time_launches(launch, steps, warmup, torch, per_graph=GRAPH_LAUNCHES):
-    """ms per launch of ``launch(i)``, replayed from a HIP graph.
-
-    ``per_graph`` consecutive launches (i = 0 .. per_graph-1) are captured
-    once; the graph is replayed ceil(steps / per_graph) times between two
-    events recorded on the current stream, which is the stream the replays
-    run on.  ``warmup`` launches run eagerly first (and compile nothing),
-    then the graph is replayed for CLOCK_RAMP_S seconds (untimed).
-    """
-    for i in range(warmup):
-        launch(i % per_graph)
-    torch.cuda.synchronize()
+def capture(launch, n, torch):
+    """A HIP graph of launch(0) .. launch(n-1) on a side stream."""
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        for i in range(per_graph):
+        for i in range(n):
             launch(i)
-    graph.replay()
-    torch.cuda.synchronize()
-    ramp_clock(graph.replay, torch)
-    replays = max(1, -(-steps // per_graph))
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(replays):
-        graph.replay()
-    stop.record()
-    torch.cuda.synchronize()
-    return start.elapsed_time(stop) / (replays * per_graph)
+    return graph
 
 
-def time_eager(launch, steps, torch):
-    """ms per launch when launched one by one from Python (host-bound for short kernels)."""
-    launch(0)
-    torch.cuda.synchronize()
-    ramp_clock(lambda: launch(0), torch, CLOCK_RAMP_S / 3)
-    start = torch.cuda.Event(enable_timing=True)
-    stop = torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(steps):
+def time_case(launch, steps, warmup, torch):
+    """Per-launch timing of ``launch(i)``.
+
+    Returns (ms per launch over exactly ``steps`` launches, timing dict).
+    The ``steps`` launches are one graph replayed once between HIP events on
+    the current stream (the graph replays on it), with device
+    synchronisation on both sides.  The dict adds the median / p10 / p90
+    over MEDIAN_REPLAYS separately timed replays of a GRAPH_LAUNCHES-launch
+    graph, and the eager (one-by-one from Python) rate.
+    """
+    for i in range(warmup):
         launch(i)
-    stop.record()
     torch.cuda.synchronize()
-    return start.elapsed_time(stop) / steps
+    g_steps = capture(launch, steps, torch)
+    g_small = capture(launch, GRAPH_LAUNCHES, torch)
+    g_small.replay()
+    torch.cuda.synchronize()
+    ramp_clock(g_small.replay, torch)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * MEDIAN_REPLAYS + 2)]
+    torch.cuda.synchronize()
+    ev[0].record()
+    g_steps.replay()
+    ev[1].record()
+    torch.cuda.synchronize()
+    ms = ev[0].elapsed_time(ev[1]) / steps
+    for r in range(MEDIAN_REPLAYS):
+        ev[2 + 2 * r].record()
+        g_small.replay()
+        ev[3 + 2 * r].record()
+    torch.cuda.synchronize()
+    per = sorted(ev[2 + 2 * r].elapsed_time(ev[3 + 2 * r]) / GRAPH_LAUNCHES
+                 for r in range(MEDIAN_REPLAYS))
+    # Eager launches (host-bound for short kernels; reported for comparison).
+    n_eager = min(steps, 64)
+    ev[0].record()
+    for i in range(n_eager):
+        launch(i)
+    ev[1].record()
+    torch.cuda.synchronize()
+    eager = ev[0].elapsed_time(ev[1]) / n_eager
+    return ms, {"graph_ms": round(ms, 6), "launches_timed": steps,
+                "median_ms": round(statistics.median(per), 6),
+                "p10_ms": round(per[len(per) // 10], 6),
+                "p90_ms": round(per[(9 * len(per)) // 10], 6),
+                "median_samples": MEDIAN_REPLAYS, "launches_per_sample": GRAPH_LAUNCHES,
+                "eager_ms": round(eager, 6)}
+
+
+def calibrate_copy(torch):
+    """Plain 256 MiB device copy: bytes moved per launch and its time."""
+    nbytes = 256 << 20
+    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    ms, _ = time_case(lambda i: dst.copy_(src), 16, 3, torch)
+    return {"metric": "device copy GB/s (read + write)", "bytes_read": nbytes,
+            "bytes_written": nbytes, "ms_per_copy": round(ms, 6),
+            "value": round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s"}
+
+
+def cpu_time(fn, reps=None):
+    """Median seconds after one warm-up: of 5 runs, or of 3 when one run takes
+    a second or more (the d = 128 config), as the CPU-baseline plan sets."""
+    t0 = time.perf_counter()
+    fn()
+    if reps is None:
+        reps = 5 if time.perf_counter() - t0 < 1.0 else 3
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
 
 
 def measured_traffic(key):
@@ -145,48 +198,143 @@ def measured_traffic(key):
     return None if entry is None else entry.get("hbm_bytes_per_launch")
 
 
-def best_time(launch, steps, warmup, torch):
-    """(ms per launch, mode, graph ms, eager ms): the faster of graph replay and eager launches.
+# ---------------------------------------------------------------------------
+# Workloads.  Each returns (launch(i), work per launch, unit kind, config,
+# cpu_fn or None, extra dict); the work is FLOP ("flop") or bytes ("bytes").
 
-    Short kernels are host-bound when launched from Python, so graph replay
-    is their rate; long kernels keep the queue full either way and the
-    graph's per-node overhead can make eager launches faster.
-    """
-    g = time_launches(launch, steps, warmup, torch)
-    e = time_eager(launch, min(steps, 64), torch)
-    return (g, "graph", g, e) if g <= e else (e, "eager", g, e)
-
-
-def calibrate_copy(torch):
-    """Plain 256 MiB device copy: bytes moved per launch and its time."""
-    nbytes = 256 << 20
-    src = torch.empty(nbytes, dtype=torch.uint8, device="cuda").random_(0, 255)
-    dst = torch.empty_like(src)
-    ms = time_launches(lambda i: dst.copy_(src), 20, 3, torch, per_graph=4)
-    return {"metric": "device copy GB/s (read + write)", "bytes_read": nbytes,
-            "bytes_written": nbytes, "ms_per_copy": round(ms, 6),
-            "value": round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "unit": "GB/s"}
-
-
-def cpu_time(fn, reps):
-    fn()
-    ts = []
-    for _ in range(reps):
-        t0 = time.perf_counter()
-        fn()
-        ts.append(time.perf_counter() - t0)
-    return statistics.median(ts)
-
-
-def fa2_case(neso_amd, torch, I, B, H, N, d, causal, steps, warmup, seed=0):
-    from oracle import attention as A  # FLOP formula only
-    q, k, v = (t.cuda() for t in I.fa2_inputs(B, H, N, d, seed=seed))
+def fa2_workload(neso_amd, torch, I, B, H, N, d, causal, want_cpu, f32=False):
+    from oracle import attention as A  # FLOP formula and CPU baseline only
+    q, k, v = (t.cuda() for t in I.fa2_inputs(B, H, N, d, seed=0))
+    if f32:
+        q, k, v = q.float(), k.float(), v.float()
     out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
-    ms, mode, g, e = best_time(lambda i: neso_amd.attention(q, k, v, causal=causal, out=out),
-                               steps, warmup, torch)
-    flop = A.flops(B, H, N, d, causal)
-    return ms, flop / (ms * 1e-3) / 1e12, (q, k, v), {"timing": mode, "graph_ms": round(g, 6),
-                                                      "eager_ms": round(e, 6)}
+    scale = A.default_scale(d)
+    launch = lambda i: neso_amd.attention(q, k, v, causal=causal, out=out)
+    cpu = None
+    if want_cpu:
+        qc, kc, vc = (t.cpu() for t in (q, k, v))
+        cpu = lambda: A.attention(qc, kc, vc, scale, causal=causal)
+    cfg = {"B": B, "H": H, "N": N, "d": d, "causal": causal}
+    return launch, A.flops(B, H, N, d, causal), "flop", cfg, cpu
+
+
+def relpos_workload(neso_amd, torch, I, want_cpu):
+    from oracle import attention as A
+    rc = I.RELPOS_CONFIG
+    q, k, v, table = (t.cuda() for t in I.relpos_inputs(**rc, seed=0))
+    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
+    launch = lambda i: neso_amd.rel_pos_attention(q, k, v, table, out=out)
+    cpu = None
+    if want_cpu:
+        qc, kc, vc, tc = (t.cpu() for t in (q, k, v, table))
+        cpu = lambda: A.rel_pos_attention_table(qc, kc, vc, tc, A.default_scale(rc["d"]))
+    return launch, 4.0 * rc["H"] * rc["N"] ** 2 * rc["d"], "flop", dict(rc), cpu
+
+
+def w4a16_workload(neso_amd, torch, I, M, want_cpu, rotate=ROTATE):
+    from oracle import qmatmul as Q
+    import numpy as np
+    K, N = 4096, 11008
+    x, codes, scales = I.qmatmul_inputs(M, K, N, seed=0)
+    words = torch.from_numpy(Q.pack_int4(codes.numpy()))
+    xs = x.cuda()
+    ws = [words.cuda() for _ in range(rotate)]
+    ss = [scales.cuda() for _ in range(rotate)]
+    y = torch.empty(M, N, dtype=torch.float16, device="cuda")
+    launch = lambda i: neso_amd.w4a16_matmul(xs, ws[i % rotate], ss[i % rotate], y, M, N, K, K, N)
+    cpu = None
+    if want_cpu:
+        xc = x.float()
+        wdq = torch.from_numpy(Q.dequant_int4(words.numpy(), scales.numpy(), dtype=np.float32))
+
+        def cpu():  # dequantise (numpy oracle) + fp32 matmul
+            w = torch.from_numpy(Q.dequant_int4(words.numpy(), scales.numpy(), dtype=np.float32))
+            return xc @ w.T
+        cpu.matmul_only = lambda: xc @ wdq.T  # weights dequantised beforehand
+    cfg = {"M": M, "K": K, "N": N, "group": 32, "zero": 8, "rotated_weight_copies": rotate}
+    return launch, Q.algorithmic_bytes(M, N, K), "bytes", cfg, cpu
+
+
+def w8a16_workload(neso_amd, torch, scaled, want_cpu):
+    m = n = k = 4096
+    g = torch.Generator().manual_seed(0)
+    a = torch.randn(m, k, generator=g).half()
+    b = torch.randint(-128, 128, (k, n), generator=g, dtype=torch.int8)
+    sc = (torch.rand(n, generator=g) * 0.1 + 0.001).half()
+    ad, bd, sd = a.cuda(), b.cuda(), sc.cuda()
+    c = torch.empty(m, n, dtype=torch.float32, device="cuda")
+    if scaled:
+        launch = lambda i: neso_amd.w8a16_scaled_matmul(ad, bd, c, sd, k, k, n, n, M=m, N=n)
+    else:
+        launch = lambda i: neso_amd.w8a16_matmul(ad, bd, c, k, k, n, n, M=m, N=n)
+    cpu = None
+    if want_cpu:
+        af, bf, sf = a.float(), b.float(), sc.float()
+        cpu = (lambda: (af @ bf) * sf) if scaled else (lambda: af @ bf)
+    return launch, 2.0 * m * n * k, "flop", {"M": m, "N": n, "K": k}, cpu
+
+
+def run_case(workload, steps, warmup, torch, want_cpu):
+    """Time one workload; returns a result row."""
+    launch, work, kind, cfg, cpu = workload
+    ms, timing = time_case(launch, steps, warmup, torch)
+    row = dict(cfg)
+    row["us"] = round(ms * 1e3, 3)
+    row["timing"] = timing
+    if kind == "flop":
+        tf = work / (ms * 1e-3) / 1e12
+        row["tflops"] = round(tf, 3)
+        row["mfma_frac"] = round(tf / MFMA_F16_PEAK_TFLOPS, 4)
+        row["tflops_median"] = round(work / (timing["median_ms"] * 1e-3) / 1e12, 3)
+    else:
+        gbs = work / (ms * 1e-3) / 1e9
+        row["gbs"] = round(gbs, 2)
+        row["hbm_frac"] = round(gbs / HBM_PEAK_GBS, 4)
+        row["gbs_median"] = round(work / (timing["median_ms"] * 1e-3) / 1e9, 2)
+        row["algorithmic_bytes"] = work
+    if want_cpu and cpu is not None:
+        sec = cpu_time(cpu)
+        row["cpu_seconds"] = round(sec, 5)
+        if kind == "flop":
+            row["cpu_tflops"] = round(work / sec / 1e12, 5)
+        else:
+            row["cpu_gbs"] = round(work / sec / 1e9, 4)
+            if hasattr(cpu, "matmul_only"):
+                row["cpu_matmul_only_gbs"] = round(work / cpu_time(cpu.matmul_only) / 1e9, 4)
+        row["gpu_over_cpu"] = round(sec / (ms * 1e-3), 1)
+    return row
+
+
+def cases(neso_amd, torch, I, want_cpu):
+    """name -> thunk building the workload (built lazily to bound memory)."""
+    c = {
+        "fa2_headline": lambda: fa2_workload(neso_amd, torch, I, 1, 16, 2048, 64, False, want_cpu),
+        "fa2_config1": lambda: fa2_workload(neso_amd, torch, I, 1, 8, 128, 64, False, want_cpu),
+        "fa2_d128": lambda: fa2_workload(neso_amd, torch, I, 2, 32, 4096, 128, True, want_cpu),
+        "fa2_f32_qkv": lambda: fa2_workload(neso_amd, torch, I, 1, 16, 2048, 64, False, want_cpu,
+                                            f32=True),
+        "relpos": lambda: relpos_workload(neso_amd, torch, I, want_cpu),
+        "w8a16": lambda: w8a16_workload(neso_amd, torch, False, want_cpu),
+        "w8a16_scaled": lambda: w8a16_workload(neso_amd, torch, True, want_cpu),
+    }
+    for cfg in I.FA2_SWEEP:
+        name = f"fa2_n{cfg['N']}{'_causal' if cfg['causal'] else ''}"
+        c[name] = (lambda cfg=cfg: fa2_workload(neso_amd, torch, I, cfg["B"], cfg["H"], cfg["N"],
+                                                cfg["d"], cfg["causal"], want_cpu))
+    for m in (1, 16, 256):
+        c[f"w4a16_m{m}"] = lambda m=m: w4a16_workload(neso_amd, torch, I, m, want_cpu)
+    return c
+
+
+SWEEP_ORDER = ["fa2_config1"] + [f"fa2_n{n}{s}" for n in (128, 256, 512, 1024, 2048)
+                                 for s in ("", "_causal")] + [
+    "fa2_d128", "relpos", "fa2_f32_qkv", "w8a16", "w8a16_scaled", "w4a16_m16", "w4a16_m256"]
+KERNEL_OF = {  # device kernel each sweep row's time is dominated by (for readers)
+    "fa2_f32_qkv": "fa2_fwd_kernel (F32IN: 3 fp16 MFMAs per product)",
+    "relpos": "fa2_fwd_kernel (BIAS = f32 table)",
+    "w8a16": "w8a16_gemm_kernel", "w8a16_scaled": "w8a16_gemm_kernel",
+    "w4a16_m16": "w4a16_skinny_lds_kernel", "w4a16_m256": "w4a16_tile_gemm_kernel",
+}
 
 
 def main():
@@ -194,8 +342,8 @@ def main():
     args = parse()
     CLOCK_RAMP_S = max(0.0, args.ramp)
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1",
-                          "n_gpus": args.gpus}))
+        print(json.dumps({"error": "this build runs on exactly one GPU (one process, one "
+                                   "device); --gpus must be 1", "n_gpus": args.gpus}))
         return 2
     import torch
 
@@ -208,22 +356,35 @@ def main():
         return 0
     dev = torch.cuda.get_device_properties(0)
     log(f"device {dev.name} {dev.gcnArchName} CUs={dev.multi_processor_count}")
+    want_cpu = not args.no_cpu
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    C = cases(neso_amd, torch, I, want_cpu and args.case is None)
+
+    if args.case is not None:
+        if args.case not in C:
+            print(json.dumps({"error": f"unknown case {args.case!r}", "cases": sorted(C)}))
+            return 2
+        row = run_case(C[args.case](), args.steps, args.warmup, torch, False)
+        print(json.dumps({"case": args.case, **row}), flush=True)
+        return 0
 
     # ---- headline: FA2 forward, B1 H16 N2048 d64 non-causal ----
-    hb = I.FA2_HEADLINE
-    ms, tflops, (q, k, v), tmode = fa2_case(neso_amd, torch, I, hb["B"], hb["H"], hb["N"],
-                                            hb["d"], False, args.steps, args.warmup)
-    log(f"fa2 headline {ms * 1e3:.2f} us/launch {tflops:.1f} TFLOP/s ({tmode})")
-    flop = 4.0 * hb["B"] * hb["H"] * hb["N"] ** 2 * hb["d"]
+    head = run_case(C["fa2_headline"](), args.steps, args.warmup, torch, want_cpu)
+    ms = head["us"] * 1e-3
+    tflops = head["tflops"]
+    log(f"fa2 headline {head['us']:.2f} us/launch {tflops:.1f} TFLOP/s "
+        f"(median {head['timing']['median_ms'] * 1e3:.2f} us)")
+    flop = 4.0 * 1 * 16 * 2048 ** 2 * 64
     result = {
         "metric": METRIC,
-        "value": round(tflops, 3),
+        "value": tflops,
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 6),
-        "timing": tmode,
+        "timing": head["timing"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -232,150 +393,65 @@ def main():
         "config": {"workload": "flash_attention_fwd B=1 H=16 N=2048 d=64 non-causal, "
                                "fp16 Q/K/V ~ N(0,1), fp32 accumulation and output",
                    "B": 1, "H": 16, "N": 2048, "d": 64, "causal": False},
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 3),
-                     "peak": MFMA_F16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+        "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("fa2_headline"),
                      "kernel": "fa2_fast_kernel<64,false,false,2,false>",
                      "algorithmic_flop_per_launch": flop},
     }
+    if want_cpu:
+        result["cpu_baseline"] = {
+            "value": head["cpu_tflops"], "unit": "TFLOP/s", "cores": threads,
+            "cpu_model": cpu_model(), "kind": "port",
+            "sample": "oracle.attention (torch fp32 CPU, chunked rows) on the full headline "
+                      "workload B1 H16 N2048 d64, median of 5 after 1 warm-up",
+            "seconds_per_step": head["cpu_seconds"]}
+        log(f"cpu baseline {head['cpu_seconds']:.3f} s/step")
 
     # ---- int4 qmatmul, M=1 (HBM-bound), rotated weights ----
-    qc = I.QMM_CONFIGS[0]
-    result["qmatmul"] = qmm_case(neso_amd, torch, I, qc, args.steps, args.warmup,
-                                 rotate=16, want_cpu=not args.no_cpu)
-    log(f"qmm M=1 {result['qmatmul']['value']:.1f} GB/s")
-
-    # ---- CPU baseline (rank 0, N=1): the oracle on the same workload ----
-    if not args.no_cpu:
-        from oracle import attention as A
-        threads = os.cpu_count() or 1
-        torch.set_num_threads(threads)
-        qc_, kc_, vc_ = (t.cpu() for t in (q, k, v))
-        sec = cpu_time(lambda: A.attention(qc_, kc_, vc_, 1 / 8), reps=3)
-        result["cpu_baseline"] = {
-            "value": round(flop / sec / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
-            "kind": "port",
-            "sample": "oracle.attention (torch fp32 CPU, chunked rows) on the full headline "
-                      "workload B1 H16 N2048 d64, median of 3 after 1 warm-up",
-            "seconds_per_step": round(sec, 4)}
-        log(f"cpu baseline {sec:.3f} s/step")
-
-    if not args.no_sweep:
-        result["sweep"] = sweep(neso_amd, torch, I, max(20, args.steps // 4), 5)
-
-    print(json.dumps(result), flush=True)
-    return 0
-
-
-def qmm_case(neso_amd, torch, I, cfg, steps, warmup, rotate=1, want_cpu=False):
-    from oracle import qmatmul as Q
-    import numpy as np
-    M, K, N = cfg["M"], cfg["K"], cfg["N"]
-    x, codes, scales = I.qmatmul_inputs(M, K, N, seed=0)
-    words = torch.from_numpy(Q.pack_int4(codes.numpy()))
-    xs = x.cuda()
-    ws = [words.cuda() for _ in range(rotate)]
-    ss = [scales.cuda() for _ in range(rotate)]
-    y = torch.empty(M, N, dtype=torch.float16, device="cuda")
-    launch = lambda i: neso_amd.w4a16_matmul(xs, ws[i % rotate], ss[i % rotate], y, M, N, K, K,
-                                             N)
-    ms, mode, g_ms, e_ms = best_time(launch, steps, warmup, torch)
-    nbytes = Q.algorithmic_bytes(M, N, K)
-    gbs = nbytes / (ms * 1e-3) / 1e9
-    tflops = Q.flops(M, N, K) / (ms * 1e-3) / 1e12
-    out = {"metric": "int4 qmatmul HBM GB/s", "value": round(gbs, 2), "unit": "GB/s",
-           "ms_per_step": round(ms, 6),
-           "timing": {"timing": mode, "graph_ms": round(g_ms, 6), "eager_ms": round(e_ms, 6)},
-           "tflops": round(tflops, 3),
-           "config": {"workload": f"w4a16_matmul M={M} K={K} N={N} group=32 zero=8, fp16 "
-                                  f"X, fp16 out, {rotate} rotated weight copies",
-                      "M": M, "K": K, "N": N},
-           "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS,
-                        "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
-                        "traffic": measured_traffic(f"w4a16_M{M}"),
-                        "algorithmic_bytes_per_launch": nbytes}}
+    qm = run_case(C["w4a16_m1"](), args.steps, args.warmup, torch, want_cpu)
+    gbs = qm["gbs"]
+    result["qmatmul"] = {
+        "metric": "int4 qmatmul HBM GB/s", "value": gbs, "unit": "GB/s",
+        "ms_per_step": round(qm["us"] * 1e-3, 6), "timing": qm["timing"],
+        "config": {"workload": f"w4a16_matmul M=1 K=4096 N=11008 group=32 zero=8, fp16 X, "
+                               f"fp16 out, {ROTATE} rotated weight copies",
+                   "M": 1, "K": 4096, "N": 11008},
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("w4a16_M1"),
+                     "kernel": "w4a16_gemv_kernel<1,2,4,true>",
+                     "algorithmic_bytes_per_launch": qm["algorithmic_bytes"]}}
     if want_cpu:
-        threads = os.cpu_count() or 1
-        torch.set_num_threads(threads)
-        xc = x.float()
-        wdq = torch.from_numpy(Q.dequant_int4(words.numpy(), scales.numpy(), dtype=np.float32))
-
-        def full():
-            w = torch.from_numpy(Q.dequant_int4(words.numpy(), scales.numpy(), dtype=np.float32))
-            return xc @ w.T
-
-        t_full = cpu_time(full, reps=3)
-        t_mm = cpu_time(lambda: xc @ wdq.T, reps=5)
-        out["cpu_baseline"] = {
-            "value": round(nbytes / t_full / 1e9, 3), "unit": "GB/s", "cores": threads,
+        result["qmatmul"]["cpu_baseline"] = {
+            "value": qm["cpu_gbs"], "unit": "GB/s", "cores": threads, "cpu_model": cpu_model(),
             "kind": "port",
             "sample": "oracle dequant_int4 (numpy) + torch fp32 matmul on the full M=1 "
-                      "workload, median of 3; matmul-only with pre-dequantised weights in "
-                      "matmul_only_gbs",
-            "matmul_only_gbs": round(nbytes / t_mm / 1e9, 3)}
-    return out
+                      "workload, median of 5 after 1 warm-up; matmul_only_gbs with the "
+                      "weights dequantised beforehand",
+            "seconds_per_step": qm["cpu_seconds"],
+            "matmul_only_gbs": qm.get("cpu_matmul_only_gbs")}
+    log(f"qmm M=1 {gbs:.1f} GB/s")
 
-
-def sweep(neso_amd, torch, I, steps, warmup):
-    rows = []
-    for cfg in I.FA2_SWEEP:
-        ms, tf, _, tm = fa2_case(neso_amd, torch, I, cfg["B"], cfg["H"], cfg["N"], cfg["d"],
-                                 cfg["causal"], steps, warmup)
-        rows.append({"kernel": "fa2", **cfg, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
-                     "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "timing": tm["timing"]})
-    c = I.FA2_D128
-    ms, tf, _, tm = fa2_case(neso_amd, torch, I, c["B"], c["H"], c["N"], c["d"], c["causal"],
-                             max(16, steps // 4), 2)
-    rows.append({"kernel": "fa2", **c, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
-                 "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "timing": tm["timing"]})
-    # fp32 Q/K/V (the reference's default qkv_dtype) at the headline shape:
-    # three fp16 MFMAs per product, so the useful-FLOP rate is compared with
-    # the fp32 dense MFMA peak, the unit that computes in this precision.
-    hb = I.FA2_HEADLINE
-    q, k, v = (t.cuda().float() for t in I.fa2_inputs(hb["B"], hb["H"], hb["N"], hb["d"]))
-    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
-    ms, mode, _, _ = best_time(lambda i: neso_amd.attention(q, k, v, out=out), steps, warmup,
-                               torch)
-    tf = 4.0 * hb["B"] * hb["H"] * hb["N"] ** 2 * hb["d"] / (ms * 1e-3) / 1e12
-    rows.append({"kernel": "fa2_f32_qkv", **hb, "causal": False, "us": round(ms * 1e3, 2),
-                 "tflops": round(tf, 2), "fp32_mfma_frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4),
-                 "timing": mode})
-    rc = I.RELPOS_CONFIG
-    q, k, v, table = (t.cuda() for t in I.relpos_inputs(**rc, seed=0))
-    out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
-    ms, mode, _, _ = best_time(lambda i: neso_amd.rel_pos_attention(q, k, v, table, out=out),
-                               steps, warmup, torch)
-    flop = 4.0 * rc["H"] * rc["N"] ** 2 * rc["d"]
-    tf = flop / (ms * 1e-3) / 1e12
-    rows.append({"kernel": "rel_pos_fa2", **rc, "us": round(ms * 1e3, 2), "tflops": round(tf, 2),
-                 "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4), "timing": mode})
-    # Reference-format W8A16 at the size the reference publishes (4096^3,
-    # PERFORMANCE.md:61-63 and :77-81: 5,744 and 5,976 GFLOP/s on Apple M2 Max).
-    m = n = k = 4096
-    a = torch.randn(m, k, dtype=torch.float16, device="cuda")
-    b = torch.randint(-128, 128, (k, n), dtype=torch.int8, device="cuda")
-    c = torch.empty(m, n, dtype=torch.float32, device="cuda")
-    sc = (torch.rand(n, device="cuda") * 0.1 + 0.001).half()
-    for name, fn, ref_gflops in (
-            ("w8a16_matmul", lambda i: neso_amd.w8a16_matmul(a, b, c, k, k, n, n, M=m, N=n),
-             5744.0),
-            ("w8a16_scaled_matmul",
-             lambda i: neso_amd.w8a16_scaled_matmul(a, b, c, sc, k, k, n, n, M=m, N=n), 5976.0)):
-        ms, mode, _, _ = best_time(fn, max(16, steps // 4), 2, torch)
-        tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-        rows.append({"kernel": name, "M": m, "N": n, "K": k, "us": round(ms * 1e3, 2),
-                     "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
-                     "reference_m2max_tflops": ref_gflops / 1e3,
-                     "x_reference": round(tf / (ref_gflops / 1e3), 1), "timing": mode})
-    for cfg in I.QMM_CONFIGS[1:]:
-        r = qmm_case(neso_amd, torch, I, cfg, steps, warmup, rotate=8)
-        rows.append({"kernel": "w4a16", **cfg, "us": round(r["ms_per_step"] * 1e3, 2),
-                     "gbs": r["value"], "tflops": r["tflops"],
-                     "hbm_frac": r["roofline"]["frac"],
-                     "mfma_frac": round(r["tflops"] / MFMA_F16_PEAK_TFLOPS, 4),
-                     "timing": r["timing"]["timing"]})
-    return rows
+    if not args.no_sweep:
+        rows = []
+        sweep_steps = max(32, min(args.steps, 64))
+        for name in SWEEP_ORDER:
+            row = run_case(C[name](), sweep_steps, 5, torch, want_cpu)
+            row = {"case": name, **({"kernel": KERNEL_OF[name]} if name in KERNEL_OF else {}),
+                   **row}
+            if name == "fa2_f32_qkv":
+                # Three fp16 MFMAs per product: the issued MFMA work is 3x
+                # the useful FLOPs counted in tflops / mfma_frac.
+                row["mfma_frac_issued"] = round(3 * row["mfma_frac"], 4)
+            if name.startswith("w4a16"):
+                row["mfma_frac"] = round(2.0 * row["M"] * row["N"] * row["K"]
+                                         / (row["us"] * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
+            rows.append(row)
+            torch.cuda.empty_cache()
+            log(f"{name}: {row['us']:.2f} us")
+        result["sweep"] = rows
+    print(json.dumps(result), flush=True)
+    return 0
 
 
 if __name__ == "__main__":
