@@ -14,6 +14,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime the library shares)
 
 LIB_PATH = Path(__file__).resolve().parent / "libneso_amd.so"
+SERIAL_LIB_PATH = Path(__file__).resolve().parent / "libneso_amd_serial.so"
 
 NESO_OK = 0
 NESO_EINVAL = 1
@@ -112,6 +113,20 @@ def load() -> ctypes.CDLL:
             fn.argtypes = args
         _lib = lib
         return lib
+
+
+def load_variant(path: Path) -> ctypes.CDLL:
+    """Load another build of the library (e.g. libneso_amd_serial.so, the
+    debug build whose fast FA2 kernel serialises every LDS phase) with the
+    same signatures; for tests that compare builds."""
+    if not Path(path).exists():
+        raise ImportError(f"{path} is missing: build it with `python -m neso_amd.build`")
+    lib = ctypes.CDLL(str(path))
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
 
 
 def check(status: int) -> None:

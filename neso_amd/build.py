@@ -20,6 +20,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 BUILD_DIR = PKG / "_build"
 LIB_PATH = PKG / "libneso_amd.so"
+SERIAL_LIB_PATH = PKG / "libneso_amd_serial.so"
 ARCH = "gfx950"
 
 SOURCES = ["neso_abi.hip", "fa2_fwd.hip", "fa2_fast.hip", "relpos_pre.hip", "qmatmul.hip",
@@ -45,6 +46,59 @@ COMMON_FLAGS = [
 ]
 
 
+# The hipcc on which the fast FA2 kernel's LDS-DMA inline asm (M0 written
+# behind the compiler's back, fa2_tiles.h: lds_dma16) was last verified on
+# the GPU.  Every build also checks the property itself in the generated
+# assembly (m0_check); a different version only adds a note.
+VERIFIED_HIPCC = "7.2.26015"
+
+# Opcodes that read or write M0 without naming it (GFX9 family): relative
+# moves, messages, GWS, append/consume, thread-indexed LDS access and
+# LDS-DMA loads.
+_M0_IMPLICIT = ("movrel", "s_sendmsg", "ds_gws", "ds_append", "ds_consume", "ds_ordered_count",
+                "_addtid", "global_load_lds", "s_ttracedata")
+
+
+def m0_check(asm: str) -> list[str]:
+    """Problems with M0 use in a device assembly listing (empty: none).
+
+    The only instructions allowed to touch M0 are the kernels' own LDS-DMA
+    sequences: an inline-asm block of exactly ``s_mov_b32 m0, sN``,
+    ``s_nop 0``, ``buffer_load_dwordx4 vN, s[..], 0 offen lds``.  Anything
+    else that names M0 or uses it implicitly, inside or outside such a
+    block, is reported.
+    """
+    import re
+    problems = []
+    lines = [ln.split(";", 1)[0].strip() if not ln.strip().startswith(";;#ASM") else ln.strip()
+             for ln in asm.splitlines()]
+    i = 0
+    while i < len(lines):
+        ln = lines[i]
+        if ln == ";;#ASMSTART":
+            j = i + 1
+            body = []
+            while j < len(lines) and lines[j] != ";;#ASMEND":
+                if lines[j]:
+                    body.append(lines[j])
+                j += 1
+            if any(re.search(r"\bm0\b", b) or " lds" in b for b in body):
+                ok = (len(body) == 3 and re.fullmatch(r"s_mov_b32 m0, s\d+", body[0])
+                      and body[1] == "s_nop 0"
+                      and re.fullmatch(r"buffer_load_dwordx4 v\d+, s\[\d+:\d+\], 0 offen lds",
+                                       body[2]))
+                if not ok:
+                    problems.append("unexpected inline-asm block: " + " | ".join(body))
+            i = j + 1
+            continue
+        if ln and not ln.startswith((".", ";")) and not ln.endswith(":"):
+            op = ln.split()[0]
+            if re.search(r"\bm0\b", ln) or any(t in op for t in _M0_IMPLICIT) or ln.endswith(" lds"):
+                problems.append("compiler-generated M0 use: " + ln)
+        i += 1
+    return problems
+
+
 def hipcc() -> str:
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not Path(exe).exists():
@@ -64,23 +118,73 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> None:
         sys.stderr.write("\n".join(lines) + "\n")
 
 
-def build(extra_flags: list[str] | None = None, jobs: int | None = None) -> Path:
-    """Compile every translation unit and link ``libneso_amd.so``; return its path."""
-    extra = list(extra_flags or [])
-    BUILD_DIR.mkdir(exist_ok=True)
-    objs = [BUILD_DIR / (Path(s).stem + ".o") for s in SOURCES]
-    jobs = jobs or min(len(SOURCES), os.cpu_count() or 1)
-    with ThreadPoolExecutor(max_workers=jobs) as ex:
-        futs = [ex.submit(_compile, CSRC / s, o, extra + SOURCE_FLAGS.get(s, []))
-                for s, o in zip(SOURCES, objs)]
-        for f in futs:
-            f.result()
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+def _device_asm(src: Path, extra: list[str]) -> str:
+    out = BUILD_DIR / (src.stem + ".gfx950.s")
+    cmd = [hipcc(), *COMMON_FLAGS, *extra, "--offload-device-only", "-S", str(src), "-o", str(out)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc -S failed for {src.name}:\n{res.stdout}{res.stderr}")
+    text = out.read_text()
+    out.unlink()
+    return text
+
+
+def _link(objs: list[Path], path: Path) -> None:
+    tmp = path.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{res.stdout}{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, path)
+
+
+def hipcc_version() -> str:
+    res = subprocess.run([hipcc(), "--version"], capture_output=True, text=True)
+    for ln in res.stdout.splitlines():
+        if ln.startswith("HIP version:"):
+            return ln.split(":", 1)[1].strip()
+    return "unknown"
+
+
+def build(extra_flags: list[str] | None = None, jobs: int | None = None) -> Path:
+    """Compile every translation unit and link ``libneso_amd.so``; return its path.
+
+    Also links ``libneso_amd_serial.so``, the same library whose fast FA2
+    kernel ends every LDS phase in a full wait and barrier
+    (NESO_FA2_SERIAL_LDS), which the GPU tests compare bit for bit with the
+    pipelined build.  The fast kernel's LDS-DMA asm is checked in the
+    generated assembly; if the check fails, both libraries are built without
+    the fast kernel (NESO_FA2_FAST_DISABLED) and a warning is printed.
+    """
+    extra = list(extra_flags or [])
+    BUILD_DIR.mkdir(exist_ok=True)
+    objs = [BUILD_DIR / (Path(s).stem + ".o") for s in SOURCES]
+    serial_obj = BUILD_DIR / "fa2_fast_serial.o"
+    jobs = jobs or min(len(SOURCES) + 2, os.cpu_count() or 1)
+    with ThreadPoolExecutor(max_workers=jobs) as ex:
+        asm = ex.submit(_device_asm, CSRC / "fa2_fast.hip", extra)
+        futs = [ex.submit(_compile, CSRC / s, o, extra + SOURCE_FLAGS.get(s, []))
+                for s, o in zip(SOURCES, objs)]
+        futs.append(ex.submit(_compile, CSRC / "fa2_fast.hip", serial_obj,
+                              extra + ["-DNESO_FA2_SERIAL_LDS"]))
+        for f in futs:
+            f.result()
+        problems = m0_check(asm.result())
+    if problems:
+        sys.stderr.write("neso_amd build: the fast FA2 kernel's LDS-DMA M0 assumption does not "
+                         "hold for this compiler; building without the fast kernel:\n  "
+                         + "\n  ".join(problems[:10]) + "\n")
+        fast = CSRC / "fa2_fast.hip"
+        _compile(fast, objs[SOURCES.index("fa2_fast.hip")], extra + ["-DNESO_FA2_FAST_DISABLED"])
+        _compile(fast, serial_obj, extra + ["-DNESO_FA2_FAST_DISABLED"])
+    ver = hipcc_version()
+    if not ver.startswith(VERIFIED_HIPCC):
+        sys.stderr.write(f"neso_amd build: hipcc {ver}; the fast FA2 kernel was last verified on "
+                         f"the GPU with {VERIFIED_HIPCC} (its assembly check passed: "
+                         f"{not problems})\n")
+    _link(objs, LIB_PATH)
+    _link([serial_obj if s == "fa2_fast.hip" else o for s, o in zip(SOURCES, objs)],
+          SERIAL_LIB_PATH)
     return LIB_PATH
 
 

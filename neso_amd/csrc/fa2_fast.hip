@@ -62,6 +62,18 @@ constexpr int fast_group_lds_halves() {
   return kSlots * 2 * fast_kb<D>() * D;
 }
 
+// Debug build (NESO_FA2_SERIAL_LDS): every LDS phase ends in a full wait and
+// a workgroup barrier, so no LDS-DMA write overlaps any LDS read and no wave
+// runs ahead of another within a step.  It must give bit-identical results
+// to the pipelined ring; a race in the ring's slot bookkeeping would show up
+// as a difference.  The pipelined build compiles this to nothing.
+__device__ __forceinline__ void serial_lds_point() {
+#ifdef NESO_FA2_SERIAL_LDS
+  wait_vmem();
+  lds_barrier();
+#endif
+}
+
 // PAIR (causal only): each workgroup takes two query blocks, see below.
 template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT, bool PAIR = false>
 __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
@@ -375,8 +387,16 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   auto body = [&](int i, float16v(&s)[NT], float16v(&sn)[NT], half8v(&pprev)[2 * NT],
                   half8v(&pcur)[2 * NT]) {
     const int si = i & 3;
+#ifdef NESO_FA2_SERIAL_LDS
+    // The debug build's barrier must be reached by every wave (my_n differs
+    // between key groups), so the loads are issued outside the branch.
+    if (i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
+    serial_lds_point();
+    if (i < my_n) {
+#else
     if (i < my_n) {
       if (i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
+#endif
       const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
       // Some key of the block is past N or outside some query's window.
       const bool masked =
@@ -391,6 +411,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     // Steps past the group's last block load nothing: no later step reads
     // those blocks, and the last block's V (read by the P V after the loop)
     // stays in place.
+    serial_lds_point();
     wait_vmem();
     lds_barrier();
   };
@@ -408,6 +429,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // of block 2.  (Scores of blocks a group does not have come from stale
   // slots and are never used.) ----
   if (my_n > 2) lds_load(2, 2);
+  serial_lds_point();
   qk(sa, kslot(0));
   if (my_n > 0) {
     const int kb0 = (blk0 + kg) * kKB;
@@ -592,7 +614,14 @@ hipError_t launch_fast_d(const Fa2Args& a, int d, bool causal, int ksplit, hipSt
 }  // namespace
 
 bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32) {
+#ifdef NESO_FA2_FAST_DISABLED
+  // Built without the fast kernel (its LDS-DMA M0 check failed at build
+  // time): every call takes the generic kernel.
+  (void)head_dim, (void)bias_kind, (void)in_f32;
+  return false;
+#else
   return (head_dim == 64 || head_dim == 128) && bias_kind == kBiasNone && !in_f32;
+#endif
 }
 
 bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid) {
@@ -610,6 +639,10 @@ bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid) {
 
 hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, int ksplit,
                            hipStream_t stream) {
+#ifdef NESO_FA2_FAST_DISABLED
+  (void)a, (void)head_dim, (void)causal, (void)out_f16, (void)ksplit, (void)stream;
+  return hipErrorInvalidValue;
+#endif
   a.num_qblocks = (a.N + kBM - 1) / kBM;
   // Paired query blocks (causal kernels only; any window is correct).
   a.pair_qblocks = (causal && a.pair_qblocks == 1) ? 1 : 0;

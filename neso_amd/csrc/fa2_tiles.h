@@ -108,8 +108,10 @@ __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70)
 // cannot tell that they read other slots); the kernel orders these writes
 // itself with s_waitcnt vmcnt(0) and a barrier before the slot is read.
 // Vector loads only; M0 holds the LDS base (one wait state after writing
-// it).  The compiler treats M0 as reserved and ignores the clobber; these
-// kernels use M0 nowhere else (checked in their ISA).
+// it).  The compiler treats M0 as reserved and ignores the clobber, so
+// correctness rests on no compiler-generated instruction using M0 in these
+// kernels: neso_amd/build.py checks the assembly of every build for that and
+// builds the library without the fast kernel if the check fails.
 __device__ __forceinline__ void lds_dma16(rsrc_t r, uint32_t lds, uint32_t voff) {
   asm volatile(
       "s_mov_b32 m0, %0\n\t"
