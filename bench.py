@@ -24,7 +24,8 @@ The same line carries:
   weight copies (> 256 MiB, more than the Infinity Cache holds), with its
   own roofline against 8 TB/s and its CPU baseline;
 * ``sweep``: every other BASELINE config (FA2 config 1 and the N sweep,
-  d=128 causal, rel-pos N=1500, qmatmul M=16/256), the fp32-input FA2 and
+  d=128 causal, rel-pos N=1500, qmatmul M=16/256), the GPU rel-pos bias
+  precompute at config 4's shape, the fp32-input FA2 at d=64 and d=128 and
   the reference-format W8A16 at 4096^3, each with its GPU rate, its
   roofline fraction and its CPU baseline.
 
@@ -47,6 +48,7 @@ import sys
 import time
 
 MFMA_F16_PEAK_TFLOPS = 2516.6  # 256 CUs * 2.4 GHz * 4096 dense fp16 FLOP/clk/CU
+MFMA_F32_PEAK_TFLOPS = 157.3   # dense fp32 MFMA
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 METRIC = "FA2 fwd TFLOP/s (d64,N2048) + % MFMA peak; int4 qmatmul HBM GB/s"
 GRAPH_LAUNCHES = 16
@@ -231,6 +233,28 @@ def relpos_workload(neso_amd, torch, I, want_cpu):
     return launch, 4.0 * rc["H"] * rc["N"] ** 2 * rc["d"], "flop", dict(rc), cpu
 
 
+def relpos_precompute_workload(neso_amd, torch, I, want_cpu):
+    """The dense-bias precompute at config 4's shape (H8 T1500 d64): Q_u and
+    the fp16 [H][T][T] bias; FLOP = 2 * H * T^2 * d (one d-long fp32 dot per
+    output element, on v_mfma_f32_32x32x2f32)."""
+    from oracle import attention as A
+    rc = I.RELPOS_CONFIG
+    h, t, d = rc["H"], rc["N"], rc["d"]
+    g = torch.Generator().manual_seed(0)
+    q, kr = torch.randn(h, t, d, generator=g), torch.randn(h, 2 * t - 1, d, generator=g)
+    bu, bv = (torch.randn(h, d, generator=g) * 0.1 for _ in range(2))
+    qd, krd, bud, bvd = (x.cuda() for x in (q, kr, bu, bv))
+    q_u = torch.empty(h, t, d, dtype=torch.float16, device="cuda")
+    rel = torch.empty(h, t, t, dtype=torch.float16, device="cuda")
+    launch = lambda i: neso_amd.rel_pos_precompute(qd, krd, bud, bvd, t, d, h, d ** -0.5, q_u, rel)
+    cpu = None
+    if want_cpu:
+        qn, krn, bun, bvn = (x.numpy() for x in (q, kr, bu, bv))
+        cpu = lambda: A.precompute_bias_and_qu(qn, krn, bun, bvn)
+    cfg = {"H": h, "T": t, "d": d, "bias_bytes": 2 * h * t * t}
+    return launch, 2.0 * h * t * t * d, "flop", cfg, cpu
+
+
 def w4a16_workload(neso_amd, torch, I, M, want_cpu, rotate=ROTATE):
     from oracle import qmatmul as Q
     import numpy as np
@@ -313,7 +337,10 @@ def cases(neso_amd, torch, I, want_cpu):
         "fa2_d128": lambda: fa2_workload(neso_amd, torch, I, 2, 32, 4096, 128, True, want_cpu),
         "fa2_f32_qkv": lambda: fa2_workload(neso_amd, torch, I, 1, 16, 2048, 64, False, want_cpu,
                                             f32=True),
+        "fa2_f32_qkv_d128": lambda: fa2_workload(neso_amd, torch, I, 1, 16, 2048, 128, False,
+                                                 want_cpu, f32=True),
         "relpos": lambda: relpos_workload(neso_amd, torch, I, want_cpu),
+        "relpos_precompute": lambda: relpos_precompute_workload(neso_amd, torch, I, want_cpu),
         "w8a16": lambda: w8a16_workload(neso_amd, torch, False, want_cpu),
         "w8a16_scaled": lambda: w8a16_workload(neso_amd, torch, True, want_cpu),
     }
@@ -328,10 +355,13 @@ def cases(neso_amd, torch, I, want_cpu):
 
 SWEEP_ORDER = ["fa2_config1"] + [f"fa2_n{n}{s}" for n in (128, 256, 512, 1024, 2048)
                                  for s in ("", "_causal")] + [
-    "fa2_d128", "relpos", "fa2_f32_qkv", "w8a16", "w8a16_scaled", "w4a16_m16", "w4a16_m256"]
+    "fa2_d128", "relpos", "relpos_precompute", "fa2_f32_qkv", "fa2_f32_qkv_d128", "w8a16",
+    "w8a16_scaled", "w4a16_m16", "w4a16_m256"]
 KERNEL_OF = {  # device kernel each sweep row's time is dominated by (for readers)
     "fa2_f32_qkv": "fa2_fwd_kernel (F32IN: 3 fp16 MFMAs per product)",
+    "fa2_f32_qkv_d128": "fa2_fwd_kernel (F32IN, 32-key blocks)",
     "relpos": "fa2_fwd_kernel (BIAS = f32 table)",
+    "relpos_precompute": "relpos_precompute_kernel (fp32 MFMA; mfma_f32_frac against 157.3 TFLOP/s)",
     "w8a16": "w8a16_gemm_kernel", "w8a16_scaled": "w8a16_gemm_kernel",
     "w4a16_m16": "w4a16_skinny_lds_kernel", "w4a16_m256": "w4a16_tile_gemm_kernel",
 }
@@ -439,10 +469,13 @@ def main():
             row = run_case(C[name](), sweep_steps, 5, torch, want_cpu)
             row = {"case": name, **({"kernel": KERNEL_OF[name]} if name in KERNEL_OF else {}),
                    **row}
-            if name == "fa2_f32_qkv":
+            if name.startswith("fa2_f32_qkv"):
                 # Three fp16 MFMAs per product: the issued MFMA work is 3x
                 # the useful FLOPs counted in tflops / mfma_frac.
                 row["mfma_frac_issued"] = round(3 * row["mfma_frac"], 4)
+            if name == "relpos_precompute":
+                row["mfma_f32_frac"] = round(row["tflops"] / MFMA_F32_PEAK_TFLOPS, 4)
+                row["gbs_written"] = round(row["bias_bytes"] / (row["us"] * 1e-6) / 1e9, 1)
             if name.startswith("w4a16"):
                 row["mfma_frac"] = round(2.0 * row["M"] * row["N"] * row["K"]
                                          / (row["us"] * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)

@@ -857,14 +857,16 @@ constexpr char kManifest[] = R"JSON({
      "threadgroup_size": "256",
      "num_warps": "4",
      "grid": [
-      "cdiv(T, 32)",
+      "cdiv(T, 128)",
       "nh",
-      "1"
+      "cdiv((T - 1 + (127 if T > 127 else T - 1)) // 32 + 1, 8)"
      ],
      "constants": {
-      "block_m": "32",
+      "block_m": "32 per wave, 128 per workgroup",
       "relative_positions_per_tile": "32",
-      "mfma": "v_mfma_f32_32x32x2f32"
+      "tiles_per_workgroup": "8",
+      "lds_bytes": "256 * D",
+      "mfma": "v_mfma_f32_32x32x16_f16 x3 (fp32 split into fp16 hi + lo: hi.hi + hi.lo + lo.hi)"
      }
     }
    ]

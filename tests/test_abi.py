@@ -127,6 +127,8 @@ PLAN_CASES = [
      dict(N=8192, batch_heads=16)),
     ("neso_rel_pos_precompute", [_P] * 4 + [1500, 64, 8, 0.125, _P, _P], dict(T=1500, nh=8)),
     ("neso_rel_pos_precompute", [_P] * 4 + [33, 128, 3, 0.1, _P, _P], dict(T=33, nh=3)),
+    ("neso_rel_pos_precompute", [_P] * 4 + [10, 32, 2, 0.1, _P, _P], dict(T=10, nh=2)),
+    ("neso_rel_pos_precompute", [_P] * 4 + [4096, 64, 1, 0.1, _P, _P], dict(T=4096, nh=1)),
     # X row stride 2^23: the tiled kernels' 32-bit buffer offsets would
     # overflow, so the fallback kernel is chosen.
     ("neso_w4a16_matmul", [_P] * 4 + [100, 11008, 4096, 1 << 23, 11008, 32, 8],

@@ -47,3 +47,23 @@ def test_serial_build_exports_every_entry_point():
     assert set(_lib.SIGNATURES) <= exported
     lib = _lib.load_variant(_lib.SERIAL_LIB_PATH)
     assert lib.neso_abi_version() == _lib.load().neso_abi_version()
+
+
+def test_build_output_filter_drops_only_expected_warnings():
+    """The M0-clobber warnings of the LDS-DMA asm are counted, not printed
+    (the assembly check above covers them); other diagnostics stay."""
+    text = "\n".join([
+        "In file included from a/fa2_fast.hip:37:",
+        "a/fa2_tiles.h:117:7: warning: inline asm clobber list contains reserved registers: m0"
+        " [-Winline-asm]",
+        "  117 |       \"s_mov_b32 m0, %0\\n\\t\"",
+        "      |       ^",
+        "a/fa2_tiles.h:117:7: note: Reserved registers on the clobber list may not be preserved",
+        "a/qmatmul.hip:10:3: warning: unused variable 'x' [-Wunused-variable]",
+        "   10 |   int x;",
+        "warning: feature flag '-packed-fp32-ops' is not a recognized feature for this target",
+        "2 warnings generated when compiling for gfx950.",
+    ])
+    kept, m0 = B._filter_diagnostics(text)
+    assert m0 == 1
+    assert len(kept) == 1 and "unused variable" in kept[0]

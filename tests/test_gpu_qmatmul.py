@@ -116,6 +116,40 @@ def test_zero_point_codes_give_zero(gpu, m):
         assert torch.count_nonzero(y).item() == 0
 
 
+@pytest.mark.parametrize("amp", [200.0, 1000.0])
+@pytest.mark.parametrize("at_zero", [False, True], ids=["random_codes", "codes_at_zero"])
+@pytest.mark.parametrize("m", [1, 2, 16])
+def test_outlier_activations(gpu, amp, at_zero, m):
+    """A few activation channels of size |x| = amp among N(0, 1) ones, as in
+    LLM hidden states.  The GEMV (M <= 2) accumulates (1024 + c) x and
+    (1024 + 16 c) x in fp32 and subtracts the zero point's share once per
+    chunk, so an outlier's terms reach ~1264 |x| before they cancel.  With
+    the outliers' codes at the zero point the cancellation is exact in real
+    arithmetic and only rounding is left, the worst case for the fold.
+
+    Bars: max|err| / max|ref| <= 2e-3, and per element half an fp16 ulp of
+    max(|ref|, |Y|) plus 2^-20 * sum_g s_g * 1264 * sum_{k in g} |x_k| (the fp32 rounding
+    of at most 16 accumulations per chunk sum, each term at most 1264 |x|).
+    """
+    k, n = 4096, 512
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=int(amp) + m)
+    rs = np.random.RandomState(m)
+    idx = rs.choice(k, 6, replace=False)
+    x[:, idx] = torch.from_numpy(amp * np.sign(rs.randn(m, 6))).half()
+    codes = codes.numpy()
+    if at_zero:
+        codes[:, idx] = 8
+    words = Q.pack_int4(codes)
+    y = gpu_w4(x, words, scales).double().numpy()
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy(), dtype=np.float64)
+    assert Q.rel_err(y, ref) <= 2e-3
+    ax = np.abs(x.double().numpy()).reshape(m, k // 32, 32).sum(-1)  # [M][groups]
+    fold = 2.0 ** -20 * 1264 * ax @ scales.double().numpy().T      # [M][N]
+    top = np.maximum(np.maximum(np.abs(ref), np.abs(y)), 2.0 ** -14)
+    half_ulp = np.exp2(np.floor(np.log2(top)) - 11)
+    assert (np.abs(y - ref) <= half_ulp + fold).all(), np.abs(y - ref).max()
+
+
 def test_strided_output(gpu):
     m, n, k = 3, 200, 512
     x, codes, scales = I.qmatmul_inputs(m, k, n, seed=9)
