@@ -48,7 +48,6 @@ import sys
 import time
 
 MFMA_F16_PEAK_TFLOPS = 2516.6  # 256 CUs * 2.4 GHz * 4096 dense fp16 FLOP/clk/CU
-MFMA_F32_PEAK_TFLOPS = 157.3   # dense fp32 MFMA
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 METRIC = "FA2 fwd TFLOP/s (d64,N2048) + % MFMA peak; int4 qmatmul HBM GB/s"
 GRAPH_LAUNCHES = 16
@@ -235,8 +234,9 @@ def relpos_workload(neso_amd, torch, I, want_cpu):
 
 def relpos_precompute_workload(neso_amd, torch, I, want_cpu):
     """The dense-bias precompute at config 4's shape (H8 T1500 d64): Q_u and
-    the fp16 [H][T][T] bias; FLOP = 2 * H * T^2 * d (one d-long fp32 dot per
-    output element, on v_mfma_f32_32x32x2f32)."""
+    the fp16 [H][T][T] bias.  FLOP = 2 * H * T^2 * d (one d-long dot per
+    output element); bytes = fp32 Q, K_rel, biases in + fp16 Q_u and bias
+    out, 46.6 MB, which bound it (5.8 us at 8 TB/s)."""
     from oracle import attention as A
     rc = I.RELPOS_CONFIG
     h, t, d = rc["H"], rc["N"], rc["d"]
@@ -251,7 +251,8 @@ def relpos_precompute_workload(neso_amd, torch, I, want_cpu):
     if want_cpu:
         qn, krn, bun, bvn = (x.numpy() for x in (q, kr, bu, bv))
         cpu = lambda: A.precompute_bias_and_qu(qn, krn, bun, bvn)
-    cfg = {"H": h, "T": t, "d": d, "bias_bytes": 2 * h * t * t}
+    nbytes = 4 * h * t * d + 4 * h * (2 * t - 1) * d + 8 * h * d + 2 * h * t * d + 2 * h * t * t
+    cfg = {"H": h, "T": t, "d": d, "algorithmic_bytes": nbytes}
     return launch, 2.0 * h * t * t * d, "flop", cfg, cpu
 
 
@@ -361,7 +362,7 @@ KERNEL_OF = {  # device kernel each sweep row's time is dominated by (for reader
     "fa2_f32_qkv": "fa2_fwd_kernel (F32IN: 3 fp16 MFMAs per product)",
     "fa2_f32_qkv_d128": "fa2_fwd_kernel (F32IN, 32-key blocks)",
     "relpos": "fa2_fwd_kernel (BIAS = f32 table)",
-    "relpos_precompute": "relpos_precompute_kernel (fp32 MFMA; mfma_f32_frac against 157.3 TFLOP/s)",
+    "relpos_precompute": "relpos_precompute_kernel (fp16 hi/lo MFMA; HBM-bound, hbm_frac)",
     "w8a16": "w8a16_gemm_kernel", "w8a16_scaled": "w8a16_gemm_kernel",
     "w4a16_m16": "w4a16_skinny_lds_kernel", "w4a16_m256": "w4a16_tile_gemm_kernel",
 }
@@ -474,8 +475,9 @@ def main():
                 # the useful FLOPs counted in tflops / mfma_frac.
                 row["mfma_frac_issued"] = round(3 * row["mfma_frac"], 4)
             if name == "relpos_precompute":
-                row["mfma_f32_frac"] = round(row["tflops"] / MFMA_F32_PEAK_TFLOPS, 4)
-                row["gbs_written"] = round(row["bias_bytes"] / (row["us"] * 1e-6) / 1e9, 1)
+                # HBM-bound: fp32 inputs in, fp16 Q_u and the T x T bias out.
+                row["gbs"] = round(row["algorithmic_bytes"] / (row["us"] * 1e-6) / 1e9, 1)
+                row["hbm_frac"] = round(row["gbs"] / HBM_PEAK_GBS, 4)
             if name.startswith("w4a16"):
                 row["mfma_frac"] = round(2.0 * row["M"] * row["N"] * row["K"]
                                          / (row["us"] * 1e-6) / 1e12 / MFMA_F16_PEAK_TFLOPS, 4)
