@@ -75,9 +75,12 @@ __device__ __forceinline__ void serial_lds_point() {
 }
 
 // PAIR (causal only): each workgroup takes two query blocks, see below.
-template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT, bool PAIR = false>
+// HALVES (full causal only): each workgroup takes two 64-row query blocks
+// from opposite ends, see below.
+template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT, bool PAIR = false, bool HALVES = false>
 __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   static_assert(!PAIR || CAUSAL, "paired query blocks are for causal grids");
+  static_assert(!HALVES || (CAUSAL && !PAIR), "64-row halves are for full causal grids");
   constexpr int kKB = fast_kb<D>();  // keys per block
   constexpr int NT = kKB / 32;  // 32-key tiles per block
   constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
@@ -101,17 +104,37 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 
   // Workgroup x of head bh takes query block nqb - 1 - x (causal: longest
   // rows first) or x.  With PAIR it then also takes block x, so that every
-  // workgroup does the work of nqb + 1 blocks' rows.
+  // workgroup does the work of nqb + 1 blocks' rows.  With HALVES it takes
+  // the 64-row blocks x and n64 - 1 - x (n64 = 64-row blocks of N): every
+  // workgroup sees about N + 64 keys in total over its 128 rows, half the
+  // work of an unmasked block, so causal grids of one workgroup per CU finish
+  // in about half the time instead of waiting for the longest block.
   const uint32_t wg = xcd_swizzle(blockIdx.x, gridDim.x);
   const int nqb = p.num_qblocks;
-  const int wph = PAIR ? (nqb + 1) / 2 : nqb;  // workgroups per head
+  const int n64 = (p.N + 63) / 64;
+  const int wph = PAIR ? (nqb + 1) / 2 : HALVES ? (n64 + 1) / 2 : nqb;  // workgroups per head
   const int bh = wg / wph;
   const int x = wg % wph;
 
   auto run = [&](const int qblk) {
   const int N = p.N;
-  const int q0 = qblk * kBM;
-  const int qw0 = q0 + wave * 32;
+  // This wave's 32 query rows start at qw0.  With HALVES, query slice sl of
+  // the workgroup's 128 rows is rows 32 (sl % 2) .. of the short block (sl <
+  // 2) or of the long block (sl >= 2); with two key groups the second group's
+  // waves take the slices two apart (sl = wave ^ 2), so that each SIMD,
+  // which holds wave w of both groups, runs one short-block and one
+  // long-block wave.  A middle block paired with itself leaves the long
+  // half empty (qw0 = N: no rows).
+  int q0, qw0, sl = wave;
+  if constexpr (HALVES) {
+    if (KSPLIT == 2) sl = wave ^ (2 * kg);
+    const int hs = qblk, hl = n64 - 1 - qblk;
+    q0 = hs * 64;
+    qw0 = sl < 2 ? hs * 64 + 32 * sl : (hl == hs ? N : hl * 64 + 32 * (sl - 2));
+  } else {
+    q0 = qblk * kBM;
+    qw0 = q0 + wave * 32;
+  }
   const int q = qw0 + ql;
 
   const half_t* Qh = static_cast<const half_t*>(p.Q) + (int64_t)bh * p.bh_stride_q;
@@ -123,12 +146,15 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // Rows past N read as zeros.
   const bool neg = p.scale_log2 < 0.f;
   const float c = fmaxf(fabsf(p.scale_log2), 1.17549435e-38f);
-  const int qrows = min(N - q0, kBM);
-  const rsrc_t rsQ = make_rsrc(Qh + (int64_t)q0 * p.stride_q, (uint32_t)qrows * p.stride_q * 2);
+  // Rows addressed from qb: the workgroup's first row, or with HALVES the
+  // wave's own (its two halves are not contiguous).
+  const int qb = HALVES ? qw0 : q0;
+  const int qrows = HALVES ? max(0, min(N - qw0, 32)) : min(N - q0, kBM);
+  const rsrc_t rsQ = make_rsrc(Qh + (int64_t)qb * p.stride_q, (uint32_t)qrows * p.stride_q * 2);
   half8v qf[KS];
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
-    const half8v t = buf_load_half8(rsQ, ((q - q0) * p.stride_q + 16 * ks + 8 * g) * 2);
+    const half8v t = buf_load_half8(rsQ, ((q - qb) * p.stride_q + 16 * ks + 8 * g) * 2);
     qf[ks] = neg ? -t : t;
   }
 
@@ -136,12 +162,22 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // blk0 + kg + KSPLIT*i.  Masked kernels visit the keys of their queries'
   // windows [q - wl, q + wr] only.
   const int wl = p.win_left, wr = p.win_right;
+  // With HALVES (full causal, wr = 0) the keys run from 0 to the end of the
+  // long block, and each wave stops after the last block any of its rows
+  // sees: its first my_nw of the group's my_n blocks (the group's loads go
+  // on to my_n).
   const int kbeg = CAUSAL ? max(0, q0 - wl) : 0;
-  const int kend = CAUSAL ? (int)min((int64_t)N, (int64_t)q0 + kBM + wr) : N;
+  const int kend = HALVES ? min(N, (n64 - q0 / 64) * 64 + wr)
+                 : CAUSAL ? (int)min((int64_t)N, (int64_t)q0 + kBM + wr) : N;
   const int blk0 = kbeg / kKB;
   const int nblk = max(0, (kend + kKB - 1) / kKB - blk0);
   const int my_n = nblk > kg ? (nblk - kg + KSPLIT - 1) / KSPLIT : 0;
   const int iters = (nblk + KSPLIT - 1) / KSPLIT;  // uniform over the workgroup
+  int my_nw = my_n;
+  if constexpr (HALVES) {
+    const int last = qw0 >= N ? -1 : min(N - 1, qw0 + 31 + wr) / kKB - blk0 - kg;
+    my_nw = last < 0 ? 0 : min(my_n, last / KSPLIT + 1);
+  }
 
   half_t* gbase = &smem[kg * GLDS];
   auto kslot = [&](int s) { return gbase + s * (KSLOT + VSLOT); };
@@ -392,10 +428,21 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     // between key groups), so the loads are issued outside the branch.
     if (i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
     serial_lds_point();
-    if (i < my_n) {
+    if constexpr (HALVES) {
+      if (i == my_nw && i < my_n) pv_only(pprev, vslot((i - 1) & 3));
+    }
+    if (i < (HALVES ? my_nw : my_n)) {
 #else
-    if (i < my_n) {
-      if (i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
+    if constexpr (HALVES) {
+      // The group's loads go on past this wave's last block; the P V of
+      // that block comes in the step after it (later loads reuse its slot).
+      if (i < my_n) {
+        if (i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
+        if (i == my_nw) pv_only(pprev, vslot((i - 1) & 3));
+      }
+    }
+    if (i < (HALVES ? my_nw : my_n)) {
+      if (!HALVES && i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
 #endif
       const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
       // Some key of the block is past N or outside some query's window.
@@ -431,7 +478,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   if (my_n > 2) lds_load(2, 2);
   serial_lds_point();
   qk(sa, kslot(0));
-  if (my_n > 0) {
+  if (HALVES ? my_nw > 0 : my_n > 0) {
     const int kb0 = (blk0 + kg) * kKB;
     const bool masked =
         (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
@@ -448,8 +495,9 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     body(i + 1, sa, sb, pa, pb2);
   }
   // P V of the group's last block.  Step j writes block j's P into pb2
-  // when j is even, into pa when j is odd.
-  if (my_n > 0) {
+  // when j is even, into pa when j is odd.  (A HALVES wave that stopped
+  // before the group's last block has done its last P V in the loop.)
+  if (HALVES ? my_nw > 0 && my_nw == my_n : my_n > 0) {
     if ((my_n - 1) & 1)
       pv_only(pa, vslot((my_n - 1) & 3));
     else
@@ -468,8 +516,8 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     constexpr int SLOTS = 16 * (DT / 2) + 2;
     static_assert(sizeof(smem) >= 8 * SLOTS * 64 * sizeof(float), "merge buffer");
     float* const red = reinterpret_cast<float*>(smem) + lane;
-    float* mine = red + (size_t)(4 * kg + wave) * SLOTS * 64;
-    const float* other = red + (size_t)(4 * (1 - kg) + wave) * SLOTS * 64;
+    float* mine = red + (size_t)(4 * kg + sl) * SLOTS * 64;
+    const float* other = red + (size_t)(4 * (1 - kg) + sl) * SLOTS * 64;
     mine[0] = m_run;
     mine[64] = l_run;
 #pragma unroll
@@ -535,7 +583,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   const float inv = 1.f / fmaxf(l_tot, 1e-6f);
   constexpr int ES = OUT_F16 ? 2 : 4;
   const rsrc_t rsO = make_rsrc(static_cast<char*>(p.O) +
-                                   ((int64_t)bh * p.bh_stride_o + (int64_t)q0 * p.stride_o) * ES,
+                                   ((int64_t)bh * p.bh_stride_o + (int64_t)qb * p.stride_o) * ES,
                                (uint32_t)qrows * p.stride_o * ES);
 #pragma unroll
   for (int u = 0; u < DT; ++u) {
@@ -543,7 +591,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const int col = 32 * u + 8 * b + 4 * g;
-      const uint32_t off = ((q - q0) * p.stride_o + col) * ES;
+      const uint32_t off = ((q - qb) * p.stride_o + col) * ES;
       float4v v = {o[u][4 * b] * inv, o[u][4 * b + 1] * inv, o[u][4 * b + 2] * inv,
                    o[u][4 * b + 3] * inv};
       if (OUT_F16) {
@@ -563,6 +611,8 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       if (pass) lds_barrier();  // the merge before read partials that this block's loads overwrite
       run(pass ? x : nqb - 1 - x);
     }
+  } else if constexpr (HALVES) {
+    run(x);
   } else {
     run(CAUSAL ? nqb - 1 - x : x);
   }
@@ -573,15 +623,21 @@ template <int D, bool CAUSAL, bool OUT_F16, int K>
 bool launch_fast_k(const Fa2Args& a, hipStream_t stream, hipError_t& err) {
   if constexpr (K * fast_group_lds_halves<D>() * 2 <= 160 * 1024) {
     if constexpr (CAUSAL) {
-      if (a.pair_qblocks) {
+      if (a.pair_qblocks == 1) {
         err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, true>>(
-            ktag("fa2_fast_kernel", D, true, OUT_F16, K, true),
+            ktag("fa2_fast_kernel", D, true, OUT_F16, K, true, false),
             dim3((a.num_qblocks + 1) / 2 * a.batch_heads), dim3(K * kGroup), stream, a);
+        return true;
+      }
+      if (a.pair_qblocks == 2) {
+        err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, false, true>>(
+            ktag("fa2_fast_kernel", D, true, OUT_F16, K, false, true),
+            dim3(((a.N + 63) / 64 + 1) / 2 * a.batch_heads), dim3(K * kGroup), stream, a);
         return true;
       }
     }
     err = launch<&fa2_fast_kernel<D, CAUSAL, OUT_F16, K>>(
-        ktag("fa2_fast_kernel", D, CAUSAL, OUT_F16, K, false),
+        ktag("fa2_fast_kernel", D, CAUSAL, OUT_F16, K, false, false),
         dim3(a.num_qblocks * a.batch_heads), dim3(K * kGroup), stream, a);
     return true;
   }
@@ -644,8 +700,11 @@ hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, i
   return hipErrorInvalidValue;
 #endif
   a.num_qblocks = (a.N + kBM - 1) / kBM;
-  // Paired query blocks (causal kernels only; any window is correct).
-  a.pair_qblocks = (causal && a.pair_qblocks == 1) ? 1 : 0;
+  // Paired query blocks (causal kernels only; any window is correct);
+  // 64-row halves only without a window (the two halves' key ranges must
+  // both start at key 0).
+  const bool full_causal = causal && a.win_left >= a.N && a.win_right == 0;
+  a.pair_qblocks = (causal && a.pair_qblocks == 1) ? 1 : (full_causal && a.pair_qblocks == 2) ? 2 : 0;
   return out_f16 ? launch_fast_d<true>(a, head_dim, causal, ksplit, stream)
                  : launch_fast_d<false>(a, head_dim, causal, ksplit, stream);
 }

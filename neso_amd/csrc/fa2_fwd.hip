@@ -600,8 +600,10 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
     // d128 B2 H32 N4096 356.6 -> 331.6 us, d64 B1 H32 N4096 102.3 -> 92.1
     // us, d64 B1 H16 N4096 51.7 -> 49.4 us; at 256 workgroups pairing
     // would idle half the CUs).  NESO_AMD_FA2_PAIR = 0 / 1 forces it.
+    // Below that, without a window: 64-row halves from opposite ends of the
+    // rows, which halve the longest workgroup's work at one workgroup per CU.
     if (a.pair_qblocks < 0)
-      a.pair_qblocks = (full_causal && wgs >= 2 * cus) ? 1 : 0;
+      a.pair_qblocks = (full_causal && wgs >= 2 * cus) ? 1 : full_causal ? 2 : 0;
     if (causal && a.pair_qblocks == 1 && a.ksplit <= 0) {
       const int64_t pwgs = (int64_t)((a.num_qblocks + 1) / 2) * a.batch_heads;
       ksplit = pwgs < 2 * cus ? 2 : 1;

@@ -128,13 +128,14 @@ constexpr char kManifest[] = R"JSON({
       "CAUSAL",
       "OUT_F16",
       "KSPLIT",
-      "PAIR"
+      "PAIR",
+      "HALVES"
      ],
-     "when": "fp16 Q/K/V without a bias at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred); KSPLIT key groups of 4 waves; PAIR (causal grids of >= 2 workgroups per CU): each workgroup takes query blocks x and nqb-1-x",
+     "when": "fp16 Q/K/V without a bias at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred); KSPLIT key groups of 4 waves; PAIR (causal grids of >= 2 workgroups per CU): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "256 * KSPLIT",
      "num_warps": "4 * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 128) * batch_heads",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 128) * batch_heads)",
       "1",
       "1"
      ],
@@ -402,13 +403,14 @@ constexpr char kManifest[] = R"JSON({
       "CAUSAL",
       "OUT_F16",
       "KSPLIT",
-      "PAIR"
+      "PAIR",
+      "HALVES"
      ],
-     "when": "fp16 Q/K/V without a bias at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred); KSPLIT key groups of 4 waves; PAIR (causal grids of >= 2 workgroups per CU): each workgroup takes query blocks x and nqb-1-x",
+     "when": "fp16 Q/K/V without a bias at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred); KSPLIT key groups of 4 waves; PAIR (causal grids of >= 2 workgroups per CU): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "256 * KSPLIT",
      "num_warps": "4 * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 128) * batch_heads",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 128) * batch_heads)",
       "1",
       "1"
      ],
@@ -565,13 +567,14 @@ constexpr char kManifest[] = R"JSON({
       "CAUSAL",
       "OUT_F16",
       "KSPLIT",
-      "PAIR"
+      "PAIR",
+      "HALVES"
      ],
-     "when": "fp16 Q/K/V without a bias at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred); KSPLIT key groups of 4 waves; PAIR (causal grids of >= 2 workgroups per CU): each workgroup takes query blocks x and nqb-1-x",
+     "when": "fp16 Q/K/V without a bias at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred); KSPLIT key groups of 4 waves; PAIR (causal grids of >= 2 workgroups per CU): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "256 * KSPLIT",
      "num_warps": "4 * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 128) * batch_heads",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 128) * batch_heads)",
       "1",
       "1"
      ],

@@ -68,13 +68,14 @@ int env_qwaves() {
   return (k == 2 || k == 4) ? k : 0;
 }
 
-// Paired query blocks for causal calls on the generic FA2 kernel:
-// NESO_AMD_FA2_PAIR=1 forces them, 0 forbids them; unset lets the launcher
-// choose.
+// Causal work balancing on the fast FA2 kernel: NESO_AMD_FA2_PAIR=1 forces
+// paired 128-row query blocks, 2 forces paired 64-row halves (no window
+// only), 0 forbids both; unset lets the launcher choose.
 int env_pair() {
   const char* v = getenv("NESO_AMD_FA2_PAIR");
   if (!v) return -1;
-  return atoi(v) ? 1 : 0;
+  const int k = atoi(v);
+  return (k == 1 || k == 2) ? k : 0;
 }
 
 int check_head_dim(int32_t d) {

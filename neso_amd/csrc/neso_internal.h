@@ -41,8 +41,9 @@ struct Fa2Args {
   // Query waves per key group of the generic kernel (its query block is 32
   // rows per wave): 4 or 2; 0 = chosen from the grid size.
   int32_t qwaves;
-  // Causal generic kernel: each workgroup takes query blocks nqb-1-x and x
-  // (filled in by launch_fa2; NESO_AMD_FA2_PAIR forces it).
+  // Causal fast kernel: 1 = each workgroup takes query blocks nqb-1-x and
+  // x; 2 = it takes the 64-row blocks x and n64-1-x (no window); 0 = one
+  // block (filled in by launch_fa2; NESO_AMD_FA2_PAIR forces it).
   int32_t pair_qblocks;
 };
 

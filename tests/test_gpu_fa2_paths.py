@@ -134,10 +134,50 @@ def test_fast_paired_causal_blocks(gpu, monkeypatch, ksplit, d, n):
     check(q, k, v, causal=True)
 
 
-@pytest.mark.parametrize("n,wl,wr", [(300, 100, 37), (1500, 128, 128), (1000, 1000, 0)])
-def test_fast_paired_windows(gpu, monkeypatch, n, wl, wr):
+@pytest.mark.parametrize("ksplit", [1, 2, 3])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("n", [1, 63, 64, 65, 129, 191, 384, 1000, 1500, 2048])
+def test_fast_causal_halves(gpu, monkeypatch, ksplit, d, n):
+    """Fast kernel, causal, 64-row halves: workgroup x takes the 64-row
+    blocks x and n64-1-x (an odd middle block alone), each wave stops after
+    its last visible block, and with two key groups the second group's
+    waves take the slices two apart."""
     monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
-    monkeypatch.setenv("NESO_AMD_FA2_PAIR", "1")
+    monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
+    monkeypatch.setenv("NESO_AMD_FA2_PAIR", "2")
+    q, k, v = I.fa2_inputs(1, 3, n, d, seed=n + d + 7 * ksplit)
+    check(q, k, v, causal=True)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_fast_causal_halves_rescale_and_f16(gpu, monkeypatch, d):
+    """Halves with logits that jump between blocks (the slow path, per wave)
+    and with fp16 output."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_PAIR", "2")
+    q, k, v = I.fa2_inputs(1, 2, 1000, d, seed=d)
+    k = k.float()
+    for blk, f in enumerate([0.5, 3.0, 9.0, 1.0, 12.0, 2.0, 6.0, 0.25] * 2):
+        k[:, :, 64 * blk:64 * blk + 64] *= f
+    k = k.half()
+    check(q, k, v, causal=True)
+    # fp16 output through the window entry with (N, 0): full causal, so the
+    # halves apply there too.
+    n, dev = q.shape[-2], torch.device("cuda:0")
+    qs, ks, vs = (t[0].permute(1, 0, 2).contiguous().to(dev) for t in (q, k, v))
+    out = neso_amd.window_attention(qs, ks, vs, n, 0, out_dtype=torch.float16)
+    out = out.float().cpu().permute(1, 0, 2)
+    ref = A.attention(q[0], k[0], v[0], 1 / math.sqrt(d), causal=True)
+    assert ((out - ref).abs() <= TOL + ref.abs() * 2.0 ** -11).all()
+
+
+@pytest.mark.parametrize("n,wl,wr", [(300, 100, 37), (1500, 128, 128), (1000, 1000, 0)])
+@pytest.mark.parametrize("pair", ["1", "2"])
+def test_fast_paired_windows(gpu, monkeypatch, n, wl, wr, pair):
+    """Windows with pairing forced: 64-row halves (2) apply only without a
+    window, so a windowed call falls back to whole blocks."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_PAIR", pair)
     heads, d = 2, 64
     q, k, v = (t[0].permute(1, 0, 2).contiguous() for t in I.fa2_inputs(1, heads, n, d, seed=n))
     dev = torch.device("cuda:0")
