@@ -65,3 +65,4 @@ def test_planted_row_range_mistake_fails():
     128 rows (a plausible slip from the one-block-per-workgroup layout)
     leaves the later blocks' far positions unwritten."""
     assert not (_walk(300, rows_used=lambda i0, T: min(i0 + 31, T - 1)) == 1).all()
+
