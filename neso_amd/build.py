@@ -22,6 +22,8 @@ CSRC = PKG / "csrc"
 BUILD_DIR = PKG / "_build"
 LIB_PATH = PKG / "libneso_amd.so"
 SERIAL_LIB_PATH = PKG / "libneso_amd_serial.so"
+HARNESS_SRC = PKG / "harness" / "neso_harness.cpp"
+HARNESS_PATH = PKG / "neso_harness"
 ARCH = "gfx950"
 
 SOURCES = ["neso_abi.hip", "fa2_fwd.hip", "fa2_fast.hip", "relpos_pre.hip", "qmatmul.hip",
@@ -226,7 +228,23 @@ def build(extra_flags: list[str] | None = None, jobs: int | None = None) -> Path
     _link(objs, LIB_PATH)
     _link([serial_obj if s == "fa2_fast.hip" else o for s, o in zip(SOURCES, objs)],
           SERIAL_LIB_PATH)
+    build_harness()
     return LIB_PATH
+
+
+def build_harness() -> Path:
+    """The native C++ harness (known answers and a timing sweep through the
+    C ABI, no Python), linked against the library beside it."""
+    cmd = [hipcc(), "-O2", "-std=c++17", "-Wall", f"-I{PKG.parent / 'include'}",
+           str(HARNESS_SRC), f"-L{PKG}", "-lneso_amd", "-Wl,-rpath,$ORIGIN",
+           "-o", str(HARNESS_PATH)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"harness build failed:\n{' '.join(cmd)}\n{res.stdout}{res.stderr}")
+    kept, _ = _filter_diagnostics(res.stdout + res.stderr)
+    if kept:
+        sys.stderr.write("\n".join(kept) + "\n")
+    return HARNESS_PATH
 
 
 if __name__ == "__main__":

@@ -67,3 +67,13 @@ def test_build_output_filter_drops_only_expected_warnings():
     kept, m0 = B._filter_diagnostics(text)
     assert m0 == 1
     assert len(kept) == 1 and "unused variable" in kept[0]
+
+
+def test_harness_usage_without_gpu():
+    """The native harness loads the library and answers usage errors
+    without touching a GPU (exit status 2)."""
+    import pytest
+    if not B.HARNESS_PATH.exists():
+        pytest.skip("neso_harness not built")
+    r = subprocess.run([str(B.HARNESS_PATH)], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "usage" in r.stderr
