@@ -91,11 +91,14 @@ __device__ __forceinline__ void lds_barrier() {
 // Workgroup index remapped so that consecutive logical indices land on the
 // same XCD.  The hardware dispatcher deals workgroups round-robin over the
 // 8 XCDs (workgroup i runs on XCD i % 8); each XCD has its own L2, so
-// workgroups that share K/V (or weight) tiles should share an XCD.
+// workgroups that share K/V (or weight) tiles should share an XCD.  XCD x
+// takes the contiguous logical range of its total / 8 workgroups, one more
+// for the first total % 8 XCDs: a bijection of [0, total) for any total.
 __device__ __forceinline__ uint32_t xcd_swizzle(uint32_t hw_id, uint32_t total) {
   constexpr uint32_t kXcds = 8;
-  if (total % kXcds != 0) return hw_id;
-  return (hw_id % kXcds) * (total / kXcds) + hw_id / kXcds;
+  const uint32_t q = total / kXcds, r = total % kXcds;
+  const uint32_t x = hw_id % kXcds, local = hw_id / kXcds;
+  return x < r ? x * (q + 1) + local : r * (q + 1) + (x - r) * q + local;
 }
 
 }  // namespace neso

@@ -840,7 +840,17 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 31, lh = lane >> 5;
-  const int m0 = blockIdx.y * kW8BM, n0 = blockIdx.x * kW8BN;
+  // Tile order: the dispatch index is remapped so that each XCD takes a
+  // contiguous run of logical tiles, and logical tiles go down groups of
+  // four m-tiles before moving to the next n-tile.  The ~32 workgroups an
+  // XCD runs at once then cover a 4 x 8 block of tiles, whose A rows and B
+  // columns its L2 serves to all of them.
+  const int mt = (int)gridDim.y, nt = (int)gridDim.x;
+  const int lid = (int)xcd_swizzle(blockIdx.y * gridDim.x + blockIdx.x, (uint32_t)(mt * nt));
+  constexpr int kGroupM = 4;
+  const int grp = lid / (kGroupM * nt), first = grp * kGroupM;
+  const int gm = min(mt - first, kGroupM), in = lid % (kGroupM * nt);
+  const int m0 = (first + in % gm) * kW8BM, n0 = (in / gm) * kW8BN;
   const int mrows = min(kW8BM, a.M - m0);
   constexpr uint32_t kOut = 0x80000000u;
   const rsrc_t ra = make_rsrc(a.A + (int64_t)m0 * a.lda, (uint32_t)((mrows - 1) * a.lda + a.K) * 2u);
