@@ -64,9 +64,15 @@ __global__ __launch_bounds__(256) void relpos_precompute_kernel(RelPreArgs a) {
   // [slot][hi, lo][32 rows x CH chunks]: 256 D bytes.
   __shared__ half8v stage[2][2][32 * CH];
 
-  const int h = blockIdx.y;
+  // (row group, head, tile group) from the dispatch index, remapped so that
+  // each XCD takes a contiguous run in (head, row group, tile group) order:
+  // the workgroups of one head, which read overlapping K_rel rows, share an
+  // XCD and its L2.
+  const uint32_t gx = gridDim.x, gy = gridDim.y, gz = gridDim.z;
+  const uint32_t lid = xcd_swizzle(blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z), gx * gy * gz);
+  const int bz = (int)(lid % gz), bx = (int)(lid / gz % gx), h = (int)(lid / (gz * gx));
   const int T = a.T;
-  const int i0 = blockIdx.x * kPreRows;
+  const int i0 = bx * kPreRows;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int row = lane & 31, g = lane >> 5;
@@ -80,7 +86,7 @@ __global__ __launch_bounds__(256) void relpos_precompute_kernel(RelPreArgs a) {
   {
     constexpr int P4 = D / 4;
     half_t* Qu = a.Q_u + (int64_t)h * T * D;
-    for (int e = blockIdx.z * 256 + tid; e < kPreRows * P4; e += 256 * gridDim.z) {
+    for (int e = bz * 256 + tid; e < kPreRows * P4; e += 256 * (int)gz) {
       const int i = i0 + e / P4, f = 4 * (e % P4);
       if (i < T) {
         const float4v x = *reinterpret_cast<const float4v*>(Qh + (int64_t)i * D + f);
@@ -98,7 +104,7 @@ __global__ __launch_bounds__(256) void relpos_precompute_kernel(RelPreArgs a) {
   const int ilast = min(i0 + kPreRows - 1, T - 1);
   const int rlo = T - 1 - ilast;
   const int ntiles = (2 * T - 2 - i0 - rlo) / 32 + 1;
-  const int t0 = blockIdx.z * kPreTilesPerGroup;
+  const int t0 = bz * kPreTilesPerGroup;
   const int t1 = min(ntiles, t0 + kPreTilesPerGroup);
   if (t0 >= t1) return;
 
