@@ -172,6 +172,28 @@ def cpu_time(fn, reps=None):
     return statistics.median(ts)
 
 
+def box_peak():
+    """Dense fp16 MFMA peak of this box from rocminfo: compute units x max
+    engine clock x 4096 FLOP/clk/CU (CDNA4), next to the spec-sheet peak.
+    None when rocminfo is unavailable."""
+    import re
+    import subprocess
+    try:
+        out = subprocess.run(["rocminfo"], capture_output=True, text=True, timeout=60).stdout
+    except (OSError, subprocess.SubprocessError):
+        return None
+    for agent in out.split("Agent ")[1:]:
+        if "gfx950" not in agent:
+            continue
+        cu = re.search(r"Compute Unit:\s+(\d+)", agent)
+        mhz = re.search(r"Max Clock Freq\. \(MHz\):\s+(\d+)", agent)
+        if cu and mhz:
+            cus, clk = int(cu.group(1)), int(mhz.group(1))
+            return {"compute_units": cus, "max_clock_mhz": clk,
+                    "tflops": round(cus * clk * 1e6 * 4096 / 1e12, 1)}
+    return None
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -376,6 +398,8 @@ def main():
         print(json.dumps({"error": "this build runs on exactly one GPU (one process, one "
                                    "device); --gpus must be 1", "n_gpus": args.gpus}))
         return 2
+    # rocminfo runs as a child process before this process touches the GPU.
+    peak_box = None if (args.case or args.calibrate_copy) else box_peak()
     import torch
 
     import neso_amd
@@ -427,8 +451,9 @@ def main():
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("fa2_headline"),
-                     "kernel": "fa2_fast_kernel<64,false,false,2,false>",
-                     "algorithmic_flop_per_launch": flop},
+                     "kernel": "fa2_fast_kernel<64,false,false,2,false,false>",
+                     "algorithmic_flop_per_launch": flop,
+                     "peak_box": peak_box},
     }
     if want_cpu:
         result["cpu_baseline"] = {
