@@ -41,25 +41,34 @@ namespace neso {
 
 namespace {
 
-constexpr int kBM = 128;          // queries per workgroup
-constexpr int kGroup = 256;       // threads per key group (4 waves)
 constexpr float kPSumMax = 4096.f;  // fast-path bound on a lane's block sum of P
+constexpr float kLog2e = 1.4426950408889634f;
 
-// Keys per block: 64 for head_dim 64, 32 for head_dim 128.  Either way a
-// block step carries 16 MFMAs per wave (8 for its scores, 8 for its P V)
-// and a K + V slot is 16 KiB, so two key groups of four slots fit in LDS.
-template <int D>
+// Keys per block.  64 for head_dim 64 with four query waves: a block step
+// then carries 16 MFMAs per wave (8 for its scores, 8 for its P V) and a
+// K + V slot is 16 KiB, so two key groups of four slots fit in LDS.  32 for
+// head_dim 128 (16 MFMAs, 16 KiB), and for two query waves or a bias table
+// at head_dim 64 (8 MFMAs, 8 KiB): two query waves run four key groups,
+// and the bias band of a 32-key block is 63 entries, one per lane.
+template <int D, int QW, bool BIAS>
 constexpr int fast_kb() {
-  return D == 128 ? 32 : 64;
+  return (D == 128 || QW == 2 || BIAS) ? 32 : 64;
 }
 
 // LDS halves of one key group: a 4-slot ring, each slot K [KB][D] then
 // V [KB][D], both row-major with 16-byte chunks swizzled (no padding: the
 // blocks arrive by LDS-direct loads, which fill LDS linearly).
 constexpr int kSlots = 4;
-template <int D>
+template <int D, int QW, bool BIAS>
 constexpr int fast_group_lds_halves() {
-  return kSlots * 2 * fast_kb<D>() * D;
+  return kSlots * 2 * fast_kb<D, QW, BIAS>() * D;
+}
+
+// Bytes of LDS of one workgroup: the key groups' rings, and with a bias
+// two 64-entry band slots per wave.
+template <int D, int QW, bool BIAS>
+constexpr int fast_lds_bytes(int ksplit) {
+  return ksplit * (fast_group_lds_halves<D, QW, BIAS>() * 2 + (BIAS ? QW * 2 * 64 * 4 : 0));
 }
 
 // Debug build (NESO_FA2_SERIAL_LDS): every LDS phase ends in a full wait and
@@ -77,28 +86,43 @@ __device__ __forceinline__ void serial_lds_point() {
 // PAIR (causal only): each workgroup takes two query blocks, see below.
 // HALVES (full causal only): each workgroup takes two 64-row query blocks
 // from opposite ends, see below.
-template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT, bool PAIR = false, bool HALVES = false>
-__global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
+// QW: query waves per key group (4: 128-query workgroups, 2: 64-query
+// workgroups, which double a small grid).
+// BIAS (unmasked only): logits = Q K^T * scale + table[h][i - j + N - 1]
+// (the f32 table of the relative-position entry point).  The table entries
+// enter as the initial accumulator of the score MFMAs, in score units
+// (t / |scale|), so that c * s is the biased logit in log2 units and the
+// softmax is the unbiased one.
+template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT, bool PAIR = false, bool HALVES = false,
+          int QW = 4, bool BIAS = false>
+__global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   static_assert(!PAIR || CAUSAL, "paired query blocks are for causal grids");
   static_assert(!HALVES || (CAUSAL && !PAIR), "64-row halves are for full causal grids");
-  constexpr int kKB = fast_kb<D>();  // keys per block
+  static_assert(QW == 4 || (QW == 2 && !PAIR && !HALVES), "query waves");
+  static_assert(!BIAS || !CAUSAL, "the biased entry point is never masked");
+  constexpr int kBMq = 32 * QW;      // queries per workgroup
+  constexpr int kGroup = 64 * QW;    // threads per key group
+  constexpr int kKB = fast_kb<D, QW, BIAS>();  // keys per block
   constexpr int NT = kKB / 32;  // 32-key tiles per block
   constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
   constexpr int KSLOT = kKB * D;
   constexpr int VSLOT = kKB * D;
-  constexpr int GLDS = fast_group_lds_halves<D>();
-  constexpr int LCH = kKB * D / 8 / 64 / 4;  // 1 KiB load instructions per wave and matrix
+  constexpr int GLDS = fast_group_lds_halves<D, QW, BIAS>();
+  constexpr int LCH = kKB * D / 8 / 64 / QW;  // 1 KiB load instructions per wave and matrix
   constexpr int CPR = D / 8;      // 16-byte chunks per K/V row
   constexpr int RPI = 64 / CPR;   // rows per 1 KiB load instruction
-  static_assert(LCH >= 1 && kKB * D * 2 == 4 * LCH * 1024 && RPI * D == 512, "tile split");
+  static_assert(LCH >= 1 && kKB * D * 2 == QW * LCH * 1024 && RPI * D == 512, "tile split");
+  static_assert(!BIAS || NT == 1, "one 32-key tile per biased block");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
+  // Bias band: two slots of 64 entries per wave (its own, no barrier).
+  __shared__ float sband[BIAS ? KSPLIT * QW * 2 * 64 : 1];
 
   const int tid = threadIdx.x;
   const int kg = __builtin_amdgcn_readfirstlane(tid / kGroup);  // key group
   const int gtid = tid % kGroup;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(gtid >> 6);  // query slice (0..3)
+  const int wave = __builtin_amdgcn_readfirstlane(gtid >> 6);  // query slice (0..QW-1)
   const int g = lane >> 5;
   const int ql = lane & 31;
 
@@ -132,7 +156,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     q0 = hs * 64;
     qw0 = sl < 2 ? hs * 64 + 32 * sl : (hl == hs ? N : hl * 64 + 32 * (sl - 2));
   } else {
-    q0 = qblk * kBM;
+    q0 = qblk * kBMq;
     qw0 = q0 + wave * 32;
   }
   const int q = qw0 + ql;
@@ -149,7 +173,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // Rows addressed from qb: the workgroup's first row, or with HALVES the
   // wave's own (its two halves are not contiguous).
   const int qb = HALVES ? qw0 : q0;
-  const int qrows = HALVES ? max(0, min(N - qw0, 32)) : min(N - q0, kBM);
+  const int qrows = HALVES ? max(0, min(N - qw0, 32)) : min(N - q0, kBMq);
   const rsrc_t rsQ = make_rsrc(Qh + (int64_t)qb * p.stride_q, (uint32_t)qrows * p.stride_q * 2);
   half8v qf[KS];
 #pragma unroll
@@ -168,7 +192,7 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // on to my_n).
   const int kbeg = CAUSAL ? max(0, q0 - wl) : 0;
   const int kend = HALVES ? min(N, (n64 - q0 / 64) * 64 + wr)
-                 : CAUSAL ? (int)min((int64_t)N, (int64_t)q0 + kBM + wr) : N;
+                 : CAUSAL ? (int)min((int64_t)N, (int64_t)q0 + kBMq + wr) : N;
   const int blk0 = kbeg / kKB;
   const int nblk = max(0, (kend + kKB - 1) / kKB - blk0);
   const int my_n = nblk > kg ? (nblk - kg + KSPLIT - 1) / KSPLIT : 0;
@@ -233,10 +257,47 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) koff[ks] = krow * D + 8 * ((2 * ks + g) ^ kswz<D>(krow));
 
-  auto qk = [&](float16v(&s)[NT], const half_t* k_l) {
+  // Bias band of block i (BIAS): entry j of the wave's band slot i % 2 is
+  // table[h][qw0 - kb0 - (KB - 1) + N - 1 + j] in score units (t / |scale|),
+  // the entries of this wave's 32 queries against the block's keys (indices
+  // past the table read as zero; they meet only keys or queries past N).
+  // One entry per lane is loaded into a register with the block's K and V
+  // (step i - 2) and stored after that step's wait; the block's scores (step
+  // i - 1) and its slow path (step i) read their 16 entries per lane from
+  // the slot, which is rewritten for block i + 2 at the end of step i.
+  const float* Th = BIAS ? static_cast<const float*>(p.bias) + (int64_t)bh * p.bias_stride_h : nullptr;
+  const rsrc_t rsT = make_rsrc(Th, BIAS ? (uint32_t)(2 * N - 1) * 4u : 0u);
+  const float tscale = kLog2e / c;  // c (s + t tscale) = c s + t log2(e)
+  float* const band = &sband[BIAS ? (kg * QW + wave) * 128 : 0];
+  auto band_load = [&](int i) -> float {
+    if constexpr (!BIAS) return 0.f;
+    const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
+    return buf_load_f32(rsT, (uint32_t)(qw0 - kb0 - (kKB - 1) + N - 1 + lane) * 4u);
+  };
+  auto band_store = [&](int i, float t) {
+    if constexpr (BIAS) band[64 * (i & 1) + lane] = t * tscale;
+  };
+  // Initial score accumulator of block i: register r of lane (ql, g) is key
+  // 16 (r / 8) + 8 g + r % 8 of the block, band entry ql - key + KB - 1.
+  auto band_acc = [&](int i) {
+    float16v a;
+    if constexpr (BIAS) {
+      const float* b = band + 64 * (i & 1) + ql + (kKB - 1) - 8 * g;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) a[r] = b[-(16 * (r >> 3) + (r & 7))];
+    } else {
+      a = float16v{};
+    }
+    return a;
+  };
+
+  // Scores of block i (K tile in k_l), with its bias band as initial
+  // accumulator.
+  auto qk = [&](float16v(&s)[NT], const half_t* k_l, int i) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      s[t] = mfma32x32x16(load_half8(k_l + koff[0] + 32 * t * D), qf[0], float16v{});
+      s[t] = mfma32x32x16(load_half8(k_l + koff[0] + 32 * t * D), qf[0],
+                          BIAS ? band_acc(i) : float16v{});
 #pragma unroll
       for (int ks = 1; ks < KS; ++ks)
         s[t] = mfma32x32x16(load_half8(k_l + koff[ks] + 32 * t * D), qf[ks], s[t]);
@@ -284,7 +345,8 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // a pair of scores is converted every second slot.  Returns the lane's
   // sum of fp16 pcur.
   auto fused = [&](const float16v(&s)[NT], float16v(&sn)[NT], const half_t* k_l,
-                   const half_t* v_l, const half8v(&pprev)[2 * NT], half8v(&pcur)[2 * NT]) {
+                   const half_t* v_l, const half8v(&pprev)[2 * NT], half8v(&pcur)[2 * NT],
+                   int inext) {
     constexpr int NQ = KS * NT;       // score MFMAs
     constexpr int NP = DT * 2 * NT;   // P V MFMAs
     constexpr int NJ = NQ + NP;       // slots
@@ -302,6 +364,8 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       const int cc = sc / 8;
       return s[cc >> 1][8 * (cc & 1) + sc % 8];
     };
+    float16v binit;  // bias band of block inext, read ahead of the K fragments
+    if constexpr (BIAS) binit = band_acc(inext);
     half8v fr[NJ];
 #pragma unroll
     for (int j = 0; j < AHEAD; ++j) fr[j] = frag(j);
@@ -325,7 +389,10 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       const int q = j / 2;
       if (j % 2 == 0) {
         const int t = q % NT, ks = q / NT;
-        sn[t] = mfma32x32x16(fr[j], qf[ks], ks == 0 ? float16v{} : sn[t]);
+        if constexpr (BIAS)
+          sn[t] = mfma32x32x16(fr[j], qf[ks], ks == 0 ? binit : sn[t]);
+        else
+          sn[t] = mfma32x32x16(fr[j], qf[ks], ks == 0 ? float16v{} : sn[t]);
       } else {
         const int u = q % DT, cc = q / DT;
         o[u] = mfma32x32x16(fr[j], pprev[cc], o[u]);
@@ -399,9 +466,9 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 
   // Slow path for block i of a step (K in slot si): its scores are
   // recomputed from LDS, so the fused step need not keep them live.
-  auto slow = [&](int si, int kb0, bool masked, half8v(&pb)[2 * NT]) {
+  auto slow = [&](int i, int kb0, bool masked, half8v(&pb)[2 * NT]) {
     float16v s[NT];
-    qk(s, kslot(si));
+    qk(s, kslot(i & 3), i);
     return slow_scores(s, kb0, masked, pb);
   };
 
@@ -422,11 +489,14 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // ran in step i-1.
   auto body = [&](int i, float16v(&s)[NT], float16v(&sn)[NT], half8v(&pprev)[2 * NT],
                   half8v(&pcur)[2 * NT]) {
-    const int si = i & 3;
+    float bload = 0.f;  // bias band entry of block i + 2
 #ifdef NESO_FA2_SERIAL_LDS
     // The debug build's barrier must be reached by every wave (my_n differs
     // between key groups), so the loads are issued outside the branch.
-    if (i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
+    if (i + 2 < my_n) {
+      lds_load(i + 2, (i + 2) & 3);
+      bload = band_load(i + 2);
+    }
     serial_lds_point();
     if constexpr (HALVES) {
       if (i == my_nw && i < my_n) pv_only(pprev, vslot((i - 1) & 3));
@@ -442,7 +512,10 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       }
     }
     if (i < (HALVES ? my_nw : my_n)) {
-      if (!HALVES && i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
+      if (!HALVES && i + 2 < my_n) {
+        lds_load(i + 2, (i + 2) & 3);
+        bload = band_load(i + 2);
+      }
 #endif
       const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
       // Some key of the block is past N or outside some query's window.
@@ -450,9 +523,9 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
           (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
       // After the group's last block the next scores come from a stale
       // slot and are never used.
-      float ls = fused(s, sn, kslot((i + 1) & 3), vslot((i + 3) & 3), pprev, pcur);
+      float ls = fused(s, sn, kslot((i + 1) & 3), vslot((i + 3) & 3), pprev, pcur, i + 1);
       // ls enters the condition so that the softmax cannot sink below it.
-      if (__any(masked || !(ls <= thr))) ls = slow(si, kb0, masked, pcur);
+      if (__any(masked || !(ls <= thr))) ls = slow(i, kb0, masked, pcur);
       l_run += ls;
     }
     // Steps past the group's last block load nothing: no later step reads
@@ -460,13 +533,23 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     // stays in place.
     serial_lds_point();
     wait_vmem();
+    if (BIAS && i + 2 < my_n) band_store(i + 2, bload);
     lds_barrier();
   };
 
   // ---- prologue: blocks 0 and 1 into LDS in one round trip, scores of 0 ----
-  if (my_n > 0) lds_load(0, 0);
-  if (my_n > 1) lds_load(1, 1);
+  float bpro[3] = {0.f, 0.f, 0.f};  // bias band entries of blocks 0..2
+  if (my_n > 0) {
+    lds_load(0, 0);
+    bpro[0] = band_load(0);
+  }
+  if (my_n > 1) {
+    lds_load(1, 1);
+    bpro[1] = band_load(1);
+  }
   wait_vmem();
+  band_store(0, bpro[0]);
+  band_store(1, bpro[1]);
   lds_barrier();
   float16v sa[NT], sb[NT];
   half8v pa[2 * NT], pb2[2 * NT];
@@ -475,17 +558,21 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // softmax is the slow path on its exact scores; scores of block 1; loads
   // of block 2.  (Scores of blocks a group does not have come from stale
   // slots and are never used.) ----
-  if (my_n > 2) lds_load(2, 2);
+  if (my_n > 2) {
+    lds_load(2, 2);
+    bpro[2] = band_load(2);
+  }
   serial_lds_point();
-  qk(sa, kslot(0));
+  qk(sa, kslot(0), 0);
   if (HALVES ? my_nw > 0 : my_n > 0) {
     const int kb0 = (blk0 + kg) * kKB;
     const bool masked =
         (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
-    qk(sb, kslot(1));
+    qk(sb, kslot(1), 1);
     l_run += slow_scores(sa, kb0, masked, pb2);
   }
   wait_vmem();
+  if (BIAS && my_n > 2) band_store(2, bpro[2]);
   lds_barrier();
 
   // Steps 1, 2, ...: unrolled by two so that the score and P arrays swap
@@ -505,48 +592,71 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   }
 
   // ---- merge the key groups through LDS ----
-  // Two key groups and an even number of 32-column tiles of O: group g
-  // finishes the tiles u with u % 2 == g.  Each group publishes (m, l) and
-  // the tiles the other group finishes, so both merge and store half of O.
-  constexpr bool kSplitMerge = KSPLIT == 2 && DT % 2 == 0;
+  // Split merge (the lane's NV = 16 DT values of O divide into KSPLIT runs
+  // of whole float4 pieces): group g finishes values [g VR, g VR + VR).
+  // Each group publishes (m, l) and the values the other groups finish, so
+  // every group merges and stores 1/KSPLIT of O.  Otherwise group 0 folds
+  // the other groups' partials and stores all of O.
+  constexpr int NV = 16 * DT;
+  constexpr bool kSplitMerge = KSPLIT > 1 && NV % (4 * KSPLIT) == 0;
+  constexpr int VR = kSplitMerge ? NV / KSPLIT : NV;
   if constexpr (kSplitMerge) {
     // The partials below overwrite the start of the LDS, where the
     // last-block P V above may still be reading V.
     lds_barrier();
-    constexpr int SLOTS = 16 * (DT / 2) + 2;
-    static_assert(sizeof(smem) >= 8 * SLOTS * 64 * sizeof(float), "merge buffer");
+    constexpr int SLOTS = NV - VR + 2;
+    static_assert(sizeof(smem) >= (size_t)KSPLIT * QW * SLOTS * 64 * sizeof(float), "merge buffer");
     float* const red = reinterpret_cast<float*>(smem) + lane;
-    float* mine = red + (size_t)(4 * kg + sl) * SLOTS * 64;
-    const float* other = red + (size_t)(4 * (1 - kg) + sl) * SLOTS * 64;
-    mine[0] = m_run;
-    mine[64] = l_run;
+    auto part = [&](int grp) { return red + (size_t)(QW * grp + sl) * SLOTS * 64; };
+    // Slot of value v in the list that group grp publishes (all values but
+    // its own run).
+    auto pos = [](int grp, int v) { return 2 + (v / VR > grp ? v - VR : v); };
 #pragma unroll
-    for (int u = 0; u < DT; ++u) {
-      if ((u & 1) == kg) continue;  // kg is wave-uniform: a scalar branch
+    for (int me = 0; me < KSPLIT; ++me) {
+      if (me != kg) continue;  // kg is wave-uniform: a scalar branch
+      float* mine = part(me);
+      mine[0] = m_run;
+      mine[64] = l_run;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mine[(2 + 16 * (u / 2) + r) * 64] = o[u][r];
+      for (int v = 0; v < NV; ++v)
+        if (v / VR != me) mine[pos(me, v) * 64] = o[v / 16][v % 16];
     }
     lds_barrier();
-    const float m1 = other[0];
-    const float l1 = other[64];
-    const float mm = fmaxf(m_run, m1);
-    const float mu = (mm == -INFINITY) ? 0.f : mm;
-    const float a0 = fast_exp2(m_run - mu);
-    const float a1 = fast_exp2(m1 - mu);
-    m_run = mm;
-    l_run = l_run * a0 + l1 * a1;
 #pragma unroll
-    for (int u = 0; u < DT; ++u) {
-      if ((u & 1) != kg) continue;
+    for (int me = 0; me < KSPLIT; ++me) {
+      if (me != kg) continue;
+      float mj[KSPLIT];
+      float mm = m_run;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o[u][r] = o[u][r] * a0 + other[(2 + 16 * (u / 2) + r) * 64] * a1;
+      for (int j = 0; j < KSPLIT; ++j) {
+        if (j == me) continue;
+        mj[j] = part(j)[0];
+        mm = fmaxf(mm, mj[j]);
+      }
+      const float mu = (mm == -INFINITY) ? 0.f : mm;
+      const float a0 = fast_exp2(m_run - mu);
+      float lsum = l_run * a0;
+#pragma unroll
+      for (int v = me * VR; v < me * VR + VR; ++v) o[v / 16][v % 16] *= a0;
+#pragma unroll
+      for (int j = 0; j < KSPLIT; ++j) {
+        if (j == me) continue;
+        const float* other = part(j);
+        const float aj = fast_exp2(mj[j] - mu);
+        lsum += other[64] * aj;
+#pragma unroll
+        for (int v = me * VR; v < me * VR + VR; ++v)
+          o[v / 16][v % 16] = __builtin_fmaf(other[pos(j, v) * 64], aj, o[v / 16][v % 16]);
+      }
+      m_run = mm;
+      l_run = lsum;
     }
   } else if constexpr (KSPLIT > 1) {
     // The partials below overwrite the start of the LDS, where group 0's
     // last-block P V above may still be reading V^T.
     lds_barrier();
     constexpr int SLOTS = 16 * DT + 2;
-    constexpr int PART = 4 * SLOTS * 64;  // floats per published group
+    constexpr int PART = QW * SLOTS * 64;  // floats per published group
     static_assert(sizeof(smem) >= (size_t)(KSPLIT - 1) * PART * sizeof(float), "merge buffer");
     float* red = reinterpret_cast<float*>(smem) + (size_t)wave * SLOTS * 64 + lane;
     if (kg > 0) {
@@ -587,9 +697,14 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
                                (uint32_t)qrows * p.stride_o * ES);
 #pragma unroll
   for (int u = 0; u < DT; ++u) {
-    if (kSplitMerge && (u & 1) != kg) continue;
+    if constexpr (kSplitMerge && VR >= 16) {
+      if (16 * u / VR != kg) continue;  // scalar branches
+    }
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
+      if constexpr (kSplitMerge && VR < 16) {
+        if ((16 * u + 4 * b) / VR != kg) continue;
+      }
       const int col = 32 * u + 8 * b + 4 * g;
       const uint32_t off = ((q - qb) * p.stride_o + col) * ES;
       float4v v = {o[u][4 * b] * inv, o[u][4 * b + 1] * inv, o[u][4 * b + 2] * inv,
@@ -619,50 +734,63 @@ __global__ __launch_bounds__(kGroup * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 }
 
 // Launches with K key groups if their LDS fits (returns false otherwise).
-template <int D, bool CAUSAL, bool OUT_F16, int K>
+template <int D, bool CAUSAL, bool OUT_F16, int K, int QW, bool BIAS>
 bool launch_fast_k(const Fa2Args& a, hipStream_t stream, hipError_t& err) {
-  if constexpr (K * fast_group_lds_halves<D>() * 2 <= 160 * 1024) {
-    if constexpr (CAUSAL) {
+  if constexpr (fast_lds_bytes<D, QW, BIAS>(K) <= 160 * 1024) {
+    if constexpr (CAUSAL && QW == 4) {
       if (a.pair_qblocks == 1) {
         err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, true>>(
-            ktag("fa2_fast_kernel", D, true, OUT_F16, K, true, false),
-            dim3((a.num_qblocks + 1) / 2 * a.batch_heads), dim3(K * kGroup), stream, a);
+            ktag("fa2_fast_kernel", D, true, OUT_F16, K, true, false, QW, BIAS),
+            dim3((a.num_qblocks + 1) / 2 * a.batch_heads), dim3(K * 64 * QW), stream, a);
         return true;
       }
       if (a.pair_qblocks == 2) {
         err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, false, true>>(
-            ktag("fa2_fast_kernel", D, true, OUT_F16, K, false, true),
-            dim3(((a.N + 63) / 64 + 1) / 2 * a.batch_heads), dim3(K * kGroup), stream, a);
+            ktag("fa2_fast_kernel", D, true, OUT_F16, K, false, true, QW, BIAS),
+            dim3(((a.N + 63) / 64 + 1) / 2 * a.batch_heads), dim3(K * 64 * QW), stream, a);
         return true;
       }
     }
-    err = launch<&fa2_fast_kernel<D, CAUSAL, OUT_F16, K>>(
-        ktag("fa2_fast_kernel", D, CAUSAL, OUT_F16, K, false, false),
-        dim3(a.num_qblocks * a.batch_heads), dim3(K * kGroup), stream, a);
+    err = launch<&fa2_fast_kernel<D, CAUSAL, OUT_F16, K, false, false, QW, BIAS>>(
+        ktag("fa2_fast_kernel", D, CAUSAL, OUT_F16, K, false, false, QW, BIAS),
+        dim3(a.num_qblocks * a.batch_heads), dim3(K * 64 * QW), stream, a);
     return true;
   }
   return false;
 }
 
-template <int D, bool CAUSAL, bool OUT_F16>
+// The requested key split, or the largest smaller one whose LDS fits: 1
+// or 2, and 4 with two query waves.
+template <int D, bool CAUSAL, bool OUT_F16, int QW, bool BIAS>
 hipError_t launch_fast_t(const Fa2Args& a, int ksplit, hipStream_t stream) {
   hipError_t err = hipSuccess;
   bool done = false;
-  if (ksplit >= 3) done = launch_fast_k<D, CAUSAL, OUT_F16, 3>(a, stream, err);
-  if (!done && ksplit >= 2) done = launch_fast_k<D, CAUSAL, OUT_F16, 2>(a, stream, err);
-  if (!done) launch_fast_k<D, CAUSAL, OUT_F16, 1>(a, stream, err);
+  if constexpr (QW == 2) {
+    if (ksplit >= 4) done = launch_fast_k<D, CAUSAL, OUT_F16, 4, QW, BIAS>(a, stream, err);
+  }
+  if (!done && ksplit >= 2) done = launch_fast_k<D, CAUSAL, OUT_F16, 2, QW, BIAS>(a, stream, err);
+  if (!done) launch_fast_k<D, CAUSAL, OUT_F16, 1, QW, BIAS>(a, stream, err);
   return err;
 }
 
+template <int D, bool CAUSAL, bool OUT_F16, bool BIAS>
+hipError_t launch_fast_q(const Fa2Args& a, int ksplit, hipStream_t stream) {
+  return a.qwaves == 2 ? launch_fast_t<D, CAUSAL, OUT_F16, 2, BIAS>(a, ksplit, stream)
+                       : launch_fast_t<D, CAUSAL, OUT_F16, 4, BIAS>(a, ksplit, stream);
+}
+
 template <bool OUT_F16>
-hipError_t launch_fast_d(const Fa2Args& a, int d, bool causal, int ksplit, hipStream_t s) {
+hipError_t launch_fast_d(const Fa2Args& a, int d, bool causal, bool bias, int ksplit,
+                         hipStream_t s) {
   switch (d) {
     case 64:
-      return causal ? launch_fast_t<64, true, OUT_F16>(a, ksplit, s)
-                    : launch_fast_t<64, false, OUT_F16>(a, ksplit, s);
+      return bias     ? launch_fast_q<64, false, OUT_F16, true>(a, ksplit, s)
+             : causal ? launch_fast_q<64, true, OUT_F16, false>(a, ksplit, s)
+                      : launch_fast_q<64, false, OUT_F16, false>(a, ksplit, s);
     case 128:
-      return causal ? launch_fast_t<128, true, OUT_F16>(a, ksplit, s)
-                    : launch_fast_t<128, false, OUT_F16>(a, ksplit, s);
+      return bias     ? launch_fast_q<128, false, OUT_F16, true>(a, ksplit, s)
+             : causal ? launch_fast_q<128, true, OUT_F16, false>(a, ksplit, s)
+                      : launch_fast_q<128, false, OUT_F16, false>(a, ksplit, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -676,37 +804,54 @@ bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32) {
   (void)head_dim, (void)bias_kind, (void)in_f32;
   return false;
 #else
-  return (head_dim == 64 || head_dim == 128) && bias_kind == kBiasNone && !in_f32;
+  return (head_dim == 64 || head_dim == 128) &&
+         (bias_kind == kBiasNone || bias_kind == kBiasTableF32) && !in_f32;
 #endif
 }
 
-bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid) {
+bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid, bool bias) {
   // Measured on MI355X (d = 64, B*H = 8..64): the fast kernel is ahead from
   // N = 128 up without a mask (3-15%) and for causal rows from N = 1024
   // (7-25%, growing with N); for shorter causal rows the generic kernel's
   // per-wave skipping of invisible blocks wins (N = 256: 8.1 vs 8.9 us).
-  // On a small grid (128-query workgroups <= half the compute units) the
-  // generic kernel's 64-query workgroups with four key groups win at d = 64
-  // from N = 512 (7-19%: H16 N1024 12.0 vs 13.4 us, H4 N2048 causal 18.3
-  // vs 22.5 us); at d = 128 the fast kernel stays ahead (5-12%).
-  if (head_dim == 64 && small_grid && N >= 512) return false;
+  // On a small grid (128-query workgroups <= half the compute units) from
+  // N = 512 it runs 64-query workgroups (two query waves, four key groups
+  // at d = 64, two at d = 128), ahead of the generic kernel's 64-query
+  // workgroups by 8-29% (H8 N1500 d64 13.0 vs 15.0 us, H16 N1024 d128 16.3
+  // vs 22.8, H4 N2048 d64 causal 15.9 vs 18.5, rel-pos table H8 N1500 d64
+  // 15.0 vs 16.6, d128 25.0 vs 35.7).  A bias table on a larger grid stays
+  // on the generic kernel, whose 64-key blocks keep it ahead of the fast
+  // kernel's 32-key biased blocks (H16 N2048 d64: 29.4 vs 30.6 us).
+  (void)head_dim;
+  if (bias) return small_grid;
   return !causal || N >= 1024;
 }
 
-hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, int ksplit,
-                           hipStream_t stream) {
+// Query waves of the fast kernel: two on a small grid from N = 512 (and
+// for every biased call, which takes the fast kernel on small grids only).
+int fa2_fast_qwaves(bool small_grid, int32_t N, bool bias) {
+  return small_grid && (bias || N >= 512) ? 2 : 4;
+}
+
+hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool bias, bool out_f16,
+                           int ksplit, hipStream_t stream) {
 #ifdef NESO_FA2_FAST_DISABLED
-  (void)a, (void)head_dim, (void)causal, (void)out_f16, (void)ksplit, (void)stream;
+  (void)a, (void)head_dim, (void)causal, (void)bias, (void)out_f16, (void)ksplit, (void)stream;
   return hipErrorInvalidValue;
 #endif
-  a.num_qblocks = (a.N + kBM - 1) / kBM;
-  // Paired query blocks (causal kernels only; any window is correct);
-  // 64-row halves only without a window (the two halves' key ranges must
-  // both start at key 0).
+  if (bias && causal) return hipErrorInvalidValue;  // the biased entry point is never masked
+  if (a.qwaves != 2) a.qwaves = 4;
+  a.num_qblocks = (a.N + 32 * a.qwaves - 1) / (32 * a.qwaves);
+  // Paired query blocks (causal kernels with four query waves only; any
+  // window is correct); 64-row halves only without a window (the two
+  // halves' key ranges must both start at key 0).
   const bool full_causal = causal && a.win_left >= a.N && a.win_right == 0;
-  a.pair_qblocks = (causal && a.pair_qblocks == 1) ? 1 : (full_causal && a.pair_qblocks == 2) ? 2 : 0;
-  return out_f16 ? launch_fast_d<true>(a, head_dim, causal, ksplit, stream)
-                 : launch_fast_d<false>(a, head_dim, causal, ksplit, stream);
+  a.pair_qblocks = (a.qwaves != 4)                          ? 0
+                   : (causal && a.pair_qblocks == 1)        ? 1
+                   : (full_causal && a.pair_qblocks == 2)   ? 2
+                                                            : 0;
+  return out_f16 ? launch_fast_d<true>(a, head_dim, causal, bias, ksplit, stream)
+                 : launch_fast_d<false>(a, head_dim, causal, bias, ksplit, stream);
 }
 
 }  // namespace neso

@@ -592,8 +592,12 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
                                                                      : 1;
   // Small grid: 128-query workgroups fill at most half the compute units.
   const bool small = 2 * wgs <= cus;
-  if (a.allow_fast && fa2_fast_supported(head_dim, bias_kind, in_f32) &&
-      (a.allow_fast == 2 || fa2_fast_preferred(causal, a.N, head_dim, small))) {
+  // The fast kernel carries a bias table in score units (t / |scale|),
+  // which needs a scale whose reciprocal stays finite.
+  const bool bias = bias_kind != kBiasNone;
+  const bool fast_ok = a.allow_fast && fa2_fast_supported(head_dim, bias_kind, in_f32) &&
+                       (!bias || fabsf(a.scale_log2) >= 1e-20f);
+  if (fast_ok && (a.allow_fast == 2 || fa2_fast_preferred(causal, a.N, head_dim, small, bias))) {
     // Causal grids of at least two workgroups per CU: each workgroup takes a
     // long and a short query block (pair_qblocks), which evens out the work,
     // and the key split then follows the halved grid (fast kernel, measured:
@@ -608,7 +612,12 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
       const int64_t pwgs = (int64_t)((a.num_qblocks + 1) / 2) * a.batch_heads;
       ksplit = pwgs < 2 * cus ? 2 : 1;
     }
-    return launch_fa2_fast(a, head_dim, causal, out_f16, ksplit, stream);
+    // Small grids: 64-query workgroups (two query waves) with four key
+    // groups, which double the grid at eight waves each (head_dim 128 fits
+    // two key groups).
+    if (a.qwaves != 2 && a.qwaves != 4) a.qwaves = fa2_fast_qwaves(small, a.N, bias);
+    if (a.qwaves == 2 && a.ksplit <= 0) ksplit = 4;
+    return launch_fa2_fast(a, head_dim, causal, bias, out_f16, ksplit, stream);
   }
   // Generic kernel on a small grid: 64-query workgroups (two query waves per
   // key group) and four key groups double the grid, still one round of

@@ -129,21 +129,23 @@ constexpr char kManifest[] = R"JSON({
       "OUT_F16",
       "KSPLIT",
       "PAIR",
-      "HALVES"
+      "HALVES",
+      "QW",
+      "BIAS"
      ],
-     "when": "fp16 Q/K/V without a bias at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred); KSPLIT key groups of 4 waves; PAIR (causal grids of >= 2 workgroups per CU): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
-     "threadgroup_size": "256 * KSPLIT",
-     "num_warps": "4 * KSPLIT",
+     "when": "fp16 Q/K/V at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred): without a bias, and with the f32 bias table (BIAS, |scale| >= 1e-20) on grids whose 128-query workgroups fill at most half the CUs; KSPLIT key groups of QW query waves (QW = 2 on such small grids from N = 512 and for the bias table, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "threadgroup_size": "64 * QW * KSPLIT",
+     "num_warps": "QW * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 128) * batch_heads)",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
       "1",
       "1"
      ],
      "constants": {
-      "block_m": "128",
-      "block_n": "32 if D == 128 else 64",
+      "block_m": "32 * QW",
+      "block_n": "64 if (D == 64 and QW == 4 and not BIAS) else 32",
       "lds_ring_slots": "4",
-      "lds_bytes": "KSPLIT * 4 * 2 * (32 if D == 128 else 64) * D * 2"
+      "lds_bytes": "KSPLIT * (4 * 2 * (64 if (D == 64 and QW == 4 and not BIAS) else 32) * D * 2 + (QW * 512 if BIAS else 0))"
      }
     },
     {
@@ -158,7 +160,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: biased (BIAS 1 = f32 table, 2 = dense f16), fp32 input (F32IN), head_dim 32, and shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -293,7 +295,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: biased (BIAS 1 = f32 table, 2 = dense f16), fp32 input (F32IN), head_dim 32, and shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -404,21 +406,23 @@ constexpr char kManifest[] = R"JSON({
       "OUT_F16",
       "KSPLIT",
       "PAIR",
-      "HALVES"
+      "HALVES",
+      "QW",
+      "BIAS"
      ],
-     "when": "fp16 Q/K/V without a bias at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred); KSPLIT key groups of 4 waves; PAIR (causal grids of >= 2 workgroups per CU): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
-     "threadgroup_size": "256 * KSPLIT",
-     "num_warps": "4 * KSPLIT",
+     "when": "fp16 Q/K/V at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred): without a bias, and with the f32 bias table (BIAS, |scale| >= 1e-20) on grids whose 128-query workgroups fill at most half the CUs; KSPLIT key groups of QW query waves (QW = 2 on such small grids from N = 512 and for the bias table, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "threadgroup_size": "64 * QW * KSPLIT",
+     "num_warps": "QW * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 128) * batch_heads)",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
       "1",
       "1"
      ],
      "constants": {
-      "block_m": "128",
-      "block_n": "32 if D == 128 else 64",
+      "block_m": "32 * QW",
+      "block_n": "64 if (D == 64 and QW == 4 and not BIAS) else 32",
       "lds_ring_slots": "4",
-      "lds_bytes": "KSPLIT * 4 * 2 * (32 if D == 128 else 64) * D * 2"
+      "lds_bytes": "KSPLIT * (4 * 2 * (64 if (D == 64 and QW == 4 and not BIAS) else 32) * D * 2 + (QW * 512 if BIAS else 0))"
      }
     },
     {
@@ -433,7 +437,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: biased (BIAS 1 = f32 table, 2 = dense f16), fp32 input (F32IN), head_dim 32, and shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -568,21 +572,23 @@ constexpr char kManifest[] = R"JSON({
       "OUT_F16",
       "KSPLIT",
       "PAIR",
-      "HALVES"
+      "HALVES",
+      "QW",
+      "BIAS"
      ],
-     "when": "fp16 Q/K/V without a bias at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred); KSPLIT key groups of 4 waves; PAIR (causal grids of >= 2 workgroups per CU): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
-     "threadgroup_size": "256 * KSPLIT",
-     "num_warps": "4 * KSPLIT",
+     "when": "fp16 Q/K/V at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred): without a bias, and with the f32 bias table (BIAS, |scale| >= 1e-20) on grids whose 128-query workgroups fill at most half the CUs; KSPLIT key groups of QW query waves (QW = 2 on such small grids from N = 512 and for the bias table, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "threadgroup_size": "64 * QW * KSPLIT",
+     "num_warps": "QW * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 128) * batch_heads)",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
       "1",
       "1"
      ],
      "constants": {
-      "block_m": "128",
-      "block_n": "32 if D == 128 else 64",
+      "block_m": "32 * QW",
+      "block_n": "64 if (D == 64 and QW == 4 and not BIAS) else 32",
       "lds_ring_slots": "4",
-      "lds_bytes": "KSPLIT * 4 * 2 * (32 if D == 128 else 64) * D * 2"
+      "lds_bytes": "KSPLIT * (4 * 2 * (64 if (D == 64 and QW == 4 and not BIAS) else 32) * D * 2 + (QW * 512 if BIAS else 0))"
      }
     },
     {
@@ -597,7 +603,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: biased (BIAS 1 = f32 table, 2 = dense f16), fp32 input (F32IN), head_dim 32, and shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -734,6 +740,34 @@ constexpr char kManifest[] = R"JSON({
    },
    "variants": [
     {
+     "device_kernel": "fa2_fast_kernel",
+     "source": "neso_amd/csrc/fa2_fast.hip",
+     "template_params": [
+      "D",
+      "CAUSAL",
+      "OUT_F16",
+      "KSPLIT",
+      "PAIR",
+      "HALVES",
+      "QW",
+      "BIAS"
+     ],
+     "when": "fp16 Q/K/V at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred): without a bias, and with the f32 bias table (BIAS, |scale| >= 1e-20) on grids whose 128-query workgroups fill at most half the CUs; KSPLIT key groups of QW query waves (QW = 2 on such small grids from N = 512 and for the bias table, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "threadgroup_size": "64 * QW * KSPLIT",
+     "num_warps": "QW * KSPLIT",
+     "grid": [
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
+      "1",
+      "1"
+     ],
+     "constants": {
+      "block_m": "32 * QW",
+      "block_n": "64 if (D == 64 and QW == 4 and not BIAS) else 32",
+      "lds_ring_slots": "4",
+      "lds_bytes": "KSPLIT * (4 * 2 * (64 if (D == 64 and QW == 4 and not BIAS) else 32) * D * 2 + (QW * 512 if BIAS else 0))"
+     }
+    },
+    {
      "device_kernel": "fa2_fwd_kernel",
      "source": "neso_amd/csrc/fa2_fwd.hip",
      "template_params": [
@@ -745,7 +779,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: biased (BIAS 1 = f32 table, 2 = dense f16), fp32 input (F32IN), head_dim 32, and shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [

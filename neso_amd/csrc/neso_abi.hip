@@ -49,9 +49,10 @@ int env_ksplit() {
   return (k >= 1 && k <= 4) ? k : 0;
 }
 
-// FA2 kernel choice for fp16 calls without a bias (tests cover both
-// kernels): NESO_AMD_FA2_FAST=0 always takes the generic kernel, =2 the fast
-// kernel wherever it applies; unset or 1 chooses by shape.
+// FA2 kernel choice for fp16 calls without a bias or with the f32 bias
+// table (tests cover both kernels): NESO_AMD_FA2_FAST=0 always takes the
+// generic kernel, =2 the fast kernel wherever it applies; unset or 1
+// chooses by shape.
 int env_allow_fast() {
   const char* v = getenv("NESO_AMD_FA2_FAST");
   if (!v) return 1;
@@ -59,7 +60,7 @@ int env_allow_fast() {
   return v[0] == '2' ? 2 : 1;
 }
 
-// Query waves per key group of the generic FA2 kernel (tests cover both):
+// Query waves per key group of either FA2 kernel (tests cover both):
 // NESO_AMD_FA2_QW=2 or 4; unset chooses from the grid size.
 int env_qwaves() {
   const char* v = getenv("NESO_AMD_FA2_QW");

@@ -34,12 +34,12 @@ struct Fa2Args {
   // i - win_left <= j <= i + win_right.  Causal is (N, 0).
   int32_t win_left;
   int32_t win_right;
-  // Kernel choice for fp16 calls without a bias: 1 = the fast kernel
-  // (fa2_fast.hip) where it is measured faster, 2 = the fast kernel
-  // wherever it applies, 0 = always the generic kernel.
+  // Kernel choice for fp16 calls without a bias or with the f32 bias
+  // table: 1 = the fast kernel (fa2_fast.hip) where it is measured faster,
+  // 2 = the fast kernel wherever it applies, 0 = always the generic kernel.
   int32_t allow_fast;
-  // Query waves per key group of the generic kernel (its query block is 32
-  // rows per wave): 4 or 2; 0 = chosen from the grid size.
+  // Query waves per key group (a query block is 32 rows per wave): 4 or 2;
+  // 0 = chosen from the grid size.
   int32_t qwaves;
   // Causal fast kernel: 1 = each workgroup takes query blocks nqb-1-x and
   // x; 2 = it takes the 64-row blocks x and n64-1-x (no window); 0 = one
@@ -83,12 +83,14 @@ hipError_t launch(const KernelTag& tag, dim3 grid, dim3 block, hipStream_t strea
 }
 
 int fa2_query_block();
-// The fast kernel covers fp16 Q/K/V without a bias at head_dim 64, and is
-// the faster one for unmasked attention from N ~ 2048 up.
+// The fast kernel covers fp16 Q/K/V at head_dim 64 and 128, without a bias
+// or with the f32 bias table; fa2_fast_preferred says where it is the
+// faster one.  qwaves (2 or 4) picks its query waves per key group.
 bool fa2_fast_supported(int head_dim, int bias_kind, bool in_f32);
-bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid);
-hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool out_f16, int ksplit,
-                           hipStream_t stream);
+bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid, bool bias);
+int fa2_fast_qwaves(bool small_grid, int32_t N, bool bias);
+hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool bias, bool out_f16,
+                           int ksplit, hipStream_t stream);
 hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool out_f16,
                       hipStream_t stream, bool in_f32 = false);
 

@@ -111,6 +111,10 @@ PLAN_CASES = [
      dict(N=2048, batch_heads=4)),
     ("neso_flash_attention_fwd", [_P] * 4 + [300, 32, 32, 0.17, 32, 3, 300 * 32, 300 * 32, 0],
      dict(N=300, batch_heads=3)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [1024, 128, 128, 0.08, 128, 16, 1024 * 128, 1024 * 128, 0],
+     dict(N=1024, batch_heads=16)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [1500, 64, 64, 0.125, 64, 8, 1500 * 64, 1500 * 64, 0],
+     dict(N=1500, batch_heads=8)),
     ("neso_flash_attention_f32_fwd", [_P] * 4 + [512, 128, 128, 0.08, 128, 2, 512 * 128, 512 * 128, 0],
      dict(N=512, batch_heads=2)),
     ("neso_flash_attention_f32_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 8, 2048 * 64, 2048 * 64, 1],
@@ -167,6 +171,56 @@ def test_manifest_geometry_matches_launches(lib, case, cus):
     assert _eval(v["threadgroup_size"], env) == rec["threadgroup_size"]
     assert _eval(v["num_warps"], env) == rec["num_warps"]
     assert [_eval(g, env) for g in v["grid"]] == rec["grid"], (v["grid"], rec)
+
+
+# (entry point, args, expected kernel, expected template arguments by name)
+CHOICE_CASES = [
+    # 96 workgroups of 128 queries fill under half of 256
+    # CUs, so the biased fast kernel runs 64-query workgroups, 4 key groups.
+    ("neso_rel_pos_fa2_fwd", [_P] * 5 + [1500, 64, 0.125, 1500 * 64, 2999, 8, 64, 1, 1],
+     "fa2_fast_kernel", dict(D=64, QW=2, KSPLIT=4, BIAS=1)),
+    # A larger biased grid stays on the generic kernel.
+    ("neso_rel_pos_fa2_fwd", [_P] * 5 + [8192, 64, 0.125, 8192 * 64, 16383, 16, 64, 1, 1],
+     "fa2_fwd_kernel", dict(BIAS=1)),
+    # A scale whose reciprocal could overflow the band: generic kernel.
+    ("neso_rel_pos_fa2_fwd", [_P] * 5 + [1500, 64, 1e-30, 1500 * 64, 2999, 8, 64, 1, 1],
+     "fa2_fwd_kernel", dict(BIAS=1)),
+    # The dense f16 bias has no fast kernel.
+    ("neso_rel_pos_fa2_fwd", [_P] * 5 + [1500, 64, 0.125, 1500 * 64, 1500 * 1500, 8, 64, 0, 0],
+     "fa2_fwd_kernel", dict(BIAS=2)),
+    # The headline: 128-query workgroups, two key groups.
+    ("neso_flash_attention_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 16, 2048 * 64, 2048 * 64, 0],
+     "fa2_fast_kernel", dict(QW=4, KSPLIT=2, PAIR=0, HALVES=0, BIAS=0)),
+    # Small grids from N = 512: two query waves (four key groups at d = 64,
+    # two at d = 128, where four do not fit the LDS).
+    ("neso_flash_attention_fwd", [_P] * 4 + [1500, 64, 64, 0.125, 64, 8, 1500 * 64, 1500 * 64, 0],
+     "fa2_fast_kernel", dict(QW=2, KSPLIT=4)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [1024, 128, 128, 0.08, 128, 16, 1024 * 128, 1024 * 128, 0],
+     "fa2_fast_kernel", dict(QW=2, KSPLIT=2)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 4, 2048 * 64, 2048 * 64, 1],
+     "fa2_fast_kernel", dict(QW=2, KSPLIT=4, CAUSAL=1, HALVES=0)),
+    # Causal, one workgroup per CU: 64-row halves on four query waves.
+    ("neso_flash_attention_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 16, 2048 * 64, 2048 * 64, 1],
+     "fa2_fast_kernel", dict(QW=4, HALVES=1)),
+    # Short rows: the fast kernel with 128-query workgroups (N < 512).
+    ("neso_flash_attention_fwd", [_P] * 4 + [128, 64, 64, 0.125, 64, 8, 128 * 64, 128 * 64, 0],
+     "fa2_fast_kernel", dict(QW=4)),
+]
+
+
+@pytest.mark.parametrize("case", range(len(CHOICE_CASES)))
+def test_fa2_kernel_choice(lib, case):
+    """The launcher's kernel and workgroup shape for shapes whose choice was
+    measured, on a 256-CU device."""
+    name, args, kernel, want = CHOICE_CASES[case]
+    man = {k["kernel_name"]: k for k in json.loads(lib.neso_kernel_manifest().decode())["kernels"]}
+    status, launches = _plan(lib, getattr(lib, name), args + [None], 256)
+    assert status == _lib.NESO_OK, lib.neso_last_error()
+    (rec,) = launches
+    assert rec["device_kernel"] == kernel, rec
+    params = {v["device_kernel"]: v["template_params"] for v in man[name]["variants"]}[kernel]
+    got = dict(zip(params, rec["template_args"]))
+    assert {k: got[k] for k in want} == want, got
 
 
 def test_plan_records_nothing_on_rejected_calls(lib):

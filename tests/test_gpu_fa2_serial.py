@@ -78,3 +78,38 @@ def test_window_equal(gpu, libs, monkeypatch):
     q, k, v = (t.to(DEV) for t in I.fa2_inputs(1, 4, 1500, 64, seed=4))
     fast, serial = (_run(lib, q, k, v, True, wl=300, wr=40) for lib in libs)
     assert torch.equal(fast, serial)
+
+
+@pytest.mark.parametrize("d,causal", [(64, False), (64, True), (128, False)])
+def test_two_query_waves_equal(gpu, libs, monkeypatch, d, causal):
+    """64-query workgroups, four key groups of two waves (d = 128: two)."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_QW", "2")
+    q, k, v = (t.to(DEV) for t in I.fa2_inputs(1, 3, 1000, d, seed=d))
+    fast, serial = (_run(lib, q, k, v, causal) for lib in libs)
+    assert torch.isfinite(fast).all()
+    assert torch.equal(fast, serial)
+
+
+def _run_table(lib, q, k, v, table):
+    h, n, d = q.shape
+    o = torch.full(q.shape, float("nan"), device=DEV)
+    st = lib.neso_rel_pos_fa2_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), table.data_ptr(),
+                                  o.data_ptr(), n, d, d ** -0.5, n * d, 2 * n - 1, h, d,
+                                  _lib.NESO_BIAS_TABLE_F32, _lib.NESO_OUT_F32, None)
+    assert st == _lib.NESO_OK
+    torch.cuda.synchronize()
+    return o.cpu()
+
+
+@pytest.mark.parametrize("qw", [2, 4])
+def test_rel_pos_table_equal(gpu, libs, monkeypatch, qw):
+    """The bias band's wave-private slots: BASELINE config 4 on the fast
+    kernel with either workgroup shape."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_QW", str(qw))
+    cfg = I.RELPOS_CONFIG
+    q, k, v, table = (t.to(DEV) for t in I.relpos_inputs(**cfg, seed=1))
+    fast, serial = (_run_table(lib, q, k, v, table) for lib in libs)
+    assert torch.isfinite(fast).all()
+    assert torch.equal(fast, serial)
