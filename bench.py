@@ -383,7 +383,7 @@ SWEEP_ORDER = ["fa2_config1"] + [f"fa2_n{n}{s}" for n in (128, 256, 512, 1024, 2
 KERNEL_OF = {  # device kernel each sweep row's time is dominated by (for readers)
     "fa2_f32_qkv": "fa2_fwd_kernel (F32IN: 3 fp16 MFMAs per product)",
     "fa2_f32_qkv_d128": "fa2_fwd_kernel (F32IN, 32-key blocks)",
-    "relpos": "fa2_fwd_kernel (BIAS = f32 table)",
+    "relpos": "fa2_fast_kernel (BIAS: f32 table band in the score accumulator; QW = 2, KSPLIT = 4)",
     "relpos_precompute": "relpos_precompute_kernel (fp16 hi/lo MFMA; HBM-bound, hbm_frac)",
     "w8a16": "w8a16_gemm_kernel", "w8a16_scaled": "w8a16_gemm_kernel",
     "w4a16_m16": "w4a16_skinny_lds_kernel", "w4a16_m256": "w4a16_tile_gemm_kernel",
@@ -451,7 +451,7 @@ def main():
         "roofline": {"bound": "mfma", "achieved": tflops, "peak": MFMA_F16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("fa2_headline"),
-                     "kernel": "fa2_fast_kernel<64,false,false,2,false,false>",
+                     "kernel": "fa2_fast_kernel<64,false,false,2,false,false,4,false>",
                      "algorithmic_flop_per_launch": flop,
                      "peak_box": peak_box},
     }

@@ -257,8 +257,9 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) koff[ks] = krow * D + 8 * ((2 * ks + g) ^ kswz<D>(krow));
 
-  // Bias band of block i (BIAS): entry j of the wave's band slot i % 2 is
-  // table[h][qw0 - kb0 - (KB - 1) + N - 1 + j] in score units (t / |scale|),
+  // Bias band of block i (BIAS): entry j, at position 63 - j of the wave's
+  // band slot i % 2, is table[h][qw0 - kb0 - (KB - 1) + N - 1 + j] in score
+  // units (t / |scale|),
   // the entries of this wave's 32 queries against the block's keys (indices
   // past the table read as zero; they meet only keys or queries past N).
   // One entry per lane is loaded into a register with the block's K and V
@@ -275,16 +276,19 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     return buf_load_f32(rsT, (uint32_t)(qw0 - kb0 - (kKB - 1) + N - 1 + lane) * 4u);
   };
   auto band_store = [&](int i, float t) {
-    if constexpr (BIAS) band[64 * (i & 1) + lane] = t * tscale;
+    if constexpr (BIAS) band[64 * (i & 1) + 63 - lane] = t * tscale;
   };
   // Initial score accumulator of block i: register r of lane (ql, g) is key
-  // 16 (r / 8) + 8 g + r % 8 of the block, band entry ql - key + KB - 1.
+  // 16 (r / 8) + 8 g + r % 8 of the block, band entry ql - key + KB - 1 at
+  // position 64 - KB - ql + key: consecutive registers read consecutive
+  // positions (pairs of them per ds_read2_b32, straight into the
+  // accumulator registers).
   auto band_acc = [&](int i) {
     float16v a;
     if constexpr (BIAS) {
-      const float* b = band + 64 * (i & 1) + ql + (kKB - 1) - 8 * g;
+      const float* b = band + 64 * (i & 1) + 64 - kKB - ql + 8 * g;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) a[r] = b[-(16 * (r >> 3) + (r & 7))];
+      for (int r = 0; r < 16; ++r) a[r] = b[16 * (r >> 3) + (r & 7)];
     } else {
       a = float16v{};
     }
@@ -817,18 +821,18 @@ bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid, b
   // On a small grid (128-query workgroups <= half the compute units) from
   // N = 512 it runs 64-query workgroups (two query waves, four key groups
   // at d = 64, two at d = 128), ahead of the generic kernel's 64-query
-  // workgroups by 8-29% (H8 N1500 d64 13.0 vs 15.0 us, H16 N1024 d128 16.3
-  // vs 22.8, H4 N2048 d64 causal 15.9 vs 18.5, rel-pos table H8 N1500 d64
-  // 15.0 vs 16.6, d128 25.0 vs 35.7).  A bias table on a larger grid stays
-  // on the generic kernel, whose 64-key blocks keep it ahead of the fast
-  // kernel's 32-key biased blocks (H16 N2048 d64: 29.4 vs 30.6 us).
+  // workgroups by 10-36% (H8 N1500 d64 13.0 vs 15.0 us, H16 N1024 d128
+  // 16.3 vs 22.8, H4 N2048 d64 causal 15.9 vs 18.5, rel-pos table H8 N1500
+  // d64 14.2 vs 16.6, d128 23.0 vs 35.7).  With the bias table it is ahead
+  // on larger grids too, with 128-query workgroups (H16 N2048 d64: 29.2 vs
+  // 30.9 us).
   (void)head_dim;
-  if (bias) return small_grid;
+  if (bias) return true;
   return !causal || N >= 1024;
 }
 
-// Query waves of the fast kernel: two on a small grid from N = 512 (and
-// for every biased call, which takes the fast kernel on small grids only).
+// Query waves of the fast kernel: two on a small grid, from N = 512
+// without a bias.
 int fa2_fast_qwaves(bool small_grid, int32_t N, bool bias) {
   return small_grid && (bias || N >= 512) ? 2 : 4;
 }

@@ -133,7 +133,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred): without a bias, and with the f32 bias table (BIAS, |scale| >= 1e-20) on grids whose 128-query workgroups fill at most half the CUs; KSPLIT key groups of QW query waves (QW = 2 on such small grids from N = 512 and for the bias table, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -160,7 +160,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -295,7 +295,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -410,7 +410,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred): without a bias, and with the f32 bias table (BIAS, |scale| >= 1e-20) on grids whose 128-query workgroups fill at most half the CUs; KSPLIT key groups of QW query waves (QW = 2 on such small grids from N = 512 and for the bias table, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -437,7 +437,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -576,7 +576,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred): without a bias, and with the f32 bias table (BIAS, |scale| >= 1e-20) on grids whose 128-query workgroups fill at most half the CUs; KSPLIT key groups of QW query waves (QW = 2 on such small grids from N = 512 and for the bias table, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -603,7 +603,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -752,7 +752,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128 where measured faster than fa2_fwd_kernel (fa2_fast_preferred): without a bias, and with the f32 bias table (BIAS, |scale| >= 1e-20) on grids whose 128-query workgroups fill at most half the CUs; KSPLIT key groups of QW query waves (QW = 2 on such small grids from N = 512 and for the bias table, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -779,7 +779,7 @@ constexpr char kManifest[] = R"JSON({
       "F32IN",
       "QW"
      ],
-     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) on larger grids or with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
+     "when": "every other FA2 call: the dense f16 bias (BIAS 2), the f32 table (BIAS 1) with |scale| < 1e-20, fp32 input (F32IN), head_dim 32, and unbiased shapes where it is measured faster; QW query waves (2 on grids that fill at most half the CUs) and KSPLIT key groups per workgroup",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [

@@ -179,9 +179,9 @@ CHOICE_CASES = [
     # CUs, so the biased fast kernel runs 64-query workgroups, 4 key groups.
     ("neso_rel_pos_fa2_fwd", [_P] * 5 + [1500, 64, 0.125, 1500 * 64, 2999, 8, 64, 1, 1],
      "fa2_fast_kernel", dict(D=64, QW=2, KSPLIT=4, BIAS=1)),
-    # A larger biased grid stays on the generic kernel.
+    # A larger biased grid: 128-query workgroups.
     ("neso_rel_pos_fa2_fwd", [_P] * 5 + [8192, 64, 0.125, 8192 * 64, 16383, 16, 64, 1, 1],
-     "fa2_fwd_kernel", dict(BIAS=1)),
+     "fa2_fast_kernel", dict(QW=4, KSPLIT=1, BIAS=1)),
     # A scale whose reciprocal could overflow the band: generic kernel.
     ("neso_rel_pos_fa2_fwd", [_P] * 5 + [1500, 64, 1e-30, 1500 * 64, 2999, 8, 64, 1, 1],
      "fa2_fwd_kernel", dict(BIAS=1)),
