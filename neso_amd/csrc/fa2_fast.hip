@@ -44,31 +44,39 @@ namespace {
 constexpr float kPSumMax = 4096.f;  // fast-path bound on a lane's block sum of P
 constexpr float kLog2e = 1.4426950408889634f;
 
-// Keys per block.  64 for head_dim 64 with four query waves: a block step
-// then carries 16 MFMAs per wave (8 for its scores, 8 for its P V) and a
-// K + V slot is 16 KiB, so two key groups of four slots fit in LDS.  32 for
-// head_dim 128 (16 MFMAs, 16 KiB), and for two query waves or a bias table
-// at head_dim 64 (8 MFMAs, 8 KiB): two query waves run four key groups,
-// and the bias band of a 32-key block is 63 entries, one per lane.
+// Keys per block: 64 at head_dim 64, 32 at head_dim 128, so that a block
+// step carries 16 MFMAs per wave (8 for its scores, 8 for its P V), and 32
+// for the bias table with four query waves (whose band of 32 + KB - 1
+// entries is then one per lane).
 template <int D, int QW, bool BIAS>
 constexpr int fast_kb() {
-  return (D == 128 || QW == 2 || BIAS) ? 32 : 64;
+  return (D == 128 || (BIAS && QW == 4)) ? 32 : 64;
 }
 
-// LDS halves of one key group: a 4-slot ring, each slot K [KB][D] then
-// V [KB][D], both row-major with 16-byte chunks swizzled (no padding: the
-// blocks arrive by LDS-direct loads, which fill LDS linearly).
+// LDS halves of one key group's K and V tiles, both row-major with 16-byte
+// chunks swizzled (no padding: the blocks arrive by LDS-direct loads, which
+// fill LDS linearly).  Four query waves: a 4-slot ring, each slot K [KB][D]
+// then V [KB][D].  Two query waves: two K slots and two V slots (the scores
+// stay in registers for the slow path, so a block's K is free once its
+// scores are formed, and its V is loaded one step before its P V).
 constexpr int kSlots = 4;
 template <int D, int QW, bool BIAS>
 constexpr int fast_group_lds_halves() {
-  return kSlots * 2 * fast_kb<D, QW, BIAS>() * D;
+  return (QW == 2 ? 4 : kSlots * 2) * fast_kb<D, QW, BIAS>() * D;
 }
 
-// Bytes of LDS of one workgroup: the key groups' rings, and with a bias
-// two 64-entry band slots per wave.
+// Bias band slot of one wave: the band's 32 + KB - 1 entries, rounded up.
+template <int D, int QW, bool BIAS>
+constexpr int fast_band_slot() {
+  return fast_kb<D, QW, BIAS>() == 64 ? 128 : 64;
+}
+
+// Bytes of LDS of one workgroup: the key groups' tiles, and with a bias two
+// band slots per wave.
 template <int D, int QW, bool BIAS>
 constexpr int fast_lds_bytes(int ksplit) {
-  return ksplit * (fast_group_lds_halves<D, QW, BIAS>() * 2 + (BIAS ? QW * 2 * 64 * 4 : 0));
+  return ksplit * (fast_group_lds_halves<D, QW, BIAS>() * 2 +
+                   (BIAS ? QW * 2 * fast_band_slot<D, QW, BIAS>() * 4 : 0));
 }
 
 // Debug build (NESO_FA2_SERIAL_LDS): every LDS phase ends in a full wait and
@@ -113,10 +121,14 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   constexpr int CPR = D / 8;      // 16-byte chunks per K/V row
   constexpr int RPI = 64 / CPR;   // rows per 1 KiB load instruction
   static_assert(LCH >= 1 && kKB * D * 2 == QW * LCH * 1024 && RPI * D == 512, "tile split");
-  static_assert(!BIAS || NT == 1, "one 32-key tile per biased block");
+  // Two query waves: K and V rings of two slots, scores kept for the slow
+  // path (see fast_group_lds_halves).
+  constexpr bool kLive = QW == 2;
+  constexpr int BSLOT = fast_band_slot<D, QW, BIAS>();
+  static_assert(!BIAS || 32 + kKB - 1 <= 2 * 64, "two band entries per lane");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
-  // Bias band: two slots of 64 entries per wave (its own, no barrier).
-  __shared__ float sband[BIAS ? KSPLIT * QW * 2 * 64 : 1];
+  // Bias band: two slots per wave (its own, no barrier).
+  __shared__ float sband[BIAS ? KSPLIT * QW * 2 * BSLOT : 1];
 
   const int tid = threadIdx.x;
   const int kg = __builtin_amdgcn_readfirstlane(tid / kGroup);  // key group
@@ -204,8 +216,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   }
 
   half_t* gbase = &smem[kg * GLDS];
-  auto kslot = [&](int s) { return gbase + s * (KSLOT + VSLOT); };
-  auto vslot = [&](int s) { return gbase + s * (KSLOT + VSLOT) + KSLOT; };
+  // Four query waves: slot s of the ring holds K then V.  Two: K slots 0
+  // and 1, then V slots 0 and 1.
+  auto kslot = [&](int s) { return kLive ? gbase + s * KSLOT : gbase + s * (KSLOT + VSLOT); };
+  auto vslot = [&](int s) {
+    return kLive ? gbase + 2 * KSLOT + s * VSLOT : gbase + s * (KSLOT + VSLOT) + KSLOT;
+  };
 
   // Global -> LDS directly (buffer_load_dwordx4 ... lds).  One instruction
   // fills 1 KiB of LDS, lane l's 16 bytes at byte 16 l, i.e. RPI rows of a
@@ -219,6 +235,18 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     kgo[j] = (row * p.stride_kv + 8 * (pos ^ kswz<D>(row))) * 2;
     vgo[j] = (row * p.stride_kv + 8 * (pos ^ vswz<D>(row))) * 2;
   }
+  // Block i's K (or V) tile alone into its slot (two query waves).
+  auto tile_load = [&](int i, bool v) {
+    const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
+    const uint32_t bytes = __builtin_amdgcn_readfirstlane(max(0, min(N - kb0, kKB)) * p.stride_kv * 2);
+    const rsrc_t r = make_rsrc((v ? Vh : Kh) + (int64_t)kb0 * p.stride_kv, bytes);
+    half_t* const base = v ? vslot(i & 1) : kslot(i & 1);
+#pragma unroll
+    for (int j = 0; j < LCH; ++j) {
+      const int x = LCH * wave + j;
+      lds_dma16(r, __builtin_amdgcn_readfirstlane(lds_addr(base + x * RPI * D)), v ? vgo[j] : kgo[j]);
+    }
+  };
   auto lds_load = [&](int i, int s) {
     const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
     // readfirstlane: min/max of scalars may be formed on the VALU, and a
@@ -257,36 +285,50 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) koff[ks] = krow * D + 8 * ((2 * ks + g) ^ kswz<D>(krow));
 
-  // Bias band of block i (BIAS): entry j, at position 63 - j of the wave's
-  // band slot i % 2, is table[h][qw0 - kb0 - (KB - 1) + N - 1 + j] in score
-  // units (t / |scale|),
-  // the entries of this wave's 32 queries against the block's keys (indices
-  // past the table read as zero; they meet only keys or queries past N).
-  // One entry per lane is loaded into a register with the block's K and V
-  // (step i - 2) and stored after that step's wait; the block's scores (step
-  // i - 1) and its slow path (step i) read their 16 entries per lane from
-  // the slot, which is rewritten for block i + 2 at the end of step i.
+  // Bias band of block i (BIAS): entry j < 32 + KB - 1, at position
+  // BSLOT - 1 - j of the wave's band slot i % 2, is table[h][qw0 - kb0 -
+  // (KB - 1) + N - 1 + j] in score units (t / |scale|), the entries of this
+  // wave's 32 queries against the block's keys (indices past the table read
+  // as zero; they meet only keys or queries past N).  Lane l loads entries
+  // l and l + 64 into registers with the block's K (step i - 2) and stores
+  // them after that step's wait.  The block's scores (step i - 1) read
+  // their 16 NT entries per lane from the slot, and so does its slow path
+  // (step i) with four query waves; the slot is rewritten for block i + 2
+  // at the end of step i.
+  constexpr int BENT = 32 + kKB - 1;  // band entries per block
   const float* Th = BIAS ? static_cast<const float*>(p.bias) + (int64_t)bh * p.bias_stride_h : nullptr;
   const rsrc_t rsT = make_rsrc(Th, BIAS ? (uint32_t)(2 * N - 1) * 4u : 0u);
   const float tscale = kLog2e / c;  // c (s + t tscale) = c s + t log2(e)
-  float* const band = &sband[BIAS ? (kg * QW + wave) * 128 : 0];
-  auto band_load = [&](int i) -> float {
-    if constexpr (!BIAS) return 0.f;
-    const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
-    return buf_load_f32(rsT, (uint32_t)(qw0 - kb0 - (kKB - 1) + N - 1 + lane) * 4u);
+  float* const band = &sband[BIAS ? (kg * QW + wave) * 2 * BSLOT : 0];
+  struct BandRegs {
+    float t[BENT > 64 ? 2 : 1];
   };
-  auto band_store = [&](int i, float t) {
-    if constexpr (BIAS) band[64 * (i & 1) + 63 - lane] = t * tscale;
+  auto band_load = [&](int i) {
+    BandRegs r{};
+    if constexpr (BIAS) {
+      const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
+      const uint32_t j0 = (uint32_t)(qw0 - kb0 - (kKB - 1) + N - 1 + lane);
+      r.t[0] = buf_load_f32(rsT, j0 * 4u);
+      if constexpr (BENT > 64) r.t[1] = buf_load_f32(rsT, (j0 + 64u) * 4u);
+    }
+    return r;
   };
-  // Initial score accumulator of block i: register r of lane (ql, g) is key
-  // 16 (r / 8) + 8 g + r % 8 of the block, band entry ql - key + KB - 1 at
-  // position 64 - KB - ql + key: consecutive registers read consecutive
-  // positions (pairs of them per ds_read2_b32, straight into the
-  // accumulator registers).
-  auto band_acc = [&](int i) {
+  auto band_store = [&](int i, const BandRegs& r) {
+    if constexpr (BIAS) {
+      float* const slot = band + BSLOT * (i & 1) + BSLOT - 1;
+      slot[-lane] = r.t[0] * tscale;
+      if constexpr (BENT > 64) slot[-(lane + 64)] = r.t[1] * tscale;  // within the slot
+    }
+  };
+  // Initial score accumulator of 32-key tile t of block i: register r of
+  // lane (ql, g) is key 32 t + 16 (r / 8) + 8 g + r % 8 of the block, band
+  // entry ql - key + KB - 1 at position BSLOT - KB - ql + key: consecutive
+  // registers read consecutive positions (pairs of them per ds_read2_b32,
+  // straight into the accumulator registers).
+  auto band_acc = [&](int i, int t) {
     float16v a;
     if constexpr (BIAS) {
-      const float* b = band + 64 * (i & 1) + 64 - kKB - ql + 8 * g;
+      const float* b = band + BSLOT * (i & 1) + BSLOT - kKB - ql + 8 * g + 32 * t;
 #pragma unroll
       for (int r = 0; r < 16; ++r) a[r] = b[16 * (r >> 3) + (r & 7)];
     } else {
@@ -301,7 +343,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       s[t] = mfma32x32x16(load_half8(k_l + koff[0] + 32 * t * D), qf[0],
-                          BIAS ? band_acc(i) : float16v{});
+                          BIAS ? band_acc(i, t) : float16v{});
 #pragma unroll
       for (int ks = 1; ks < KS; ++ks)
         s[t] = mfma32x32x16(load_half8(k_l + koff[ks] + 32 * t * D), qf[ks], s[t]);
@@ -368,8 +410,10 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       const int cc = sc / 8;
       return s[cc >> 1][8 * (cc & 1) + sc % 8];
     };
-    float16v binit;  // bias band of block inext, read ahead of the K fragments
-    if constexpr (BIAS) binit = band_acc(inext);
+    float16v binit[NT];  // bias band of block inext, read ahead of the K fragments
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+      if constexpr (BIAS) binit[t] = band_acc(inext, t);
     half8v fr[NJ];
 #pragma unroll
     for (int j = 0; j < AHEAD; ++j) fr[j] = frag(j);
@@ -394,7 +438,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       if (j % 2 == 0) {
         const int t = q % NT, ks = q / NT;
         if constexpr (BIAS)
-          sn[t] = mfma32x32x16(fr[j], qf[ks], ks == 0 ? binit : sn[t]);
+          sn[t] = mfma32x32x16(fr[j], qf[ks], ks == 0 ? binit[t] : sn[t]);
         else
           sn[t] = mfma32x32x16(fr[j], qf[ks], ks == 0 ? float16v{} : sn[t]);
       } else {
@@ -484,16 +528,48 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       for (int cc = 0; cc < 2 * NT; ++cc) o[u] = mfma32x32x16(vfrag(v_l, u, cc), pb[cc], o[u]);
   };
 
-  // One block step i: loads of block i+2 straight into its LDS slot, then
-  // scores of block i+1 into sn, softmax of block i (scores in s, P into
-  // pcur) and P V of block i-1 (P in pprev) in the fused stretch, then a
-  // wait for the loads and the barrier that publishes block i+2.  Block j
-  // lives in LDS slot j % 4, so the four blocks a step touches (i-1, i, i+1,
-  // i+2) never share one; slot (i+2) % 4 last served block i-2, whose P V
-  // ran in step i-1.
+  // One block step i: loads straight into LDS slots, then scores of block
+  // i+1 into sn, softmax of block i (scores in s, P into pcur) and P V of
+  // block i-1 (P in pprev) in the fused stretch, then a wait for the loads
+  // and the barrier that publishes them.
+  // Four query waves: block j lives in ring slot j % 4 and is loaded in step
+  // j - 2, so the four blocks a step touches (i-1, i, i+1, i+2) never share
+  // a slot; slot (i+2) % 4 last served block i-2, whose P V ran in step i-1.
+  // Two query waves: step i loads K of block i+2 into K slot i % 2, whose
+  // block i had its scores formed in step i-1 (the slow path of block i
+  // uses those scores, kept in s), and V of block i into V slot i % 2, whose
+  // block i-2 had its P V in step i-1.
   auto body = [&](int i, float16v(&s)[NT], float16v(&sn)[NT], half8v(&pprev)[2 * NT],
                   half8v(&pcur)[2 * NT]) {
-    float bload = 0.f;  // bias band entry of block i + 2
+    BandRegs bload{};  // bias band of block i + 2
+    if constexpr (kLive) {
+#ifdef NESO_FA2_SERIAL_LDS
+      // The debug build's barrier must be reached by every wave (my_n
+      // differs between key groups), so the loads are issued outside the
+      // branch.
+      if (i + 2 < my_n) {
+        tile_load(i + 2, false);
+        bload = band_load(i + 2);
+      }
+      if (i < my_n) tile_load(i, true);
+      serial_lds_point();
+      if (i < my_n) {
+#else
+      if (i < my_n) {
+        if (i + 2 < my_n) {
+          tile_load(i + 2, false);
+          bload = band_load(i + 2);
+        }
+        tile_load(i, true);
+#endif
+        const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
+        const bool masked =
+            (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
+        float ls = fused(s, sn, kslot((i + 1) & 1), vslot((i + 1) & 1), pprev, pcur, i + 1);
+        if (__any(masked || !(ls <= thr))) ls = slow_scores(s, kb0, masked, pcur);
+        l_run += ls;
+      }
+    } else {
 #ifdef NESO_FA2_SERIAL_LDS
     // The debug build's barrier must be reached by every wave (my_n differs
     // between key groups), so the loads are issued outside the branch.
@@ -532,6 +608,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       if (__any(masked || !(ls <= thr))) ls = slow(i, kb0, masked, pcur);
       l_run += ls;
     }
+    }
     // Steps past the group's last block load nothing: no later step reads
     // those blocks, and the last block's V (read by the P V after the loop)
     // stays in place.
@@ -541,38 +618,55 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     lds_barrier();
   };
 
-  // ---- prologue: blocks 0 and 1 into LDS in one round trip, scores of 0 ----
-  float bpro[3] = {0.f, 0.f, 0.f};  // bias band entries of blocks 0..2
+  // ---- prologue: blocks 0 and 1 into LDS in one round trip ----
+  BandRegs bpro[3] = {};  // bias bands of blocks 0..2
+  float16v sa[NT], sb[NT];
+  half8v pa[2 * NT], pb2[2 * NT];
   if (my_n > 0) {
-    lds_load(0, 0);
+    if constexpr (kLive)
+      tile_load(0, false);
+    else
+      lds_load(0, 0);
     bpro[0] = band_load(0);
   }
   if (my_n > 1) {
-    lds_load(1, 1);
+    if constexpr (kLive)
+      tile_load(1, false);
+    else
+      lds_load(1, 1);
     bpro[1] = band_load(1);
   }
   wait_vmem();
   band_store(0, bpro[0]);
   band_store(1, bpro[1]);
   lds_barrier();
-  float16v sa[NT], sb[NT];
-  half8v pa[2 * NT], pb2[2 * NT];
+  if constexpr (kLive) {
+    // Scores of blocks 0 and 1 before step 0 reloads K slot 0.
+    qk(sa, kslot(0), 0);
+    qk(sb, kslot(1), 1);
+    lds_barrier();
+  }
 
   // ---- step 0, peeled: block 0 is every row's first visible block, so its
   // softmax is the slow path on its exact scores; scores of block 1; loads
-  // of block 2.  (Scores of blocks a group does not have come from stale
-  // slots and are never used.) ----
+  // of block 2 (two query waves: K of block 2, V of block 0).  (Scores of
+  // blocks a group does not have come from stale slots and are never
+  // used.) ----
   if (my_n > 2) {
-    lds_load(2, 2);
+    if constexpr (kLive)
+      tile_load(2, false);
+    else
+      lds_load(2, 2);
     bpro[2] = band_load(2);
   }
+  if (kLive && my_n > 0) tile_load(0, true);
   serial_lds_point();
-  qk(sa, kslot(0), 0);
+  if constexpr (!kLive) qk(sa, kslot(0), 0);
   if (HALVES ? my_nw > 0 : my_n > 0) {
     const int kb0 = (blk0 + kg) * kKB;
     const bool masked =
         (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
-    qk(sb, kslot(1), 1);
+    if constexpr (!kLive) qk(sb, kslot(1), 1);
     l_run += slow_scores(sa, kb0, masked, pb2);
   }
   wait_vmem();
@@ -589,10 +683,11 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // when j is even, into pa when j is odd.  (A HALVES wave that stopped
   // before the group's last block has done its last P V in the loop.)
   if (HALVES ? my_nw > 0 && my_nw == my_n : my_n > 0) {
+    const int vs = (my_n - 1) & (kLive ? 1 : 3);
     if ((my_n - 1) & 1)
-      pv_only(pa, vslot((my_n - 1) & 3));
+      pv_only(pa, vslot(vs));
     else
-      pv_only(pb2, vslot((my_n - 1) & 3));
+      pv_only(pb2, vslot(vs));
   }
 
   // ---- merge the key groups through LDS ----
@@ -819,13 +914,12 @@ bool fa2_fast_preferred(bool causal, int32_t N, int head_dim, bool small_grid, b
   // (7-25%, growing with N); for shorter causal rows the generic kernel's
   // per-wave skipping of invisible blocks wins (N = 256: 8.1 vs 8.9 us).
   // On a small grid (128-query workgroups <= half the compute units) from
-  // N = 512 it runs 64-query workgroups (two query waves, four key groups
-  // at d = 64, two at d = 128), ahead of the generic kernel's 64-query
-  // workgroups by 10-36% (H8 N1500 d64 13.0 vs 15.0 us, H16 N1024 d128
-  // 16.3 vs 22.8, H4 N2048 d64 causal 15.9 vs 18.5, rel-pos table H8 N1500
-  // d64 14.2 vs 16.6, d128 23.0 vs 35.7).  With the bias table it is ahead
-  // on larger grids too, with 128-query workgroups (H16 N2048 d64: 29.2 vs
-  // 30.9 us).
+  // N = 512 it runs 64-query workgroups (two query waves), ahead of the
+  // generic kernel's 64-query workgroups by 14-40% (H8 N1500 d64 12.7 vs
+  // 15.1 us, H16 N1024 d128 16.5 vs 22.8, H4 N2048 d64 causal 15.0 vs 18.5,
+  // rel-pos table H8 N1500 d64 14.1 vs 16.6, d128 21.3 vs 35.8).  With the
+  // bias table it is ahead on larger grids too, with 128-query workgroups
+  // (H16 N2048 d64: 28.1 vs 29.8 us).
   (void)head_dim;
   if (bias) return true;
   return !causal || N >= 1024;

@@ -612,11 +612,17 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
       const int64_t pwgs = (int64_t)((a.num_qblocks + 1) / 2) * a.batch_heads;
       ksplit = pwgs < 2 * cus ? 2 : 1;
     }
-    // Small grids: 64-query workgroups (two query waves) with four key
-    // groups, which double the grid at eight waves each (head_dim 128 fits
-    // two key groups).
+    // Small grids: 64-query workgroups (two query waves).  Four key groups
+    // (eight waves, one workgroup per CU) while those workgroups fit the
+    // CUs in one round and each group still sees 4+ key blocks; two
+    // otherwise, where shorter rows make the split's prologue and merge
+    // cost more (measured, d = 64: H8 N1500 12.7 vs 13.4 us, rel-pos H8
+    // N2048 16.7 vs 18.3; H8 N512 7.3 vs 6.9).
     if (a.qwaves != 2 && a.qwaves != 4) a.qwaves = fa2_fast_qwaves(small, a.N, bias);
-    if (a.qwaves == 2 && a.ksplit <= 0) ksplit = 4;
+    if (a.qwaves == 2 && a.ksplit <= 0) {
+      const int64_t wgs64 = (int64_t)((a.N + 63) / 64) * a.batch_heads;
+      ksplit = (wgs64 <= cus && a.N >= 1024) ? 4 : 2;
+    }
     return launch_fa2_fast(a, head_dim, causal, bias, out_f16, ksplit, stream);
   }
   // Generic kernel on a small grid: 64-query workgroups (two query waves per

@@ -133,7 +133,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -143,9 +143,9 @@ constexpr char kManifest[] = R"JSON({
      ],
      "constants": {
       "block_m": "32 * QW",
-      "block_n": "64 if (D == 64 and QW == 4 and not BIAS) else 32",
-      "lds_ring_slots": "4",
-      "lds_bytes": "KSPLIT * (4 * 2 * (64 if (D == 64 and QW == 4 and not BIAS) else 32) * D * 2 + (QW * 512 if BIAS else 0))"
+      "block_n": "(32 if (D == 128 or (BIAS and QW == 4)) else 64)",
+      "lds_ring_slots": "4 (K and V together) if QW == 4 else 2 K + 2 V",
+      "lds_bytes": "KSPLIT * ((8 if QW == 4 else 4) * (32 if (D == 128 or (BIAS and QW == 4)) else 64) * D * 2 + (QW * 2 * (128 if (32 if (D == 128 or (BIAS and QW == 4)) else 64) == 64 else 64) * 4 if BIAS else 0))"
      }
     },
     {
@@ -410,7 +410,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -420,9 +420,9 @@ constexpr char kManifest[] = R"JSON({
      ],
      "constants": {
       "block_m": "32 * QW",
-      "block_n": "64 if (D == 64 and QW == 4 and not BIAS) else 32",
-      "lds_ring_slots": "4",
-      "lds_bytes": "KSPLIT * (4 * 2 * (64 if (D == 64 and QW == 4 and not BIAS) else 32) * D * 2 + (QW * 512 if BIAS else 0))"
+      "block_n": "(32 if (D == 128 or (BIAS and QW == 4)) else 64)",
+      "lds_ring_slots": "4 (K and V together) if QW == 4 else 2 K + 2 V",
+      "lds_bytes": "KSPLIT * ((8 if QW == 4 else 4) * (32 if (D == 128 or (BIAS and QW == 4)) else 64) * D * 2 + (QW * 2 * (128 if (32 if (D == 128 or (BIAS and QW == 4)) else 64) == 64 else 64) * 4 if BIAS else 0))"
      }
     },
     {
@@ -576,7 +576,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -586,9 +586,9 @@ constexpr char kManifest[] = R"JSON({
      ],
      "constants": {
       "block_m": "32 * QW",
-      "block_n": "64 if (D == 64 and QW == 4 and not BIAS) else 32",
-      "lds_ring_slots": "4",
-      "lds_bytes": "KSPLIT * (4 * 2 * (64 if (D == 64 and QW == 4 and not BIAS) else 32) * D * 2 + (QW * 512 if BIAS else 0))"
+      "block_n": "(32 if (D == 128 or (BIAS and QW == 4)) else 64)",
+      "lds_ring_slots": "4 (K and V together) if QW == 4 else 2 K + 2 V",
+      "lds_bytes": "KSPLIT * ((8 if QW == 4 else 4) * (32 if (D == 128 or (BIAS and QW == 4)) else 64) * D * 2 + (QW * 2 * (128 if (32 if (D == 128 or (BIAS and QW == 4)) else 64) == 64 else 64) * 4 if BIAS else 0))"
      }
     },
     {
@@ -752,7 +752,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 at head_dim 64 and 2 at 128); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -762,9 +762,9 @@ constexpr char kManifest[] = R"JSON({
      ],
      "constants": {
       "block_m": "32 * QW",
-      "block_n": "64 if (D == 64 and QW == 4 and not BIAS) else 32",
-      "lds_ring_slots": "4",
-      "lds_bytes": "KSPLIT * (4 * 2 * (64 if (D == 64 and QW == 4 and not BIAS) else 32) * D * 2 + (QW * 512 if BIAS else 0))"
+      "block_n": "(32 if (D == 128 or (BIAS and QW == 4)) else 64)",
+      "lds_ring_slots": "4 (K and V together) if QW == 4 else 2 K + 2 V",
+      "lds_bytes": "KSPLIT * ((8 if QW == 4 else 4) * (32 if (D == 128 or (BIAS and QW == 4)) else 64) * D * 2 + (QW * 2 * (128 if (32 if (D == 128 or (BIAS and QW == 4)) else 64) == 64 else 64) * 4 if BIAS else 0))"
      }
     },
     {

@@ -191,11 +191,13 @@ CHOICE_CASES = [
     # The headline: 128-query workgroups, two key groups.
     ("neso_flash_attention_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 16, 2048 * 64, 2048 * 64, 0],
      "fa2_fast_kernel", dict(QW=4, KSPLIT=2, PAIR=0, HALVES=0, BIAS=0)),
-    # Small grids from N = 512: two query waves (four key groups at d = 64,
-    # two at d = 128, where four do not fit the LDS).
+    # Small grids from N = 512: two query waves; four key groups while the
+    # 64-query workgroups fit the CUs and N >= 1024.
     ("neso_flash_attention_fwd", [_P] * 4 + [1500, 64, 64, 0.125, 64, 8, 1500 * 64, 1500 * 64, 0],
      "fa2_fast_kernel", dict(QW=2, KSPLIT=4)),
     ("neso_flash_attention_fwd", [_P] * 4 + [1024, 128, 128, 0.08, 128, 16, 1024 * 128, 1024 * 128, 0],
+     "fa2_fast_kernel", dict(QW=2, KSPLIT=4)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [512, 64, 64, 0.125, 64, 8, 512 * 64, 512 * 64, 0],
      "fa2_fast_kernel", dict(QW=2, KSPLIT=2)),
     ("neso_flash_attention_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 4, 2048 * 64, 2048 * 64, 1],
      "fa2_fast_kernel", dict(QW=2, KSPLIT=4, CAUSAL=1, HALVES=0)),
