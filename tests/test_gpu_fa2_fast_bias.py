@@ -2,11 +2,12 @@
 bias table, against the CPU oracle.
 
 ``NESO_AMD_FA2_FAST=2`` forces the fast kernel, ``NESO_AMD_FA2_QW`` its
-query waves per key group (2: 64-query workgroups, 32-key blocks) and
-``NESO_AMD_FA2_KSPLIT`` its key groups (1, 2, and 4 with two query waves;
-d = 128 with two query waves falls back to two key groups, four do not fit
-the LDS).  The table form carries the bias band of each 32-key block in the
-initial accumulator of the score MFMAs, in score units (t / |scale|).
+query waves per key group (2: 64-query workgroups with two K and two V LDS
+slots per key group and the scores kept in registers for the slow path)
+and ``NESO_AMD_FA2_KSPLIT`` its key groups (1, 2, and 4 with two query
+waves).  The table form carries the bias band of each block in the initial
+accumulator of the score MFMAs, in score units (t / |scale|): 32-key blocks
+with four query waves, 64-key blocks (two bands per lane) with two.
 Bar: max abs error <= 2e-3 against the fp32 CPU oracle
 (tests/test_rel_pos_fa2.py:155-253 for the biased softmax).
 """
@@ -60,6 +61,22 @@ def test_two_query_waves(gpu, fast, ksplit, causal, d, n):
     assert (out - ref).abs().max().item() <= TOL
 
 
+@pytest.mark.parametrize("ksplit", [None, 2, 4])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("n,wl,wr", [(7, 2, 1), (300, 100, 37), (300, 5, 290), (1500, 128, 128)])
+def test_two_query_waves_windows(gpu, fast, ksplit, d, n, wl, wr):
+    """Sliding windows on 64-query workgroups: blocks partly outside some
+    query's window take the slow path on the scores kept in registers."""
+    fast(2, ksplit)
+    heads = 2
+    q, k, v = (t[0].permute(1, 0, 2).contiguous() for t in I.fa2_inputs(1, heads, n, d, seed=n + d))
+    out = neso_amd.window_attention(q.to(DEV), k.to(DEV), v.to(DEV), wl, wr,
+                                    out_dtype=torch.float32).cpu()
+    qh, kh, vh = (t.permute(1, 0, 2) for t in (q, k, v))
+    ref = A.attention(qh, kh, vh, 1 / math.sqrt(d), window=(wl, wr)).permute(1, 0, 2)
+    assert (out - ref).abs().max().item() <= TOL
+
+
 @pytest.mark.parametrize("qw,ksplit", [(2, None), (2, 1), (2, 2), (4, None), (4, 1), (4, 2)])
 @pytest.mark.parametrize("h,n,d", [(8, 1500, 64), (2, 129, 128), (1, 1, 64), (3, 37, 64),
                                    (2, 31, 64), (2, 33, 128), (1, 1023, 64), (2, 2048, 128)])
@@ -84,8 +101,9 @@ def test_rel_pos_table_fp16_out(gpu, fast, qw):
 def test_rel_pos_rescale_path(gpu, fast, qw, ksplit):
     """A table that grows by 0.05 per key of distance: every row's logits
     rise by ~1.6 (log2 units ~2.3) per 32-key block, so blocks past the
-    lazy bound take the slow path (exact row max, O and l rescaled, scores
-    recomputed from LDS with the band again)."""
+    lazy bound take the slow path (exact row max, O and l rescaled; with
+    four query waves the scores are recomputed from LDS with the band
+    again, with two the kept scores are reused)."""
     fast(qw, ksplit)
     h, n, d = 2, 1200, 64
     q, k, v, _ = I.relpos_inputs(h, n, d, seed=2)
