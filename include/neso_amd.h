@@ -101,7 +101,7 @@ int neso_flash_attention_fwd(const void* Q, const void* K, const void* V, float*
  * same buffer order as above).  Parameters as neso_flash_attention_fwd,
  * except:
  *   Q, K, V   fp32 rows; strides and slice strides multiples of 4 elements
- *   head_dim  32 or 64
+ *   head_dim  32, 64 or 128
  * Each fp32 operand is split into fp16 hi + lo and every product is formed
  * as hi*hi + hi*lo + lo*hi on the fp16 MFMA with fp32 accumulation, as is P
  * for P V, so results track an fp32 computation (about 1e-6 absolute for
