@@ -44,39 +44,54 @@ namespace {
 constexpr float kPSumMax = 4096.f;  // fast-path bound on a lane's block sum of P
 constexpr float kLog2e = 1.4426950408889634f;
 
-// Keys per block: 64 at head_dim 64, 32 at head_dim 128, so that a block
-// step carries 16 MFMAs per wave (8 for its scores, 8 for its P V), and 32
-// for the bias table with four query waves (whose band of 32 + KB - 1
-// entries is then one per lane).
-template <int D, int QW, bool BIAS>
-constexpr int fast_kb() {
-  return (D == 128 || (BIAS && QW == 4)) ? 32 : 64;
+// LDS layout of a key group's K and V tiles, both row-major with 16-byte
+// chunks swizzled (no padding: the blocks arrive by LDS-direct loads, which
+// fill LDS linearly).
+// * Ring: a 4-slot ring, each slot K [KB][D] then V [KB][D].
+// * Live: two K slots and two V slots.  The scores of a block stay in
+//   registers for its slow path, so a block's K is free once its scores are
+//   formed, and its V is loaded one step before its P V.  Used by every
+//   two-query-wave kernel, and at head_dim 128 with four query waves
+//   (without a bias or 64-row halves), where it fits 64-key blocks; not
+//   for paired blocks with one key group, whose 276 registers per wave
+//   leave one workgroup per CU (measured, B2 H32 N4096 causal: 360 against
+//   341 us in the ring; other d = 128 shapes 2-6% faster in this layout).
+template <int D, int QW, bool BIAS, bool HALVES, bool PAIR, int K>
+constexpr bool fast_live() {
+  return QW == 2 || (D == 128 && !BIAS && !HALVES && !(PAIR && K == 1));
 }
 
-// LDS halves of one key group's K and V tiles, both row-major with 16-byte
-// chunks swizzled (no padding: the blocks arrive by LDS-direct loads, which
-// fill LDS linearly).  Four query waves: a 4-slot ring, each slot K [KB][D]
-// then V [KB][D].  Two query waves: two K slots and two V slots (the scores
-// stay in registers for the slow path, so a block's K is free once its
-// scores are formed, and its V is loaded one step before its P V).
+// Keys per block: 64 at head_dim 64 and 32 at head_dim 128 in the ring, so
+// that a block step carries 16 MFMAs per wave (8 for its scores, 8 for its
+// P V); 64 at head_dim 128 in the live layout with four query waves (32
+// MFMAs per step: half the steps, and half their barriers and pipeline
+// fills); 32 for the bias table with four query waves (whose band of
+// 32 + KB - 1 entries is then one per lane).
+template <int D, int QW, bool BIAS, bool HALVES, bool PAIR, int K>
+constexpr int fast_kb() {
+  if (D == 128) return (QW == 4 && fast_live<D, QW, BIAS, HALVES, PAIR, K>()) ? 64 : 32;
+  return (BIAS && QW == 4) ? 32 : 64;
+}
+
 constexpr int kSlots = 4;
-template <int D, int QW, bool BIAS>
+template <int D, int QW, bool BIAS, bool HALVES, bool PAIR, int K>
 constexpr int fast_group_lds_halves() {
-  return (QW == 2 ? 4 : kSlots * 2) * fast_kb<D, QW, BIAS>() * D;
+  return (fast_live<D, QW, BIAS, HALVES, PAIR, K>() ? 4 : kSlots * 2) *
+         fast_kb<D, QW, BIAS, HALVES, PAIR, K>() * D;
 }
 
 // Bias band slot of one wave: the band's 32 + KB - 1 entries, rounded up.
-template <int D, int QW, bool BIAS>
+template <int D, int QW, bool BIAS, bool HALVES, bool PAIR, int K>
 constexpr int fast_band_slot() {
-  return fast_kb<D, QW, BIAS>() == 64 ? 128 : 64;
+  return fast_kb<D, QW, BIAS, HALVES, PAIR, K>() == 64 ? 128 : 64;
 }
 
 // Bytes of LDS of one workgroup: the key groups' tiles, and with a bias two
 // band slots per wave.
-template <int D, int QW, bool BIAS>
-constexpr int fast_lds_bytes(int ksplit) {
-  return ksplit * (fast_group_lds_halves<D, QW, BIAS>() * 2 +
-                   (BIAS ? QW * 2 * fast_band_slot<D, QW, BIAS>() * 4 : 0));
+template <int D, int QW, bool BIAS, bool HALVES, bool PAIR, int K>
+constexpr int fast_lds_bytes() {
+  return K * (fast_group_lds_halves<D, QW, BIAS, HALVES, PAIR, K>() * 2 +
+              (BIAS ? QW * 2 * fast_band_slot<D, QW, BIAS, HALVES, PAIR, K>() * 4 : 0));
 }
 
 // Debug build (NESO_FA2_SERIAL_LDS): every LDS phase ends in a full wait and
@@ -110,21 +125,21 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   static_assert(!BIAS || !CAUSAL, "the biased entry point is never masked");
   constexpr int kBMq = 32 * QW;      // queries per workgroup
   constexpr int kGroup = 64 * QW;    // threads per key group
-  constexpr int kKB = fast_kb<D, QW, BIAS>();  // keys per block
+  constexpr int kKB = fast_kb<D, QW, BIAS, HALVES, PAIR, KSPLIT>();  // keys per block
   constexpr int NT = kKB / 32;  // 32-key tiles per block
   constexpr int KS = D / 16;    // k-steps of S^T = K Q^T
   constexpr int DT = D / 32;    // 32-row tiles of O^T
   constexpr int KSLOT = kKB * D;
   constexpr int VSLOT = kKB * D;
-  constexpr int GLDS = fast_group_lds_halves<D, QW, BIAS>();
+  constexpr int GLDS = fast_group_lds_halves<D, QW, BIAS, HALVES, PAIR, KSPLIT>();
   constexpr int LCH = kKB * D / 8 / 64 / QW;  // 1 KiB load instructions per wave and matrix
   constexpr int CPR = D / 8;      // 16-byte chunks per K/V row
   constexpr int RPI = 64 / CPR;   // rows per 1 KiB load instruction
   static_assert(LCH >= 1 && kKB * D * 2 == QW * LCH * 1024 && RPI * D == 512, "tile split");
-  // Two query waves: K and V rings of two slots, scores kept for the slow
-  // path (see fast_group_lds_halves).
-  constexpr bool kLive = QW == 2;
-  constexpr int BSLOT = fast_band_slot<D, QW, BIAS>();
+  // K and V slots of the live layout, scores kept for the slow path (see
+  // fast_live).
+  constexpr bool kLive = fast_live<D, QW, BIAS, HALVES, PAIR, KSPLIT>();
+  constexpr int BSLOT = fast_band_slot<D, QW, BIAS, HALVES, PAIR, KSPLIT>();
   static_assert(!BIAS || 32 + kKB - 1 <= 2 * 64, "two band entries per lane");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
   // Bias band: two slots per wave (its own, no barrier).
@@ -835,14 +850,16 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 // Launches with K key groups if their LDS fits (returns false otherwise).
 template <int D, bool CAUSAL, bool OUT_F16, int K, int QW, bool BIAS>
 bool launch_fast_k(const Fa2Args& a, hipStream_t stream, hipError_t& err) {
-  if constexpr (fast_lds_bytes<D, QW, BIAS>(K) <= 160 * 1024) {
-    if constexpr (CAUSAL && QW == 4) {
+  if constexpr (CAUSAL && QW == 4) {
+    if constexpr (fast_lds_bytes<D, QW, BIAS, false, true, K>() <= 160 * 1024) {
       if (a.pair_qblocks == 1) {
         err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, true>>(
             ktag("fa2_fast_kernel", D, true, OUT_F16, K, true, false, QW, BIAS),
             dim3((a.num_qblocks + 1) / 2 * a.batch_heads), dim3(K * 64 * QW), stream, a);
         return true;
       }
+    }
+    if constexpr (fast_lds_bytes<D, QW, BIAS, true, false, K>() <= 160 * 1024) {
       if (a.pair_qblocks == 2) {
         err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, false, true>>(
             ktag("fa2_fast_kernel", D, true, OUT_F16, K, false, true, QW, BIAS),
@@ -850,6 +867,8 @@ bool launch_fast_k(const Fa2Args& a, hipStream_t stream, hipError_t& err) {
         return true;
       }
     }
+  }
+  if constexpr (fast_lds_bytes<D, QW, BIAS, false, false, K>() <= 160 * 1024) {
     err = launch<&fa2_fast_kernel<D, CAUSAL, OUT_F16, K, false, false, QW, BIAS>>(
         ktag("fa2_fast_kernel", D, CAUSAL, OUT_F16, K, false, false, QW, BIAS),
         dim3(a.num_qblocks * a.batch_heads), dim3(K * 64 * QW), stream, a);

@@ -143,9 +143,9 @@ constexpr char kManifest[] = R"JSON({
      ],
      "constants": {
       "block_m": "32 * QW",
-      "block_n": "(32 if (D == 128 or (BIAS and QW == 4)) else 64)",
-      "lds_ring_slots": "4 (K and V together) if QW == 4 else 2 K + 2 V",
-      "lds_bytes": "KSPLIT * ((8 if QW == 4 else 4) * (32 if (D == 128 or (BIAS and QW == 4)) else 64) * D * 2 + (QW * 2 * (128 if (32 if (D == 128 or (BIAS and QW == 4)) else 64) == 64 else 64) * 4 if BIAS else 0))"
+      "block_n": "(64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32)",
+      "lds_layout": "2 K + 2 V slots (scores kept for the slow path) if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else a 4-slot ring of K + V",
+      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0))"
      }
     },
     {
@@ -420,9 +420,9 @@ constexpr char kManifest[] = R"JSON({
      ],
      "constants": {
       "block_m": "32 * QW",
-      "block_n": "(32 if (D == 128 or (BIAS and QW == 4)) else 64)",
-      "lds_ring_slots": "4 (K and V together) if QW == 4 else 2 K + 2 V",
-      "lds_bytes": "KSPLIT * ((8 if QW == 4 else 4) * (32 if (D == 128 or (BIAS and QW == 4)) else 64) * D * 2 + (QW * 2 * (128 if (32 if (D == 128 or (BIAS and QW == 4)) else 64) == 64 else 64) * 4 if BIAS else 0))"
+      "block_n": "(64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32)",
+      "lds_layout": "2 K + 2 V slots (scores kept for the slow path) if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else a 4-slot ring of K + V",
+      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0))"
      }
     },
     {
@@ -586,9 +586,9 @@ constexpr char kManifest[] = R"JSON({
      ],
      "constants": {
       "block_m": "32 * QW",
-      "block_n": "(32 if (D == 128 or (BIAS and QW == 4)) else 64)",
-      "lds_ring_slots": "4 (K and V together) if QW == 4 else 2 K + 2 V",
-      "lds_bytes": "KSPLIT * ((8 if QW == 4 else 4) * (32 if (D == 128 or (BIAS and QW == 4)) else 64) * D * 2 + (QW * 2 * (128 if (32 if (D == 128 or (BIAS and QW == 4)) else 64) == 64 else 64) * 4 if BIAS else 0))"
+      "block_n": "(64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32)",
+      "lds_layout": "2 K + 2 V slots (scores kept for the slow path) if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else a 4-slot ring of K + V",
+      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0))"
      }
     },
     {
@@ -762,9 +762,9 @@ constexpr char kManifest[] = R"JSON({
      ],
      "constants": {
       "block_m": "32 * QW",
-      "block_n": "(32 if (D == 128 or (BIAS and QW == 4)) else 64)",
-      "lds_ring_slots": "4 (K and V together) if QW == 4 else 2 K + 2 V",
-      "lds_bytes": "KSPLIT * ((8 if QW == 4 else 4) * (32 if (D == 128 or (BIAS and QW == 4)) else 64) * D * 2 + (QW * 2 * (128 if (32 if (D == 128 or (BIAS and QW == 4)) else 64) == 64 else 64) * 4 if BIAS else 0))"
+      "block_n": "(64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32)",
+      "lds_layout": "2 K + 2 V slots (scores kept for the slow path) if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else a 4-slot ring of K + V",
+      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0))"
      }
     },
     {
