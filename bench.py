@@ -16,7 +16,9 @@ The same line carries:
 
 * ``roofline`` for that kernel against dense-fp16 MFMA peak (2516.6 TFLOP/s
   = 256 CU x 2.4 GHz x 4096 FLOP/clk), with the HBM traffic per launch from
-  the committed counter summary;
+  the committed counter summary, and ``roofline.clock``: the shader clock
+  sampled during the median replays (the part lowers its clock under MFMA
+  load), the peak at that clock, and board power and clock after a 1 s soak;
 * ``cpu_baseline``: the CPU oracle (torch fp32, all host threads) on the
   same workload, with the host CPU model;
 * ``qmatmul``: the int4 qmatmul at M=1, K=4096, N=11008 in HBM GB/s
@@ -98,7 +100,7 @@ def capture(launch, n, torch):
     return graph
 
 
-def time_case(launch, steps, warmup, torch):
+def time_case(launch, steps, warmup, torch, power=False):
     """Per-launch timing of ``launch(i)``.
 
     Returns (ms per launch over exactly ``steps`` launches, timing dict).
@@ -106,7 +108,8 @@ def time_case(launch, steps, warmup, torch):
     the current stream (the graph replays on it), with device
     synchronisation on both sides.  The dict adds the median / p10 / p90
     over MEDIAN_REPLAYS separately timed replays of a GRAPH_LAUNCHES-launch
-    graph, and the eager (one-by-one from Python) rate.
+    graph (with the shader clock sampled during them), the eager (one-by-one
+    from Python) rate and, with ``power``, the board power after a 1 s soak.
     """
     for i in range(warmup):
         launch(i)
@@ -123,6 +126,8 @@ def time_case(launch, steps, warmup, torch):
     ev[1].record()
     torch.cuda.synchronize()
     ms = ev[0].elapsed_time(ev[1]) / steps
+    clock = ClockSampler(torch)
+    clock.start()  # one sleeping wave on a second stream during the replays below
     for r in range(MEDIAN_REPLAYS):
         ev[2 + 2 * r].record()
         g_small.replay()
@@ -138,12 +143,106 @@ def time_case(launch, steps, warmup, torch):
     ev[1].record()
     torch.cuda.synchronize()
     eager = ev[0].elapsed_time(ev[1]) / n_eager
-    return ms, {"graph_ms": round(ms, 6), "launches_timed": steps,
-                "median_ms": round(statistics.median(per), 6),
-                "p10_ms": round(per[len(per) // 10], 6),
-                "p90_ms": round(per[(9 * len(per)) // 10], 6),
-                "median_samples": MEDIAN_REPLAYS, "launches_per_sample": GRAPH_LAUNCHES,
-                "eager_ms": round(eager, 6)}
+    timing = {"graph_ms": round(ms, 6), "launches_timed": steps,
+              "median_ms": round(statistics.median(per), 6),
+              "p10_ms": round(per[len(per) // 10], 6),
+              "p90_ms": round(per[(9 * len(per)) // 10], 6),
+              "median_samples": MEDIAN_REPLAYS, "launches_per_sample": GRAPH_LAUNCHES,
+              "eager_ms": round(eager, 6),
+              "clock_mhz": clock.mhz()}
+    if power:
+        timing["power"] = board_power(g_small, torch)
+    return ms, timing
+
+
+class ClockSampler:
+    """Shader clock while the GPU runs other work: ``neso_clock_sample`` puts
+    one wave on a second stream that records (shader clock, 100 MHz reference
+    clock) pairs every 2 us for 2 ms.  ``start()`` before enqueueing the work,
+    ``mhz()`` after synchronising: the median over 20 us windows.  Under
+    MFMA-heavy load the part lowers its clock below the 2.4 GHz that the
+    published peak assumes."""
+
+    def __init__(self, torch, samples=1000, gap_ticks=200):
+        from neso_amd import _lib
+        self.lib, self.n, self.gap = _lib.load(), samples, gap_ticks
+        self.buf = torch.empty(2 * samples, dtype=torch.int64, device="cuda")
+        self.side = torch.cuda.Stream()
+        self.status = None
+
+    def start(self):
+        import ctypes
+        self.status = self.lib.neso_clock_sample(ctypes.c_void_p(self.buf.data_ptr()), self.n,
+                                                 self.gap, ctypes.c_void_p(self.side.cuda_stream))
+
+    def mhz(self):
+        if self.status != 0:
+            return None
+        s = self.buf.cpu().view(self.n, 2).tolist()
+        w = 10
+        return round(statistics.median((s[i + w][0] - s[i][0]) * 100.0 / (s[i + w][1] - s[i][1])
+                                       for i in range(0, self.n - w, w)))
+
+
+def board_power(graph, torch, seconds=1.0):
+    """Median board power (W) from the amdgpu hwmon ``power1_input`` over the
+    second half of ``seconds`` of back-to-back replays of ``graph``, with the
+    power cap and the shader clock in that half; None where the sysfs
+    entries are absent."""
+    import glob
+    import threading
+    files = sorted(glob.glob("/sys/class/drm/card*/device/hwmon/hwmon*/power1_input"))
+    if len(files) != 1:
+        return None
+    cap_file = files[0].replace("power1_input", "power1_cap")
+    readings, stop = [], threading.Event()
+
+    def poll():
+        t0 = time.perf_counter()
+        while not stop.is_set():
+            try:
+                readings.append((time.perf_counter() - t0, int(open(files[0]).read()) / 1e6))
+            except (OSError, ValueError):
+                pass
+            time.sleep(0.01)
+
+    clock = ClockSampler(torch)
+    th = threading.Thread(target=poll)
+    th.start()
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        if clock.status is None and time.perf_counter() - t0 >= seconds / 2:
+            clock.start()
+        for _ in range(8):
+            graph.replay()
+        torch.cuda.synchronize()
+    stop.set()
+    th.join()
+    late = [w for t, w in readings if t >= seconds / 2]
+    if not late:
+        return None
+    try:
+        cap = int(open(cap_file).read()) / 1e6
+    except (OSError, ValueError):
+        cap = None
+    return {"board_power_w": round(statistics.median(late)), "power_cap_w": cap,
+            "soak_clock_mhz": clock.mhz(),
+            "source": "1 s of back-to-back replays: amdgpu hwmon power1_input, median over "
+                      "the last half; shader clock sampled in the last half"}
+
+
+def clock_note(tflops, timing):
+    """The MFMA peak at the shader clock sampled during the workload, and the
+    achieved rate against it (the published peak assumes 2.4 GHz)."""
+    mhz = timing.get("clock_mhz")
+    if not mhz:
+        return None
+    peak = MFMA_F16_PEAK_TFLOPS * mhz / 2400.0
+    out = {"sampled_mhz": mhz, "peak_at_sampled_clock": round(peak, 1),
+           "frac_at_sampled_clock": round(tflops / peak, 4)}
+    if timing.get("power"):
+        out.update(timing["power"])
+    return out
 
 
 def calibrate_copy(torch):
@@ -321,10 +420,10 @@ def w8a16_workload(neso_amd, torch, scaled, want_cpu):
     return launch, 2.0 * m * n * k, "flop", {"M": m, "N": n, "K": k}, cpu
 
 
-def run_case(workload, steps, warmup, torch, want_cpu):
+def run_case(workload, steps, warmup, torch, want_cpu, power=False):
     """Time one workload; returns a result row."""
     launch, work, kind, cfg, cpu = workload
-    ms, timing = time_case(launch, steps, warmup, torch)
+    ms, timing = time_case(launch, steps, warmup, torch, power)
     row = dict(cfg)
     row["us"] = round(ms * 1e3, 3)
     row["timing"] = timing
@@ -425,7 +524,7 @@ def main():
         return 0
 
     # ---- headline: FA2 forward, B1 H16 N2048 d64 non-causal ----
-    head = run_case(C["fa2_headline"](), args.steps, args.warmup, torch, want_cpu)
+    head = run_case(C["fa2_headline"](), args.steps, args.warmup, torch, want_cpu, power=True)
     ms = head["us"] * 1e-3
     tflops = head["tflops"]
     log(f"fa2 headline {head['us']:.2f} us/launch {tflops:.1f} TFLOP/s "
@@ -453,7 +552,8 @@ def main():
                      "traffic": measured_traffic("fa2_headline"),
                      "kernel": "fa2_fast_kernel<64,false,false,2,false,false,4,false>",
                      "algorithmic_flop_per_launch": flop,
-                     "peak_box": peak_box},
+                     "peak_box": peak_box,
+                     "clock": clock_note(tflops, head["timing"])},
     }
     if want_cpu:
         result["cpu_baseline"] = {

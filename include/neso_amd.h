@@ -71,6 +71,18 @@ int neso_plan_begin(int32_t cu_count);
 const char* neso_plan_end(void);
 
 /*
+ * Shader-clock sampler, a measurement aid with no counterpart in the
+ * reference.  Launches one wave on `stream` that writes `samples` pairs
+ * (shader-clock counter, 100 MHz reference counter) to out[2 i], out[2 i + 1],
+ * one pair every `gap_ticks` reference ticks (gap_ticks / 100 us), and then
+ * exits.  Launched on a second stream while a workload runs on another, it
+ * gives the clock that workload ran at: d(out[2 i]) / d(out[2 i + 1]) * 100
+ * MHz.  `out` is device memory of 2 * samples uint64 values, 8-byte aligned;
+ * 1 <= samples, gap_ticks <= 2^20.
+ */
+int neso_clock_sample(uint64_t* out, int32_t samples, int32_t gap_ticks, void* stream);
+
+/*
  * Flash-Attention-2 forward.  Replaces the `flash_attention_fwd` kernel of
  * tests/test_flash_attention.py:149-153 (launched at :287-290 and by
  * macos/harness.rs:149-169 with buffers 0-3 = Q, K, V, O and scalars 4-7 =

@@ -41,6 +41,7 @@ SIGNATURES = {
     "neso_kernel_manifest": (ctypes.c_char_p, []),
     "neso_plan_begin": (ctypes.c_int, [_i32]),
     "neso_plan_end": (ctypes.c_char_p, []),
+    "neso_clock_sample": (ctypes.c_int, [_p, _i32, _i32, _p]),
     "neso_flash_attention_fwd": (
         ctypes.c_int,
         [_p, _p, _p, _p, _i32, _i32, _i32, _f32, _i32, _i32, _i64, _i64, _i32, _p],

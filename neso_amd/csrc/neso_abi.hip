@@ -199,6 +199,27 @@ int device_cu_count() {
   return cus;
 }
 
+// One wave records (shader clock, 100 MHz reference clock) pairs from
+// s_memtime and s_memrealtime, one pair every gap_ticks of the reference
+// clock.  Each wait ends once the reference clock has advanced, so the
+// kernel runs samples * gap_ticks / 100 us and then exits.
+__global__ __launch_bounds__(64) void clock_sample_kernel(uint64_t* out, int samples,
+                                                          int gap_ticks) {
+  for (int i = 0; i < samples; ++i) {
+    const uint64_t t = __builtin_amdgcn_s_memtime();
+    const uint64_t r = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+      out[2 * i] = t;
+      out[2 * i + 1] = r;
+    }
+    uint64_t now = r;
+    while (now < r + (uint64_t)gap_ticks) {
+      __builtin_amdgcn_s_sleep(1);
+      now = __builtin_amdgcn_s_memrealtime();
+    }
+  }
+}
+
 }  // namespace neso
 
 extern "C" {
@@ -226,6 +247,18 @@ int neso_plan_begin(int32_t cu_count) {
   g_plan.count = 0;
   g_plan.json.clear();
   return ok();
+}
+
+int neso_clock_sample(uint64_t* out, int32_t samples, int32_t gap_ticks, void* stream) {
+  if (!out || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(NESO_EINVAL, "clock_sample: null or misaligned out");
+  if (samples < 1 || samples > (1 << 20) || gap_ticks < 1 || gap_ticks > (1 << 20))
+    return fail(NESO_EINVAL, "clock_sample: samples=%d, gap_ticks=%d outside [1, 2^20]", samples,
+                gap_ticks);
+  return launched(neso::launch<&neso::clock_sample_kernel>(
+                      neso::ktag("clock_sample_kernel"), dim3(1), dim3(64),
+                      static_cast<hipStream_t>(stream), out, (int)samples, (int)gap_ticks),
+                  "clock_sample");
 }
 
 const char* neso_plan_end(void) {

@@ -232,6 +232,18 @@ def test_plan_records_nothing_on_rejected_calls(lib):
     assert lib.neso_plan_begin(-1) == _lib.NESO_EINVAL
 
 
+def test_clock_sample_arguments(lib):
+    """The clock sampler rejects bad buffers and counts before any HIP call,
+    and launches exactly one 64-thread wave."""
+    for args in ([None, 8, 100], [A16 + 4, 8, 100], [A16, 0, 100], [A16, 8, 0],
+                 [A16, (1 << 20) + 1, 100], [A16, 8, (1 << 20) + 1]):
+        assert lib.neso_clock_sample(*args, None) == _lib.NESO_EINVAL, args
+    status, launches = _plan(lib, lib.neso_clock_sample, [A16, 8, 100, None], 256)
+    assert status == _lib.NESO_OK
+    assert [(k["device_kernel"], k["grid"], k["threadgroup_size"]) for k in launches] == [
+        ("clock_sample_kernel", [1, 1, 1], 64)]
+
+
 def test_status_strings(lib):
     for code in (_lib.NESO_OK, _lib.NESO_EINVAL, _lib.NESO_EUNSUPPORTED, _lib.NESO_ELAUNCH):
         assert lib.neso_status_string(code).startswith(b"NESO_")
