@@ -38,12 +38,14 @@ constexpr int kThreads = 256;
 // end come back as zeros from the buffer bounds check.
 //
 // Dequantisation without the zero-point subtraction: the exponent trick
-// yields (1024 + c) and (1024 + 16 c) as f16, v_dot2_f32_f16 accumulates
-// them against X pairs, and the per-chunk constant
+// yields (1024 + c) for the low nibble of each byte (OR 0x6400: ulp 1) and
+// (64 + c) for the high one (the nibble sits at 16 c in the mantissa; OR
+// 0x5400: ulp 1/16), both exact f16.  v_dot2_f32_f16 accumulates them
+// against X pairs in one fp32 chain per chunk that starts at
 //   corr = -(1024 + z) * S_A - (64 + z) * S_B
-// (S_A, S_B = sums of the X elements paired with the two nibble sets)
-// restores sum((c - z) x) = acc1 + acc16 / 16 + corr exactly in real
-// arithmetic.  Per 8 codes: 1 shift, 4 v_and_or_b32, 4 v_dot2.
+// (S_A, S_B = sums of the X elements paired with the two nibble sets), so
+// the chain ends at sum((c - z) x) exactly in real arithmetic.  Per 8
+// codes: 1 shift, 4 v_and_or_b32, 4 v_dot2.
 
 // Sum over the 64 lanes with DPP row operations; the total lands in lane 63
 // and is returned to every lane.
@@ -81,7 +83,8 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
   const int SG = a.K / a.group;  // scales per row
   const uint32_t mlo = sgpr_const(0x000F000Fu);
   const uint32_t mhi = sgpr_const(0x00F000F0u);
-  const uint32_t mag = vgpr_const(0x64006400u);
+  const uint32_t mag = vgpr_const(0x64006400u);    // f16 1024: low nibble -> 1024 + c
+  const uint32_t mag16 = vgpr_const(0x54005400u);  // f16 64: nibble at 16 c -> 64 + c
 
   half2v xp[MR][GI][16];  // X pairs, paired like the nibbles of a word
   float corr[MR][GI];
@@ -124,37 +127,35 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
   auto row_dot = [&](GemvRow<GI>& r, float (&y)[MR]) {
     pair_scales_of(r);
 #pragma unroll
-    for (int m = 0; m < MR; ++m) y[m] = 0.f;
-#pragma unroll
     for (int gi = 0; gi < GI; ++gi) {
-      float a1[MR][2], a16[MR][2];
+      // One chain per chunk and X row, started at the correction: the GI
+      // chunks, the MR rows and the waves of a SIMD overlap the chains (two
+      // or four chains per chunk measured no faster).
+      float acc[MR];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) a1[m][0] = a1[m][1] = a16[m][0] = a16[m][1] = 0.f;
+      for (int m = 0; m < MR; ++m) acc[m] = corr[m][gi];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const uint32_t w = r.w[gi][i];
         const uint32_t w8 = w >> 8;
-        const half2v h0 = as_half2((w & mlo) | mag);    // (1024 + c0, 1024 + c4)
-        const half2v h1 = as_half2((w & mhi) | mag);    // (1024 + 16 c1, 1024 + 16 c5)
-        const half2v h2 = as_half2((w8 & mlo) | mag);   // (1024 + c2, 1024 + c6)
-        const half2v h3 = as_half2((w8 & mhi) | mag);   // (1024 + 16 c3, 1024 + 16 c7)
+        const half2v h0 = as_half2((w & mlo) | mag);     // (1024 + c0, 1024 + c4)
+        const half2v h1 = as_half2((w & mhi) | mag16);   // (64 + c1, 64 + c5)
+        const half2v h2 = as_half2((w8 & mlo) | mag);    // (1024 + c2, 1024 + c6)
+        const half2v h3 = as_half2((w8 & mhi) | mag16);  // (64 + c3, 64 + c7)
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          a1[m][i & 1] = __builtin_amdgcn_fdot2(h0, xp[m][gi][4 * i + 0], a1[m][i & 1], false);
-          a16[m][i & 1] = __builtin_amdgcn_fdot2(h1, xp[m][gi][4 * i + 1], a16[m][i & 1], false);
-          a1[m][i & 1] = __builtin_amdgcn_fdot2(h2, xp[m][gi][4 * i + 2], a1[m][i & 1], false);
-          a16[m][i & 1] = __builtin_amdgcn_fdot2(h3, xp[m][gi][4 * i + 3], a16[m][i & 1], false);
+          acc[m] = __builtin_amdgcn_fdot2(h0, xp[m][gi][4 * i + 0], acc[m], false);
+          acc[m] = __builtin_amdgcn_fdot2(h1, xp[m][gi][4 * i + 1], acc[m], false);
+          acc[m] = __builtin_amdgcn_fdot2(h2, xp[m][gi][4 * i + 2], acc[m], false);
+          acc[m] = __builtin_amdgcn_fdot2(h3, xp[m][gi][4 * i + 3], acc[m], false);
         }
       }
 #pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const float gd = (a1[m][0] + a1[m][1]) + (a16[m][0] + a16[m][1]) * 0.0625f + corr[m][gi];
-        y[m] = __builtin_fmaf(gd, r.s[gi], y[m]);
-      }
+      for (int m = 0; m < MR; ++m) y[m] = gi ? __builtin_fmaf(acc[m], r.s[gi], y[m]) : acc[m] * r.s[gi];
     }
   };
 
-  // X is requested first, then the first PF weight rows: loads complete in
+  // X is requested first, then the first EARLY weight rows: loads complete in
   // issue order, so the X pairs and corrections below are computed while
   // the weights are still in flight.  Buffer loads: rows m >= M and chunks
   // past K read as zeros, with no branch around them.
@@ -175,10 +176,14 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
   // back-edge makes the compiler drain every outstanding load).  A ring of
   // PF rows is in flight.  Rows past N read zeros and their (lane-0) stores
   // fall outside ry.
+  // The first EARLY rows are requested before the X work below and the rest
+  // of the ring after it, pinned there by scheduling barriers (all rows up
+  // front only queues behind the first two; this order measured fastest).
   constexpr int PF = R < 4 ? R : 4;
+  constexpr int EARLY = PF < 2 ? PF : 2;
   GemvRow<GI> ring[PF];
 #pragma unroll
-  for (int k = 0; k < PF; ++k) load_row(ring[k], wid + k * T);
+  for (int k = 0; k < EARLY; ++k) load_row(ring[k], wid + k * T);
 
   // Chunk sums for the corrections with v_dot2 against (1, 1).
   const half2v ones = {(half_t)1, (half_t)1};
@@ -202,6 +207,10 @@ __global__ __launch_bounds__(kThreads) void w4a16_gemv_kernel(W4Args a) {
       corr[m][gi] = -(1024.f + a.zero) * sa - (64.f + a.zero) * sb;
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = EARLY; k < PF; ++k) load_row(ring[k], wid + k * T);
+  __builtin_amdgcn_sched_barrier(0);
 
 
   rsrc_t ry[MR];
