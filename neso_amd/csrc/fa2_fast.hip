@@ -121,7 +121,7 @@ template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT, bool PAIR = false, bool 
 __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   static_assert(!PAIR || CAUSAL, "paired query blocks are for causal grids");
   static_assert(!HALVES || (CAUSAL && !PAIR), "64-row halves are for full causal grids");
-  static_assert(QW == 4 || (QW == 2 && !PAIR && !HALVES), "query waves");
+  static_assert(QW == 4 || (QW == 2 && !HALVES), "query waves");
   static_assert(!BIAS || !CAUSAL, "the biased entry point is never masked");
   constexpr int kBMq = 32 * QW;      // queries per workgroup
   constexpr int kGroup = 64 * QW;    // threads per key group
@@ -850,15 +850,17 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 // Launches with K key groups if their LDS fits (returns false otherwise).
 template <int D, bool CAUSAL, bool OUT_F16, int K, int QW, bool BIAS>
 bool launch_fast_k(const Fa2Args& a, hipStream_t stream, hipError_t& err) {
-  if constexpr (CAUSAL && QW == 4) {
+  if constexpr (CAUSAL && !BIAS) {
     if constexpr (fast_lds_bytes<D, QW, BIAS, false, true, K>() <= 160 * 1024) {
       if (a.pair_qblocks == 1) {
-        err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, true>>(
+        err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, true, false, QW>>(
             ktag("fa2_fast_kernel", D, true, OUT_F16, K, true, false, QW, BIAS),
             dim3((a.num_qblocks + 1) / 2 * a.batch_heads), dim3(K * 64 * QW), stream, a);
         return true;
       }
     }
+  }
+  if constexpr (CAUSAL && QW == 4) {
     if constexpr (fast_lds_bytes<D, QW, BIAS, true, false, K>() <= 160 * 1024) {
       if (a.pair_qblocks == 2) {
         err = launch<&fa2_fast_kernel<D, true, OUT_F16, K, false, true>>(
@@ -959,14 +961,13 @@ hipError_t launch_fa2_fast(Fa2Args a, int head_dim, bool causal, bool bias, bool
   if (bias && causal) return hipErrorInvalidValue;  // the biased entry point is never masked
   if (a.qwaves != 2) a.qwaves = 4;
   a.num_qblocks = (a.N + 32 * a.qwaves - 1) / (32 * a.qwaves);
-  // Paired query blocks (causal kernels with four query waves only; any
-  // window is correct); 64-row halves only without a window (the two
-  // halves' key ranges must both start at key 0).
+  // Paired query blocks (causal kernels, two or four query waves; any
+  // window is correct); 64-row halves only with four query waves and
+  // without a window (the two halves' key ranges must both start at key 0).
   const bool full_causal = causal && a.win_left >= a.N && a.win_right == 0;
-  a.pair_qblocks = (a.qwaves != 4)                          ? 0
-                   : (causal && a.pair_qblocks == 1)        ? 1
-                   : (full_causal && a.pair_qblocks == 2)   ? 2
-                                                            : 0;
+  a.pair_qblocks = (causal && a.pair_qblocks == 1)                          ? 1
+                   : (a.qwaves == 4 && full_causal && a.pair_qblocks == 2)  ? 2
+                                                                            : 0;
   return out_f16 ? launch_fast_d<true>(a, head_dim, causal, bias, ksplit, stream)
                  : launch_fast_d<false>(a, head_dim, causal, bias, ksplit, stream);
 }

@@ -606,9 +606,22 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
     // would idle half the CUs).  NESO_AMD_FA2_PAIR = 0 / 1 forces it.
     // Below that, without a window: 64-row halves from opposite ends of the
     // rows, which halve the longest workgroup's work at one workgroup per CU.
+    // head_dim 128, full causal, from N = 2048, where the paired 64-row
+    // blocks fill at most one round: paired blocks on 64-query workgroups
+    // with four key groups instead of 128-row halves, whose long-half waves
+    // end up alone on their SIMDs (measured: d128 B1 H8 N4096 53.1 -> 49.1
+    // us, B1 H16 N2048 32.1 -> 31.7; at d = 64 the halves stay ahead, H16
+    // N2048 19.9 against 21.4).
+    const int64_t pairs64 = (int64_t)(((a.N + 63) / 64 + 1) / 2) * a.batch_heads;
+    if (head_dim == 128 && full_causal && a.N >= 2048 && pairs64 <= cus && a.pair_qblocks < 0 &&
+        a.qwaves != 4 && !bias) {
+      a.pair_qblocks = 1;
+      a.qwaves = 2;
+      if (a.ksplit <= 0) ksplit = 4;
+    }
     if (a.pair_qblocks < 0)
       a.pair_qblocks = (full_causal && wgs >= 2 * cus) ? 1 : full_causal ? 2 : 0;
-    if (causal && a.pair_qblocks == 1 && a.ksplit <= 0) {
+    if (causal && a.pair_qblocks == 1 && a.ksplit <= 0 && a.qwaves != 2) {
       const int64_t pwgs = (int64_t)((a.num_qblocks + 1) / 2) * a.batch_heads;
       ksplit = pwgs < 2 * cus ? 2 : 1;
     }
@@ -619,7 +632,7 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
     // cost more (measured, d = 64: H8 N1500 12.7 vs 13.4 us, rel-pos H8
     // N2048 16.7 vs 18.3; H8 N512 7.3 vs 6.9).
     if (a.qwaves != 2 && a.qwaves != 4) a.qwaves = fa2_fast_qwaves(small, a.N, bias);
-    if (a.qwaves == 2 && a.ksplit <= 0) {
+    if (a.qwaves == 2 && a.ksplit <= 0 && a.pair_qblocks != 1) {
       const int64_t wgs64 = (int64_t)((a.N + 63) / 64) * a.batch_heads;
       ksplit = (wgs64 <= cus && a.N >= 1024) ? 4 : 2;
     }

@@ -133,11 +133,11 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 32 * QW), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
       "1",
       "1"
      ],
@@ -410,11 +410,11 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 32 * QW), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
       "1",
       "1"
      ],
@@ -576,11 +576,11 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 32 * QW), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
       "1",
       "1"
      ],
@@ -752,11 +752,11 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU, QW = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
-      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 128), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
+      "cdiv(cdiv(N, 64), 2) * batch_heads if HALVES else (cdiv(cdiv(N, 32 * QW), 2) * batch_heads if PAIR else cdiv(N, 32 * QW) * batch_heads)",
       "1",
       "1"
      ],

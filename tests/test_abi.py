@@ -105,6 +105,8 @@ PLAN_CASES = [
      dict(N=1024, batch_heads=16)),
     ("neso_flash_attention_fwd", [_P] * 4 + [512, 64, 64, 0.125, 64, 16, 512 * 64, 512 * 64, 1],
      dict(N=512, batch_heads=16)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [4096, 128, 128, 0.08, 128, 8, 4096 * 128, 4096 * 128, 1],
+     dict(N=4096, batch_heads=8)),
     ("neso_flash_attention_fwd", [_P] * 4 + [4096, 128, 128, 0.08, 128, 64, 4096 * 128, 4096 * 128, 1],
      dict(N=4096, batch_heads=64)),
     ("neso_flash_attention_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 4, 2048 * 64, 2048 * 64, 1],
@@ -204,6 +206,17 @@ CHOICE_CASES = [
     # Causal, one workgroup per CU: 64-row halves on four query waves.
     ("neso_flash_attention_fwd", [_P] * 4 + [2048, 64, 64, 0.125, 64, 16, 2048 * 64, 2048 * 64, 1],
      "fa2_fast_kernel", dict(QW=4, HALVES=1)),
+    # head_dim 128, causal, one round of paired 64-row blocks from N = 2048:
+    # paired blocks on two query waves with four key groups.
+    ("neso_flash_attention_fwd", [_P] * 4 + [4096, 128, 128, 0.08, 128, 8, 4096 * 128, 4096 * 128, 1],
+     "fa2_fast_kernel", dict(D=128, QW=2, KSPLIT=4, PAIR=1, HALVES=0)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [2048, 128, 128, 0.08, 128, 16, 2048 * 128, 2048 * 128, 1],
+     "fa2_fast_kernel", dict(D=128, QW=2, KSPLIT=4, PAIR=1)),
+    # Below N = 2048, or with more pairs than CUs: as before.
+    ("neso_flash_attention_fwd", [_P] * 4 + [1024, 128, 128, 0.08, 128, 32, 1024 * 128, 1024 * 128, 1],
+     "fa2_fast_kernel", dict(D=128, QW=4, HALVES=1)),
+    ("neso_flash_attention_fwd", [_P] * 4 + [4096, 128, 128, 0.08, 128, 64, 4096 * 128, 4096 * 128, 1],
+     "fa2_fast_kernel", dict(D=128, QW=4, PAIR=1)),
     # Short rows: the fast kernel with 128-query workgroups (N < 512).
     ("neso_flash_attention_fwd", [_P] * 4 + [128, 64, 64, 0.125, 64, 8, 128 * 64, 128 * 64, 0],
      "fa2_fast_kernel", dict(QW=4)),

@@ -134,6 +134,43 @@ def test_fast_paired_causal_blocks(gpu, monkeypatch, ksplit, d, n):
     check(q, k, v, causal=True)
 
 
+@pytest.mark.parametrize("ksplit", [1, 2, 4])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("n", [1, 64, 65, 128, 129, 384, 1000, 1500, 2048])
+def test_fast_paired_two_query_waves(gpu, monkeypatch, ksplit, d, n):
+    """Paired query blocks on 64-query workgroups (two query waves per key
+    group, two K and two V slots): workgroup x takes the 64-row blocks
+    nqb-1-x and x, one pass each, with a barrier between the first pass's
+    merge and the second pass's loads."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_QW", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
+    monkeypatch.setenv("NESO_AMD_FA2_PAIR", "1")
+    q, k, v = I.fa2_inputs(1, 3, n, d, seed=n + d + 5 * ksplit)
+    check(q, k, v, causal=True)
+
+
+@pytest.mark.parametrize("d", [64, 128])
+def test_fast_paired_two_query_waves_rescale(gpu, monkeypatch, d):
+    """The same with logits that jump between key blocks (the slow path on
+    the kept scores) and with fp16 output through the window entry."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_QW", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_PAIR", "1")
+    q, k, v = I.fa2_inputs(1, 2, 1000, d, seed=3 * d)
+    k = k.float()
+    for blk, f in enumerate([0.5, 3.0, 9.0, 1.0, 12.0, 2.0, 6.0, 0.25] * 2):
+        k[:, :, 64 * blk:64 * blk + 64] *= f
+    k = k.half()
+    check(q, k, v, causal=True)
+    n, dev = q.shape[-2], torch.device("cuda:0")
+    qs, ks, vs = (t[0].permute(1, 0, 2).contiguous().to(dev) for t in (q, k, v))
+    out = neso_amd.window_attention(qs, ks, vs, n, 0, out_dtype=torch.float16)
+    out = out.float().cpu().permute(1, 0, 2)
+    ref = A.attention(q[0], k[0], v[0], 1 / math.sqrt(d), causal=True)
+    assert ((out - ref).abs() <= TOL + ref.abs() * 2.0 ** -11).all()
+
+
 @pytest.mark.parametrize("ksplit", [1, 2, 3])
 @pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("n", [1, 63, 64, 65, 129, 191, 384, 1000, 1500, 2048])
@@ -172,12 +209,14 @@ def test_fast_causal_halves_rescale_and_f16(gpu, monkeypatch, d):
 
 
 @pytest.mark.parametrize("n,wl,wr", [(300, 100, 37), (1500, 128, 128), (1000, 1000, 0)])
-@pytest.mark.parametrize("pair", ["1", "2"])
-def test_fast_paired_windows(gpu, monkeypatch, n, wl, wr, pair):
+@pytest.mark.parametrize("pair,qw", [("1", "4"), ("2", "4"), ("1", "2"), ("2", "2")])
+def test_fast_paired_windows(gpu, monkeypatch, n, wl, wr, pair, qw):
     """Windows with pairing forced: 64-row halves (2) apply only without a
-    window, so a windowed call falls back to whole blocks."""
+    window and with four query waves, so a windowed call (or a two-query-wave
+    one) falls back to whole blocks; paired blocks (1) take any window."""
     monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
     monkeypatch.setenv("NESO_AMD_FA2_PAIR", pair)
+    monkeypatch.setenv("NESO_AMD_FA2_QW", qw)
     heads, d = 2, 64
     q, k, v = (t[0].permute(1, 0, 2).contiguous() for t in I.fa2_inputs(1, heads, n, d, seed=n))
     dev = torch.device("cuda:0")

@@ -91,6 +91,20 @@ def test_two_query_waves_equal(gpu, libs, monkeypatch, d, causal):
     assert torch.equal(fast, serial)
 
 
+@pytest.mark.parametrize("d,ksplit", [(64, 4), (128, 4), (128, 2)])
+def test_paired_two_query_waves_equal(gpu, libs, monkeypatch, d, ksplit):
+    """Paired causal blocks on 64-query workgroups: the second pass's loads
+    reuse the slots the first pass's merge read."""
+    monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_QW", "2")
+    monkeypatch.setenv("NESO_AMD_FA2_PAIR", "1")
+    monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", str(ksplit))
+    q, k, v = (t.to(DEV) for t in I.fa2_inputs(1, 3, 1000, d, seed=d + ksplit))
+    fast, serial = (_run(lib, q, k, v, True) for lib in libs)
+    assert torch.isfinite(fast).all()
+    assert torch.equal(fast, serial)
+
+
 def _run_table(lib, q, k, v, table):
     h, n, d = q.shape
     o = torch.full(q.shape, float("nan"), device=DEV)
