@@ -638,10 +638,17 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   float16v sa[NT], sb[NT];
   half8v pa[2 * NT], pb2[2 * NT];
   if (my_n > 0) {
-    if constexpr (kLive)
+    if constexpr (kLive) {
+      // Without a bias, V of block 0 too: the V slots are free until step
+      // 0, and loading it here keeps its latency out of step 0's wait
+      // (measured: H16 N1024 d64 10.25 -> 10.05 us; with the bias band the
+      // longer prologue cost more, rel-pos 14.21 -> 14.52, so step 0 loads
+      // it there).
       tile_load(0, false);
-    else
+      if constexpr (!BIAS) tile_load(0, true);
+    } else {
       lds_load(0, 0);
+    }
     bpro[0] = band_load(0);
   }
   if (my_n > 1) {
@@ -664,7 +671,8 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 
   // ---- step 0, peeled: block 0 is every row's first visible block, so its
   // softmax is the slow path on its exact scores; scores of block 1; loads
-  // of block 2 (two query waves: K of block 2, V of block 0).  (Scores of
+  // of block 2 (two query waves: K of block 2, and with the bias V of
+  // block 0).  (Scores of
   // blocks a group does not have come from stale slots and are never
   // used.) ----
   if (my_n > 2) {
@@ -674,7 +682,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       lds_load(2, 2);
     bpro[2] = band_load(2);
   }
-  if (kLive && my_n > 0) tile_load(0, true);
+  if (kLive && BIAS && my_n > 0) tile_load(0, true);
   serial_lds_point();
   if constexpr (!kLive) qk(sa, kslot(0), 0);
   if (HALVES ? my_nw > 0 : my_n > 0) {
