@@ -663,23 +663,24 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   band_store(1, bpro[1]);
   lds_barrier();
   if constexpr (kLive) {
-    // Scores of blocks 0 and 1 before step 0 reloads K slot 0.
+    // Scores of block 0, a barrier (every wave done with K slot 0), then K
+    // of block 2 into that slot while the scores of block 1 are formed.
     qk(sa, kslot(0), 0);
-    qk(sb, kslot(1), 1);
     lds_barrier();
+    if (my_n > 2) {
+      tile_load(2, false);
+      bpro[2] = band_load(2);
+    }
+    qk(sb, kslot(1), 1);
   }
 
   // ---- step 0, peeled: block 0 is every row's first visible block, so its
   // softmax is the slow path on its exact scores; scores of block 1; loads
-  // of block 2 (two query waves: K of block 2, and with the bias V of
-  // block 0).  (Scores of
+  // of block 2 (two query waves: with the bias, V of block 0).  (Scores of
   // blocks a group does not have come from stale slots and are never
   // used.) ----
-  if (my_n > 2) {
-    if constexpr (kLive)
-      tile_load(2, false);
-    else
-      lds_load(2, 2);
+  if (!kLive && my_n > 2) {
+    lds_load(2, 2);
     bpro[2] = band_load(2);
   }
   if (kLive && BIAS && my_n > 0) tile_load(0, true);
