@@ -271,8 +271,7 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_kernel(W4Args a) {
   const rsrc_t rs = make_rsrc(a.S + (int64_t)n0 * SG, (uint32_t)nrows * (uint32_t)SG * 2u);
   const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx,
                               (uint32_t)((mrows - 1) * a.ldx + a.K) * 2u);
-  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
-  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const ZeroPoint zp = zero_point(a.zero);
   const Nibbles nib = nibble_consts();
   const uint32_t gm = (uint32_t)a.group >> 5;  // chunks per scale group
   const bool gpow2 = (gm & (gm - 1)) == 0;
@@ -354,11 +353,9 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_kernel(W4Args a) {
         for (int t = 0; t < 4; ++t) {
           const half_t s = b.s[qi][nt][t];
           const half2v s1 = {s, s};
-          const half_t s16v = s * (half_t)0.0625f;
-          const half2v s16 = {s16v, s16v};
           half2v r[4];
-          unpack_word(wt[t], nib, z1, z16, r);
-          const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
+          unpack_word(wt[t], nib, zp, r);
+          const half2v d0 = r[0] * s1, d1 = r[1] * s1, d2 = r[2] * s1, d3 = r[3] * s1;
           const half8v bv = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) acc[mt][nt] = mfma16x16x32(xa[mt][t], bv, acc[mt][nt]);
@@ -449,8 +446,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
   const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)((mrows - 1) * a.ldx + a.K) * 2u);
   const rsrc_t rw = make_rsrc(a.W + (int64_t)(nwrows ? nw0 : 0) * KW, (uint32_t)nwrows * KW * 4u);
   const rsrc_t rs = make_rsrc(a.S + (int64_t)(nwrows ? nw0 : 0) * SG, (uint32_t)nwrows * SG * 2u);
-  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
-  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const ZeroPoint zp = zero_point(a.zero);
   const Nibbles nib = nibble_consts();
   const uint32_t gm = (uint32_t)a.group >> 5;
   const bool gpow2 = (gm & (gm - 1)) == 0;
@@ -503,13 +499,11 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
       const half2v s1 = {g.s[nt], g.s[nt]};
-      const half_t s16v = g.s[nt] * (half_t)0.0625f;
-      const half2v s16 = {s16v, s16v};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
         half2v r[4];
-        unpack_word(g.w[nt][ks], nib, z1, z16, r);
-        const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
+        unpack_word(g.w[nt][ks], nib, zp, r);
+        const half2v d0 = r[0] * s1, d1 = r[1] * s1, d2 = r[2] * s1, d3 = r[3] * s1;
         const half8v bfr = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
 #pragma unroll
         for (int mi = 0; mi < MI; ++mi) {
@@ -603,8 +597,7 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)((mrows - 1) * a.ldx + a.K) * 2u);
   const rsrc_t rw = make_rsrc(a.W + (int64_t)n0 * KW, (uint32_t)nrows * KW * 4u);
   const rsrc_t rs = make_rsrc(a.S + (int64_t)n0 * SG, (uint32_t)nrows * SG * 2u);
-  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
-  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const ZeroPoint zp = zero_point(a.zero);
   const Nibbles nib = nibble_consts();
   const uint32_t gm = (uint32_t)a.group >> 5;  // 32-code chunks per scale group
   const bool gpow2 = (gm & (gm - 1)) == 0;
@@ -647,7 +640,7 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
       const half_t s16v = g.s * (half_t)0.0625f;
       const half2v s16 = {s16v, s16v};
       half2v r[4];
-      unpack_word(g.w[i], nib, z1, z16, r);
+      unpack_word_x16(g.w[i], nib, zp, r);
       const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
       lds[kg][buf][1][(wrow * kTLD + 32 * wq + 8 * i) / 8] =
           half8v{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
@@ -775,8 +768,7 @@ __global__ __launch_bounds__(kThreads) void w4a16_mfma_kernel(W4Args a) {
   if (nw0 >= a.N) return;
   const int KW = a.K >> 3;
   const int SG = a.K / a.group;
-  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
-  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const ZeroPoint zp = zero_point(a.zero);
   const Nibbles nib = nibble_consts();
 
   float16v acc[TN];
@@ -802,13 +794,11 @@ __global__ __launch_bounds__(kThreads) void w4a16_mfma_kernel(W4Args a) {
                           : uint4v{0x88888888u, 0x88888888u, 0x88888888u, 0x88888888u};
       const half_t s = ok ? a.S[(int64_t)n * SG + kc / a.group] : (half_t)0;
       const half2v s1 = {s, s};
-      const half_t s16v = s * (half_t)0.0625f;
-      const half2v s16 = {s16v, s16v};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         half2v r[4];
-        unpack_word(w[j], nib, z1, z16, r);
-        const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
+        unpack_word(w[j], nib, zp, r);
+        const half2v d0 = r[0] * s1, d1 = r[1] * s1, d2 = r[2] * s1, d3 = r[3] * s1;
         const half8v b = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
         acc[t] = mfma32x32x16(xa[j], b, acc[t]);
       }

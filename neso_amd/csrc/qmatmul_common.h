@@ -24,25 +24,52 @@ __device__ __forceinline__ uint32_t vgpr_const(uint32_t v) {
   return r;
 }
 
-// Nibble masks and the f16 exponent pattern, held in registers so that
-// (w & mask) | magic is one v_and_or_b32.
+// Nibble masks and the f16 exponent patterns, held in registers so that
+// (w & mask) | magic is one v_and_or_b32: 0x6400 (f16 1024, ulp 1) turns a
+// low nibble c into 1024 + c, 0x5400 (f16 64, ulp 1/16) turns a high
+// nibble, which sits at 16 c, into 64 + c.
 struct Nibbles {
-  uint32_t lo, hi, mag;
+  uint32_t lo, hi, mag, mag16;
 };
 __device__ __forceinline__ Nibbles nibble_consts() {
-  return Nibbles{sgpr_const(0x000F000Fu), sgpr_const(0x00F000F0u), vgpr_const(0x64006400u)};
+  return Nibbles{sgpr_const(0x000F000Fu), sgpr_const(0x00F000F0u), vgpr_const(0x64006400u),
+                 vgpr_const(0x54005400u)};
 }
 
-// Four f16 pairs of one packed word, shifted by the zero point:
-//   r[0] = (c0 - z, c4 - z)        r[1] = 16 * (c1 - z, c5 - z)
-//   r[2] = (c2 - z, c6 - z)        r[3] = 16 * (c3 - z, c7 - z)
-__device__ __forceinline__ void unpack_word(uint32_t w, const Nibbles& k, half2v z1, half2v z16,
+// The zero-point offsets: z1 = 1024 + z for the low nibbles, z64 = 64 + z
+// for the high ones, z16 = 1024 + 16 z for high nibbles taken with the 0x6400
+// pattern (all exact in f16).
+struct ZeroPoint {
+  half2v z1, z64, z16;
+};
+__device__ __forceinline__ ZeroPoint zero_point(int z) {
+  const half_t a = (half_t)(1024 + z), b = (half_t)(64 + z), c = (half_t)(1024 + 16 * z);
+  return ZeroPoint{{a, a}, {b, b}, {c, c}};
+}
+
+// Four f16 pairs of one packed word, shifted by the zero point, all exact:
+//   r[0] = (c0 - z, c4 - z)        r[1] = (c1 - z, c5 - z)
+//   r[2] = (c2 - z, c6 - z)        r[3] = (c3 - z, c7 - z)
+__device__ __forceinline__ void unpack_word(uint32_t w, const Nibbles& k, const ZeroPoint& z,
                                             half2v r[4]) {
   const uint32_t w8 = w >> 8;
-  r[0] = as_half2((w & k.lo) | k.mag) - z1;
-  r[1] = as_half2((w & k.hi) | k.mag) - z16;
-  r[2] = as_half2((w8 & k.lo) | k.mag) - z1;
-  r[3] = as_half2((w8 & k.hi) | k.mag) - z16;
+  r[0] = as_half2((w & k.lo) | k.mag) - z.z1;
+  r[1] = as_half2((w & k.hi) | k.mag16) - z.z64;
+  r[2] = as_half2((w8 & k.lo) | k.mag) - z.z1;
+  r[3] = as_half2((w8 & k.hi) | k.mag16) - z.z64;
+}
+
+// The same with the high nibbles as 16 (c - z), for a scale of s / 16 on
+// r[1] and r[3] (the tile GEMM: the form above measured 1.5-2% slower there,
+// M = 256 / 512).  Equal results to unpack_word's while s / 16 is a normal
+// f16.
+__device__ __forceinline__ void unpack_word_x16(uint32_t w, const Nibbles& k, const ZeroPoint& z,
+                                                half2v r[4]) {
+  const uint32_t w8 = w >> 8;
+  r[0] = as_half2((w & k.lo) | k.mag) - z.z1;
+  r[1] = as_half2((w & k.hi) | k.mag) - z.z16;
+  r[2] = as_half2((w8 & k.lo) | k.mag) - z.z1;
+  r[3] = as_half2((w8 & k.hi) | k.mag) - z.z16;
 }
 
 // Word j of register w_j in 16-lane row g (chunk g, word j) becomes word g

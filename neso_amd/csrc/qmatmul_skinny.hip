@@ -38,8 +38,7 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
   const int q0 = wave * QW;
   const int cend = min(4 * min(q0 + QW, Q), C);
   const int ntiles = (a.N + 15) >> 4;
-  const half2v z1 = {(half_t)(1024 + a.zero), (half_t)(1024 + a.zero)};
-  const half2v z16 = {(half_t)(1024 + 16 * a.zero), (half_t)(1024 + 16 * a.zero)};
+  const ZeroPoint zp = zero_point(a.zero);
   const Nibbles nib = nibble_consts();
 
   __shared__ half8v xs[kLdsQuads * 4 * kWave];
@@ -131,11 +130,9 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
         const half8v xa = xs[(4 * q + t) * kWave + 16 * lg + (li ^ (4 * t + lg))];
         const half_t s = sq[t];
         const half2v s1 = {s, s};
-        const half_t s16v = s * (half_t)0.0625f;
-        const half2v s16 = {s16v, s16v};
         half2v r[4];
-        unpack_word(wt[t], nib, z1, z16, r);
-        const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
+        unpack_word(wt[t], nib, zp, r);
+        const half2v d0 = r[0] * s1, d1 = r[1] * s1, d2 = r[2] * s1, d3 = r[3] * s1;
         const half8v bv = {d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
         acc[i] = mfma16x16x32(xa, bv, acc[i]);
       }
