@@ -17,8 +17,9 @@ The same line carries:
 * ``roofline`` for that kernel against dense-fp16 MFMA peak (2516.6 TFLOP/s
   = 256 CU x 2.4 GHz x 4096 FLOP/clk), with the HBM traffic per launch from
   the committed counter summary, and ``roofline.clock``: the shader clock
-  sampled during the median replays (the part lowers its clock under MFMA
-  load), the peak at that clock, and board power and clock after a 1 s soak;
+  sampled over replays right after the timed ones (the part lowers its clock
+  under MFMA load), the peak at that clock, and board power and clock after
+  a 1 s soak;
 * ``cpu_baseline``: the CPU oracle (torch fp32, all host threads) on the
   same workload, with the host CPU model;
 * ``qmatmul``: the int4 qmatmul at M=1, K=4096, N=11008 in HBM GB/s
@@ -108,8 +109,9 @@ def time_case(launch, steps, warmup, torch, power=False):
     the current stream (the graph replays on it), with device
     synchronisation on both sides.  The dict adds the median / p10 / p90
     over MEDIAN_REPLAYS separately timed replays of a GRAPH_LAUNCHES-launch
-    graph (with the shader clock sampled during them), the eager (one-by-one
-    from Python) rate and, with ``power``, the board power after a 1 s soak.
+    graph, the shader clock sampled over ~3 ms of further replays, the eager
+    (one-by-one from Python) rate and, with ``power``, the board power after
+    a 1 s soak.
     """
     for i in range(warmup):
         launch(i)
@@ -126,12 +128,17 @@ def time_case(launch, steps, warmup, torch, power=False):
     ev[1].record()
     torch.cuda.synchronize()
     ms = ev[0].elapsed_time(ev[1]) / steps
-    clock = ClockSampler(torch)
-    clock.start()  # one sleeping wave on a second stream during the replays below
     for r in range(MEDIAN_REPLAYS):
         ev[2 + 2 * r].record()
         g_small.replay()
         ev[3 + 2 * r].record()
+    # The shader clock over further replays right after (untimed: the
+    # sampler's wave on one CU measurably slows that CU's workgroup).
+    clock = ClockSampler(torch)
+    n_clock = int(3.0 / max(ms * GRAPH_LAUNCHES, 1e-3)) + 1  # ~3 ms of replays
+    clock.start()
+    for _ in range(n_clock):
+        g_small.replay()
     torch.cuda.synchronize()
     per = sorted(ev[2 + 2 * r].elapsed_time(ev[3 + 2 * r]) / GRAPH_LAUNCHES
                  for r in range(MEDIAN_REPLAYS))
