@@ -20,6 +20,7 @@
 #include "common.h"
 #include "neso_internal.h"
 #include "qmatmul_common.h"
+#include "fa2_tiles.h"
 
 namespace neso {
 
@@ -824,21 +825,38 @@ __global__ __launch_bounds__(kThreads) void w4a16_mfma_kernel(W4Args a) {
 // Workgroup tile 128 x 128, four waves of 64 x 64 (2 x 2
 // v_mfma_f32_32x32x16_f16 tiles), K-steps of kW8BK.  A goes through LDS with
 // rows padded by 8 halves (conflict-free ds_read_b128).  B is N-contiguous
-// in memory but the MFMA B operand needs 8 consecutive k of one column per
-// lane, so the tile is transposed on the way into LDS: thread (c, kp) loads
-// eight columns of k-rows 2kp and 2kp+1, converts them to f16 exactly
-// (int8 -> f16 via the exponent trick: 0x6400 | (b ^ 0x80) is 1024 + b +
-// 128) and stores (k, k+1) pairs per column, Bs[n][k] (2-way write
-// conflicts).  Double-buffered LDS, global loads one step ahead.
+// in memory and stays so in LDS: thread (row, column group) loads 32
+// contiguous bytes of one k-row, converts them to f16 exactly (int8 -> f16
+// via the exponent trick: 0x6400 | (b ^ 0x80) is 1024 + b + 128) and stores
+// them as two 16-byte chunks of Bs[k][n]; the MFMA B operand (8 consecutive
+// k of one column per lane) comes from gfx950's transposing LDS read,
+// ds_read_b64_tr_b16, two per fragment.  (The earlier layout, transposed on
+// the way in as (k, k+1) pairs per column, took 16 ds_write_b32 per thread
+// and step and was ~10% slower: 176.8 against 160.9 us at 4096^3.)
+// Double-buffered LDS, global loads one step ahead.
 // K-step 64: 16 MFMAs per wave between barriers (measured at 4096^3 on one
 // box: 179.0 us against 181.9 us with K-steps of 32).
 constexpr int kW8BM = 128, kW8BN = 128, kW8BK = 64, kW8LD = kW8BK + 8;
 constexpr int kW8AP = kW8BK / 32;  // 16-byte A pieces per thread and 64-row half
-constexpr int kW8BP = kW8BK / 32;  // k-row pairs per thread
+
+// B tile in LDS: [k][n] f16 rows of 128 halves (16 chunks of 16 bytes, one
+// row spans every bank), chunk c of row r at c ^ 5 (r % 4).  A store pass
+// (16 lanes: 4 rows x chunks 4 j + s of 4 column groups j) then covers 16
+// positions 4 (j ^ i) + (s ^ i), and so does a transposed-read pass (4 rows
+// i x chunks 4 u .. 4 u + 3): every bank once.
+__device__ __forceinline__ int w8_b_at(int r, int c) { return r * kW8BN + 8 * (c ^ (5 * (r & 3))); }
+// This lane's offset for the B fragment of column tile u (v_frag_tr's
+// addressing: key row 8 (l / 32) + (l % 16) / 4, columns 32 u + 16 ((l / 16)
+// % 2) + 4 (l % 4)); adding 4 or 16 rows keeps the swizzle.
+__device__ __forceinline__ int w8_b_tr_offset(int lane, int u) {
+  const int row = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int cu = 32 * u + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  return w8_b_at(row, cu >> 3) + (cu & 7);
+}
 
 __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
   __shared__ half8v as[2][kW8BM * kW8LD / 8];
-  __shared__ uint32_t bs[2][kW8BN * kW8LD / 2];  // (k, k+1) f16 pairs
+  __shared__ __attribute__((aligned(16))) half_t bs[2][kW8BK * kW8BN];  // [k][n], swizzled chunks
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
@@ -863,12 +881,14 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
       a.B + n0, (uint32_t)max((int64_t)0, (a.K - 1) * (int64_t)a.ldb + min(kW8BN, a.N - n0)));
   // A: rows (tid >> 2) + 64j, 16-byte pieces (tid & 3) + 4p of the step.
   const int ar = tid >> 2, ap = tid & 3;
-  // B: column chunk c (8 columns), k pairs kp + 16p.
-  const int bc = tid >> 4, bkp = tid & 15;
+  // B: k-row br of the step, columns 32 bc .. 32 bc + 31 (two 16-byte
+  // pieces; four lanes read a row's 128 contiguous bytes).
+  static_assert(kW8BK * kW8BN == 32 * kThreads, "one 32-byte row piece per thread");
+  const int br = tid >> 2, bc = tid & 3;
   const uint32_t nlim = (uint32_t)min(kW8BN, a.N - n0);
   struct Stage {
     half8v av[2][kW8AP];
-    uint32_t b0[kW8BP][2], b1[kW8BP][2];  // 8 int8 of k-rows 2kp and 2kp + 1
+    uint4v b[2];  // 16 int8 of row br, columns 32 bc + 16 h ..
   };
   auto load = [&](Stage& g, int k0) {
 #pragma unroll
@@ -879,19 +899,16 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
       for (int j = 0; j < 2; ++j)
         g.av[j][p] = buf_load_half8(ra, (((uint32_t)(ar + 64 * j) * a.lda + kc) * 2u) | aoob);
     }
-    // Columns past N: offsets beyond the row end read the next row's bytes,
-    // so mask them; rows past K fall outside the buffer.
-    const uint32_t coob = (uint32_t)(8 * bc) < nlim ? 0u : kOut;
-    typedef int int2v __attribute__((ext_vector_type(2)));
+    // Pieces wholly past N are masked; a piece that straddles N (N % 16 =
+    // 8) reads bytes of columns >= N, whose products only reach columns of
+    // C that are never stored.  Rows past K fall outside the buffer.
+    const int k = k0 + br;
 #pragma unroll
-    for (int p = 0; p < kW8BP; ++p) {
-      const int k = k0 + 2 * (bkp + 16 * p);
-      const int2v r0 = __builtin_amdgcn_raw_buffer_load_b64(
-          rb, ((uint32_t)k * a.ldb + 8u * bc) | (k < a.K ? coob : kOut), 0, 0);
-      const int2v r1 = __builtin_amdgcn_raw_buffer_load_b64(
-          rb, ((uint32_t)(k + 1) * a.ldb + 8u * bc) | (k + 1 < a.K ? coob : kOut), 0, 0);
-      g.b0[p][0] = r0[0]; g.b0[p][1] = r0[1];
-      g.b1[p][0] = r1[0]; g.b1[p][1] = r1[1];
+    for (int h = 0; h < 2; ++h) {
+      const uint32_t col = 32u * bc + 16u * h;
+      g.b[h] = __builtin_bit_cast(
+          uint4v, __builtin_amdgcn_raw_buffer_load_b128(
+                      rb, ((uint32_t)k * a.ldb + col) | (k < a.K && col < nlim ? 0u : kOut), 0, 0));
     }
   };
   const uint32_t magic = vgpr_const(0x64006400u);
@@ -902,21 +919,29 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
 #pragma unroll
       for (int j = 0; j < 2; ++j)
         as[buf][((ar + 64 * j) * kW8LD + 8 * (ap + 4 * p)) / 8] = g.av[j][p];
+    // Row br as f16 in [k][n] order: bytes (n, n+1) of a word -> one f16
+    // pair; chunk c of the row at w8_b_at(br, c).
 #pragma unroll
-    for (int p = 0; p < kW8BP; ++p)
+    for (int h = 0; h < 2; ++h) {
+      uint32_t pr[8];
 #pragma unroll
-      for (int w = 0; w < 2; ++w) {
-        const uint32_t x0 = g.b0[p][w] ^ 0x80808080u, x1 = g.b1[p][w] ^ 0x80808080u;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // Byte e of both k-rows -> the f16 pair (B[k][n], B[k+1][n]).
-          const uint32_t sel = 0x0c000c00u | (uint32_t)(4 + e) << 16 | (uint32_t)e;
-          const uint32_t pr = __builtin_amdgcn_perm(x1, x0, sel) | magic;
-          const half2v v = __builtin_bit_cast(half2v, pr) - bias;
-          const int n = 8 * bc + 4 * w + e;
-          bs[buf][(n * kW8LD + 2 * (bkp + 16 * p)) / 2] = __builtin_bit_cast(uint32_t, v);
-        }
+      for (int wd = 0; wd < 4; ++wd) {
+        const uint32_t x = g.b[h][wd] ^ 0x80808080u;
+        pr[2 * wd] = __builtin_amdgcn_perm(0u, x, 0x0c010c00u) | magic;
+        pr[2 * wd + 1] = __builtin_amdgcn_perm(0u, x, 0x0c030c02u) | magic;
       }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        half8v v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const half2v hp = __builtin_bit_cast(half2v, pr[4 * c + j]) - bias;
+          v[2 * j] = hp[0];
+          v[2 * j + 1] = hp[1];
+        }
+        *reinterpret_cast<half8v*>(&bs[buf][w8_b_at(br, 4 * bc + 2 * h + c)]) = v;
+      }
+    }
   };
 
   float16v acc[2][2];
@@ -930,8 +955,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
       half8v bf[2];
 #pragma unroll
       for (int ni = 0; ni < 2; ++ni)
-        bf[ni] = __builtin_bit_cast(half8v, *reinterpret_cast<const uint4v*>(
-                                                &bs[buf][((64 * wn + 32 * ni + li) * kW8LD + 16 * ks + 8 * lh) / 2]));
+        bf[ni] = v_frag_tr<kW8BN>(bs[buf], w8_b_tr_offset(lane, 2 * wn + ni), ks);
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
         const half8v af = as[buf][((64 * wm + 32 * mi + li) * kW8LD + 16 * ks + 8 * lh) / 8];
