@@ -1210,19 +1210,21 @@ constexpr char kManifest[] = R"JSON({
     {
      "device_kernel": "w8a16_gemm_kernel",
      "source": "neso_amd/csrc/qmatmul.hip",
-     "template_params": [],
-     "when": "K, N, lda, ldb multiples of 8 and A 16-byte / B 8-byte aligned: 128 x 128 MFMA tiles, B dequantised into LDS",
-     "threadgroup_size": "256",
-     "num_warps": "4",
+     "template_params": [
+      "T"
+     ],
+     "when": "K, N, lda, ldb multiples of 8 and A 16-byte / B 8-byte aligned: T x T MFMA tiles, B dequantised into LDS as [k][n] f16 and read transposed; T = 256 (eight waves of 64 x 128) when cdiv(M, 256) * cdiv(N, 256) >= cus, else T = 128 (four waves of 64 x 64)",
+     "threadgroup_size": "2 * T",
+     "num_warps": "T // 32",
      "grid": [
-      "cdiv(N, 128)",
-      "cdiv(M, 128)",
+      "cdiv(N, T)",
+      "cdiv(M, T)",
       "1"
      ],
      "constants": {
-      "block_m": "128",
-      "block_n": "128",
-      "block_k": "32"
+      "block_m": "T",
+      "block_n": "T",
+      "block_k": "64"
      }
     },
     {
@@ -1333,19 +1335,21 @@ constexpr char kManifest[] = R"JSON({
     {
      "device_kernel": "w8a16_gemm_kernel",
      "source": "neso_amd/csrc/qmatmul.hip",
-     "template_params": [],
-     "when": "K, N, lda, ldb multiples of 8 and A 16-byte / B 8-byte aligned: 128 x 128 MFMA tiles, B dequantised into LDS",
-     "threadgroup_size": "256",
-     "num_warps": "4",
+     "template_params": [
+      "T"
+     ],
+     "when": "K, N, lda, ldb multiples of 8 and A 16-byte / B 8-byte aligned: T x T MFMA tiles, B dequantised into LDS as [k][n] f16 and read transposed; T = 256 (eight waves of 64 x 128) when cdiv(M, 256) * cdiv(N, 256) >= cus, else T = 128 (four waves of 64 x 64)",
+     "threadgroup_size": "2 * T",
+     "num_warps": "T // 32",
      "grid": [
-      "cdiv(N, 128)",
-      "cdiv(M, 128)",
+      "cdiv(N, T)",
+      "cdiv(M, T)",
       "1"
      ],
      "constants": {
-      "block_m": "128",
-      "block_n": "128",
-      "block_k": "32"
+      "block_m": "T",
+      "block_n": "T",
+      "block_k": "64"
      }
     },
     {

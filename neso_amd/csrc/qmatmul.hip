@@ -836,56 +836,65 @@ __global__ __launch_bounds__(kThreads) void w4a16_mfma_kernel(W4Args a) {
 // Double-buffered LDS, global loads one step ahead.
 // K-step 64: 16 MFMAs per wave between barriers (measured at 4096^3 on one
 // box: 179.0 us against 181.9 us with K-steps of 32).
-constexpr int kW8BM = 128, kW8BN = 128, kW8BK = 64, kW8LD = kW8BK + 8;
-constexpr int kW8AP = kW8BK / 32;  // 16-byte A pieces per thread and 64-row half
+constexpr int kW8BK = 64, kW8LD = kW8BK + 8;
+constexpr int kW8AP = kW8BK / 32;  // 16-byte A pieces per thread and row half
 
-// B tile in LDS: [k][n] f16 rows of 128 halves (16 chunks of 16 bytes, one
-// row spans every bank), chunk c of row r at c ^ 5 (r % 4).  A store pass
-// (16 lanes: 4 rows x chunks 4 j + s of 4 column groups j) then covers 16
-// positions 4 (j ^ i) + (s ^ i), and so does a transposed-read pass (4 rows
-// i x chunks 4 u .. 4 u + 3): every bank once.
-__device__ __forceinline__ int w8_b_at(int r, int c) { return r * kW8BN + 8 * (c ^ (5 * (r & 3))); }
-// This lane's offset for the B fragment of column tile u (v_frag_tr's
-// addressing: key row 8 (l / 32) + (l % 16) / 4, columns 32 u + 16 ((l / 16)
-// % 2) + 4 (l % 4)); adding 4 or 16 rows keeps the swizzle.
-__device__ __forceinline__ int w8_b_tr_offset(int lane, int u) {
+// B tile in LDS: [k][n] f16 in 128-column halves, rows of 128 halves (16
+// chunks of 16 bytes, one row spans every bank); in half hb, chunk c of row
+// r sits at c ^ 5 (r % 4) ^ 2 hb.  A store pass (16 lanes: 4 rows x chunks
+// 4 j + s of 4 column groups j, or with two halves 2 rows x 2 x 4 groups)
+// covers 16 positions 4 (j ^ i) + (s ^ i [^ 2]), and so does a transposed-
+// read pass (4 rows i x chunks 4 u .. 4 u + 3): every bank once.
+__device__ __forceinline__ int w8_b_at(int hb, int r, int c) {
+  return (hb * kW8BK + r) * 128 + 8 * (c ^ (5 * (r & 3)) ^ (2 * hb));
+}
+// This lane's offset for the B fragment of column tile u of half hb
+// (v_frag_tr's addressing: row 8 (l / 32) + (l % 16) / 4, columns 32 u + 16
+// ((l / 16) % 2) + 4 (l % 4)); adding 4 or 16 rows keeps the swizzle.
+__device__ __forceinline__ int w8_b_tr_offset(int lane, int hb, int u) {
   const int row = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int cu = 32 * u + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  return w8_b_at(row, cu >> 3) + (cu & 7);
+  return w8_b_at(hb, row, cu >> 3) + (cu & 7);
 }
 
-__global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
-  __shared__ half8v as[2][kW8BM * kW8LD / 8];
-  __shared__ __attribute__((aligned(16))) half_t bs[2][kW8BK * kW8BN];  // [k][n], swizzled chunks
+// Workgroup tile T x T (T = 128: four waves of 64 x 64; T = 256: eight
+// waves of 64 x 128, a third fewer LDS bytes per MFMA), K-steps of kW8BK.
+template <int T>
+__global__ __launch_bounds__(2 * T) void w8a16_gemm_kernel(W8Args a) {
+  constexpr int NT = 2 * T;          // threads
+  constexpr int NI = T / 64;         // 32-column MFMA tiles per wave
+  constexpr int NH = T / 128;        // 128-column B halves
+  __shared__ half8v as[2][T * kW8LD / 8];
+  __shared__ __attribute__((aligned(16))) half_t bs[2][NH * kW8BK * 128];  // [half][k][n]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 31, lh = lane >> 5;
   // Tile order: the dispatch index is remapped so that each XCD takes a
   // contiguous run of logical tiles, and logical tiles go down groups of
-  // four m-tiles before moving to the next n-tile.  The ~32 workgroups an
-  // XCD runs at once then cover a 4 x 8 block of tiles, whose A rows and B
-  // columns its L2 serves to all of them.
+  // four m-tiles before moving to the next n-tile, so that the workgroups
+  // an XCD runs at once share the A rows and B columns its L2 holds.
   const int mt = (int)gridDim.y, nt = (int)gridDim.x;
   const int lid = (int)xcd_swizzle(blockIdx.y * gridDim.x + blockIdx.x, (uint32_t)(mt * nt));
   constexpr int kGroupM = 4;
   const int grp = lid / (kGroupM * nt), first = grp * kGroupM;
   const int gm = min(mt - first, kGroupM), in = lid % (kGroupM * nt);
-  const int m0 = (first + in % gm) * kW8BM, n0 = (in / gm) * kW8BN;
-  const int mrows = min(kW8BM, a.M - m0);
+  const int m0 = (first + in % gm) * T, n0 = (in / gm) * T;
+  const int mrows = min(T, a.M - m0);
   constexpr uint32_t kOut = 0x80000000u;
   const rsrc_t ra = make_rsrc(a.A + (int64_t)m0 * a.lda, (uint32_t)((mrows - 1) * a.lda + a.K) * 2u);
   // K >= 1 (the ABI rejects K = 0 with a non-empty output); the extent is
   // clamped at 0 anyway so a bad call cannot wrap it to ~4 GiB.
   const rsrc_t rb = make_rsrc(
-      a.B + n0, (uint32_t)max((int64_t)0, (a.K - 1) * (int64_t)a.ldb + min(kW8BN, a.N - n0)));
-  // A: rows (tid >> 2) + 64j, 16-byte pieces (tid & 3) + 4p of the step.
+      a.B + n0, (uint32_t)max((int64_t)0, (a.K - 1) * (int64_t)a.ldb + min(T, a.N - n0)));
+  // A: rows ar + (T/2) j, 16-byte pieces ap + 4p of the step.
   const int ar = tid >> 2, ap = tid & 3;
   // B: k-row br of the step, columns 32 bc .. 32 bc + 31 (two 16-byte
-  // pieces; four lanes read a row's 128 contiguous bytes).
-  static_assert(kW8BK * kW8BN == 32 * kThreads, "one 32-byte row piece per thread");
-  const int br = tid >> 2, bc = tid & 3;
-  const uint32_t nlim = (uint32_t)min(kW8BN, a.N - n0);
+  // pieces; four or eight lanes read a row's contiguous bytes).
+  static_assert(kW8BK * T == 32 * NT, "one 32-byte row piece per thread");
+  constexpr int BG = T / 32;  // column groups per row
+  const int br = tid / BG, bc = tid % BG;
+  const uint32_t nlim = (uint32_t)min(T, a.N - n0);
   struct Stage {
     half8v av[2][kW8AP];
     uint4v b[2];  // 16 int8 of row br, columns 32 bc + 16 h ..
@@ -897,7 +906,7 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
       const uint32_t aoob = kc < a.K ? 0u : kOut;
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        g.av[j][p] = buf_load_half8(ra, (((uint32_t)(ar + 64 * j) * a.lda + kc) * 2u) | aoob);
+        g.av[j][p] = buf_load_half8(ra, (((uint32_t)(ar + (T / 2) * j) * a.lda + kc) * 2u) | aoob);
     }
     // Pieces wholly past N are masked; a piece that straddles N (N % 16 =
     // 8) reads bytes of columns >= N, whose products only reach columns of
@@ -918,9 +927,9 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
     for (int p = 0; p < kW8AP; ++p)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        as[buf][((ar + 64 * j) * kW8LD + 8 * (ap + 4 * p)) / 8] = g.av[j][p];
+        as[buf][((ar + (T / 2) * j) * kW8LD + 8 * (ap + 4 * p)) / 8] = g.av[j][p];
     // Row br as f16 in [k][n] order: bytes (n, n+1) of a word -> one f16
-    // pair; chunk c of the row at w8_b_at(br, c).
+    // pair; chunk c of the row at w8_b_at.
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       uint32_t pr[8];
@@ -939,28 +948,32 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
           v[2 * j] = hp[0];
           v[2 * j + 1] = hp[1];
         }
-        *reinterpret_cast<half8v*>(&bs[buf][w8_b_at(br, 4 * bc + 2 * h + c)]) = v;
+        const int chunk = 4 * bc + 2 * h + c;  // of the T-wide row
+        *reinterpret_cast<half8v*>(&bs[buf][w8_b_at(chunk >> 4, br, chunk & 15)]) = v;
       }
     }
   };
 
-  float16v acc[2][2];
+  float16v acc[2][NI];
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = float16v{};
+    for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = float16v{};
+  // Wave (wm, wn) computes rows 64 wm .. and columns (T/2) wn ..: with T =
+  // 256 that is half wn of the B tile, with T = 128 tiles 2 wn, 2 wn + 1.
+  const int hb = NH == 2 ? wn : 0;
   auto compute = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < kW8BK / 16; ++ks) {
-      half8v bf[2];
+      half8v bf[NI];
 #pragma unroll
-      for (int ni = 0; ni < 2; ++ni)
-        bf[ni] = v_frag_tr<kW8BN>(bs[buf], w8_b_tr_offset(lane, 2 * wn + ni), ks);
+      for (int ni = 0; ni < NI; ++ni)
+        bf[ni] = v_frag_tr<128>(bs[buf], w8_b_tr_offset(lane, hb, NH == 2 ? ni : 2 * wn + ni), ks);
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
         const half8v af = as[buf][((64 * wm + 32 * mi + li) * kW8LD + 16 * ks + 8 * lh) / 8];
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma32x32x16(af, bf[ni], acc[mi][ni]);
+        for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32x32x16(af, bf[ni], acc[mi][ni]);
       }
     }
   };
@@ -983,10 +996,10 @@ __global__ __launch_bounds__(kThreads) void w8a16_gemm_kernel(W8Args a) {
   }
 
   // acc[mi][ni] register r: row 64wm + 32mi + 8(r/4) + 4(lane/32) + r%4,
-  // column 64wn + 32ni + lane%32.
+  // column (T/2) wn + 32ni + lane%32.
 #pragma unroll
-  for (int ni = 0; ni < 2; ++ni) {
-    const int n = n0 + 64 * wn + 32 * ni + li;
+  for (int ni = 0; ni < NI; ++ni) {
+    const int n = n0 + (T / 2) * wn + 32 * ni + li;
     if (n >= a.N) continue;
     const float s = a.scale ? (float)a.scale[n] : 1.f;
 #pragma unroll
@@ -1175,11 +1188,18 @@ hipError_t launch_w8a16(const W8Args& a, hipStream_t s) {
   const bool tiled = a.K % 8 == 0 && a.lda % 8 == 0 && a.N % 8 == 0 && a.ldb % 8 == 0 &&
                      (reinterpret_cast<uintptr_t>(a.A) & 15u) == 0 &&
                      (reinterpret_cast<uintptr_t>(a.B) & 7u) == 0 &&
-                     (int64_t)kW8BM * a.lda * 2 < ((int64_t)1 << 31) &&
+                     (int64_t)256 * a.lda * 2 < ((int64_t)1 << 31) &&
                      (int64_t)a.K * a.ldb < ((int64_t)1 << 31);
   if (tiled) {
-    const dim3 grid((a.N + kW8BN - 1) / kW8BN, (a.M + kW8BM - 1) / kW8BM);
-    return launch<&w8a16_gemm_kernel>(ktag("w8a16_gemm_kernel"), grid, dim3(kThreads), s, a);
+    // 256 x 256 tiles (a third fewer LDS bytes per MFMA) when they still
+    // give every CU a workgroup; 128 x 128 otherwise.
+    const int64_t big = (int64_t)((a.N + 255) / 256) * ((a.M + 255) / 256);
+    if (big >= device_cu_count()) {
+      const dim3 grid((a.N + 255) / 256, (a.M + 255) / 256);
+      return launch<&w8a16_gemm_kernel<256>>(ktag("w8a16_gemm_kernel", 256), grid, dim3(512), s, a);
+    }
+    const dim3 grid((a.N + 127) / 128, (a.M + 127) / 128);
+    return launch<&w8a16_gemm_kernel<128>>(ktag("w8a16_gemm_kernel", 128), grid, dim3(256), s, a);
   }
   const dim3 grid((a.N + 127) / 128, (a.M + 31) / 32);
   return launch<&w8a16_kernel>(ktag("w8a16_kernel"), grid, dim3(kThreads), s, a);

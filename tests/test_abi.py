@@ -217,6 +217,11 @@ CHOICE_CASES = [
      "fa2_fast_kernel", dict(D=128, QW=4, HALVES=1)),
     ("neso_flash_attention_fwd", [_P] * 4 + [4096, 128, 128, 0.08, 128, 64, 4096 * 128, 4096 * 128, 1],
      "fa2_fast_kernel", dict(D=128, QW=4, PAIR=1)),
+    # W8A16: 256 x 256 tiles once they give every CU a workgroup.
+    ("neso_w8a16_matmul", [_P] * 3 + [4096, 4096, 4096, 4096, 4096, 4096],
+     "w8a16_gemm_kernel", dict(T=256)),
+    ("neso_w8a16_matmul", [_P] * 3 + [520, 520, 3000, 3000, 1000, 3000],
+     "w8a16_gemm_kernel", dict(T=128)),
     # Short rows: the fast kernel with 128-query workgroups (N < 512).
     ("neso_flash_attention_fwd", [_P] * 4 + [128, 64, 64, 0.125, 64, 8, 128 * 64, 128 * 64, 0],
      "fa2_fast_kernel", dict(QW=4)),

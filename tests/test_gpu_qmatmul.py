@@ -220,6 +220,43 @@ def test_w8a16_tiled_and_fallback(gpu, m, n, k, scaled):
     assert Q.rel_err(c.cpu().numpy(), ref) < 1e-4
 
 
+@pytest.mark.parametrize("scaled", [False, True])
+def test_w8a16_large_tiles(gpu, scaled):
+    """The 256 x 256-tile kernel (chosen once its tiles give every CU a
+    workgroup) on ragged M (4000 = 15.6 tiles), N with a 16-byte B piece
+    straddling the end (4104 % 16 = 8) and K not a multiple of the 64-wide
+    K-step, against the float64 oracle on the fp16-rounded activations."""
+    import json
+    from neso_amd import _lib
+    m, n, k = 4000, 4104, 520
+    g = torch.Generator().manual_seed(17)
+    a = torch.randn(m, k, generator=g).half()
+    b = torch.randint(-128, 128, (k, n), generator=g, dtype=torch.int8)
+    s = (torch.rand(n, generator=g) * 0.1 + 0.001).half()
+    c = torch.full((m, n), float("nan"), dtype=torch.float32, device=DEV)
+    ad, bd, sd = a.to(DEV), b.to(DEV), s.to(DEV)
+    lib = _lib.load()
+    args = [ad.data_ptr(), bd.data_ptr(), c.data_ptr()] + ([sd.data_ptr()] if scaled else []) + \
+        [k, k, n, n, m, n, None]
+    fn = lib.neso_w8a16_scaled_matmul if scaled else lib.neso_w8a16_matmul
+    assert lib.neso_plan_begin(0) == _lib.NESO_OK
+    try:
+        assert fn(*args) == _lib.NESO_OK
+    finally:
+        plan = json.loads(lib.neso_plan_end().decode())["launches"]
+    if torch.cuda.get_device_properties(0).multi_processor_count <= 16 * 17:
+        assert plan[0]["template_args"] == [256], plan
+    if scaled:
+        neso_amd.w8a16_scaled_matmul(ad, bd, c, sd, k, k, n, n, M=m, N=n)
+        ref = Q.w8a16_scaled_matmul(a.double().numpy(), b.double().numpy(), s.double().numpy())
+    else:
+        neso_amd.w8a16_matmul(ad, bd, c, k, k, n, n, M=m, N=n)
+        ref = Q.w8a16_matmul(a.double().numpy(), b.double().numpy())
+    torch.cuda.synchronize()
+    assert torch.isfinite(c).all()
+    assert Q.rel_err(c.cpu().numpy(), ref) < 1e-4
+
+
 @pytest.mark.parametrize("kgroups", ["1", "2"])
 @pytest.mark.parametrize("m,n,k", [(128, 11008, 4096), (200, 300, 4096), (256, 1000, 4128),
                                    (300, 129, 96), (640, 256, 1024)])
