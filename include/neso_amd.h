@@ -78,7 +78,8 @@ const char* neso_plan_end(void);
  * exits.  Launched on a second stream while a workload runs on another, it
  * gives the clock that workload ran at: d(out[2 i]) / d(out[2 i + 1]) * 100
  * MHz.  `out` is device memory of 2 * samples uint64 values, 8-byte aligned;
- * 1 <= samples, gap_ticks <= 2^20.
+ * 1 <= samples, gap_ticks <= 2^20, and samples * gap_ticks <= 2^30 (the wave
+ * runs at most 10.7 s).
  */
 int neso_clock_sample(uint64_t* out, int32_t samples, int32_t gap_ticks, void* stream);
 

@@ -255,6 +255,10 @@ int neso_clock_sample(uint64_t* out, int32_t samples, int32_t gap_ticks, void* s
   if (samples < 1 || samples > (1 << 20) || gap_ticks < 1 || gap_ticks > (1 << 20))
     return fail(NESO_EINVAL, "clock_sample: samples=%d, gap_ticks=%d outside [1, 2^20]", samples,
                 gap_ticks);
+  // The wave spins samples * gap_ticks reference ticks: at most 2^30 (10.7 s).
+  if ((int64_t)samples * gap_ticks > (int64_t)1 << 30)
+    return fail(NESO_EINVAL, "clock_sample: samples * gap_ticks = %lld above 2^30 (10.7 s)",
+                (long long)samples * gap_ticks);
   return launched(neso::launch<&neso::clock_sample_kernel>(
                       neso::ktag("clock_sample_kernel"), dim3(1), dim3(64),
                       static_cast<hipStream_t>(stream), out, (int)samples, (int)gap_ticks),

@@ -254,9 +254,9 @@ def test_clock_sample_arguments(lib):
     """The clock sampler rejects bad buffers and counts before any HIP call,
     and launches exactly one 64-thread wave."""
     for args in ([None, 8, 100], [A16 + 4, 8, 100], [A16, 0, 100], [A16, 8, 0],
-                 [A16, (1 << 20) + 1, 100], [A16, 8, (1 << 20) + 1]):
+                 [A16, (1 << 20) + 1, 100], [A16, 8, (1 << 20) + 1], [A16, 1 << 20, 1025]):
         assert lib.neso_clock_sample(*args, None) == _lib.NESO_EINVAL, args
-    status, launches = _plan(lib, lib.neso_clock_sample, [A16, 8, 100, None], 256)
+    status, launches = _plan(lib, lib.neso_clock_sample, [A16, 1 << 20, 1024, None], 256)
     assert status == _lib.NESO_OK
     assert [(k["device_kernel"], k["grid"], k["threadgroup_size"]) for k in launches] == [
         ("clock_sample_kernel", [1, 1, 1], 64)]
