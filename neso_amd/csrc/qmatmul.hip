@@ -1182,9 +1182,10 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
 }
 
 hipError_t launch_w8a16(const W8Args& a, hipStream_t s) {
-  // The tiled kernel reads A in 16-byte and B in 8-byte pieces: it needs
-  // those pieces aligned and never straddling the end of a row, and buffer
-  // offsets below 2^31 bytes.
+  // The tiled kernel reads A and B in 16-byte pieces: A's must be 16-byte
+  // aligned and never straddle the end of a row; B's need 8-byte alignment
+  // (a piece that straddles N reads columns that are never stored).  Buffer
+  // offsets stay below 2^31 bytes.
   const bool tiled = a.K % 8 == 0 && a.lda % 8 == 0 && a.N % 8 == 0 && a.ldb % 8 == 0 &&
                      (reinterpret_cast<uintptr_t>(a.A) & 15u) == 0 &&
                      (reinterpret_cast<uintptr_t>(a.B) & 7u) == 0 &&
