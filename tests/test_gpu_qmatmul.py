@@ -58,6 +58,36 @@ def test_ragged(gpu, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
+@pytest.mark.parametrize("m", [3, 16])
+@pytest.mark.parametrize("n,k", [(4100, 4096), (13000, 2048), (20000, 2048)])
+def test_skinny_tiles_per_workgroup(gpu, m, n, k):
+    """The X-in-LDS skinny kernel gives each workgroup T = ceil(tiles / CUs)
+    16-row tiles, at most 4: N = 4100 / 13000 / 20000 take T = 2, 4 and 4
+    with more workgroups than CUs on 256 CUs (N = 11008 takes T = 3 in the
+    config-5 test).  Checked against the float64 oracle."""
+    import json
+    from neso_amd import _lib
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n)
+    words = Q.pack_int4(codes.numpy())
+    lib = _lib.load()
+    xd, wd, sd = x.to(DEV), torch.as_tensor(words).to(DEV), scales.to(DEV)
+    y = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert lib.neso_plan_begin(cus) == _lib.NESO_OK
+    try:
+        assert lib.neso_w4a16_matmul(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), y.data_ptr(),
+                                     m, n, k, k, n, 32, 8, None) == _lib.NESO_OK
+    finally:
+        plan = json.loads(lib.neso_plan_end().decode())["launches"]
+    tiles = (n + 15) // 16
+    t = min(4, -(-tiles // cus))
+    assert [(p["device_kernel"], p["template_args"][1], p["grid"][0]) for p in plan] == [
+        ("w4a16_skinny_lds_kernel", t, -(-tiles // t))], plan
+    out = gpu_w4(x, words, scales)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy(), dtype=np.float64)
+    assert Q.rel_err(out.float().numpy(), ref) <= 2e-3
+
+
 @pytest.mark.parametrize("m", [1, 3])
 @pytest.mark.parametrize("k", [2048, 2080, 2112, 4064, 4096, 6144])
 @pytest.mark.parametrize("n", [1, 65, 300])
