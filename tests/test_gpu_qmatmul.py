@@ -251,14 +251,16 @@ def test_w8a16_tiled_and_fallback(gpu, m, n, k, scaled):
 
 
 @pytest.mark.parametrize("scaled", [False, True])
-def test_w8a16_large_tiles(gpu, scaled):
+@pytest.mark.parametrize("m,n,k", [(4000, 4104, 520), (1300, 11008, 256)])
+def test_w8a16_large_tiles(gpu, scaled, m, n, k):
     """The 256 x 256-tile kernel (chosen once its tiles give every CU a
     workgroup) on ragged M (4000 = 15.6 tiles), N with a 16-byte B piece
     straddling the end (4104 % 16 = 8) and K not a multiple of the 64-wide
-    K-step, against the float64 oracle on the fp16-rounded activations."""
+    K-step; and on 6 x 43 tiles, whose tile order (groups of four m-tiles)
+    ends in a group of two.  Against the float64 oracle on the fp16-rounded
+    activations."""
     import json
     from neso_amd import _lib
-    m, n, k = 4000, 4104, 520
     g = torch.Generator().manual_seed(17)
     a = torch.randn(m, k, generator=g).half()
     b = torch.randint(-128, 128, (k, n), generator=g, dtype=torch.int8)
