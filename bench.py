@@ -338,7 +338,8 @@ def fa2_workload(neso_amd, torch, I, B, H, N, d, causal, want_cpu, f32=False):
         q, k, v = q.float(), k.float(), v.float()
     out = torch.empty(q.shape, dtype=torch.float32, device="cuda")
     scale = A.default_scale(d)
-    launch = lambda i: neso_amd.attention(q, k, v, causal=causal, out=out)
+    # Synthetic inputs are far inside the fp16 range: no per-call range check.
+    launch = lambda i: neso_amd.attention(q, k, v, causal=causal, out=out, check_range=False)
     cpu = None
     if want_cpu:
         qc, kc, vc = (t.cpu() for t in (q, k, v))
@@ -374,7 +375,8 @@ def relpos_precompute_workload(neso_amd, torch, I, want_cpu):
     qd, krd, bud, bvd = (x.cuda() for x in (q, kr, bu, bv))
     q_u = torch.empty(h, t, d, dtype=torch.float16, device="cuda")
     rel = torch.empty(h, t, t, dtype=torch.float16, device="cuda")
-    launch = lambda i: neso_amd.rel_pos_precompute(qd, krd, bud, bvd, t, d, h, d ** -0.5, q_u, rel)
+    launch = lambda i: neso_amd.rel_pos_precompute(qd, krd, bud, bvd, t, d, h, d ** -0.5, q_u, rel,
+                                                   check_range=False)
     cpu = None
     if want_cpu:
         qn, krn, bun, bvn = (x.numpy() for x in (q, kr, bu, bv))

@@ -91,10 +91,30 @@ def _stream(stream: Any, *tensors: Any) -> int:
     return 0
 
 
+def _check_f16_range(t: Any, name: str, bh: int, n: int, d: int, s_row: int, s_bh: int) -> None:
+    """Raise NesoArgumentError if an fp32 input the kernel reads reaches the
+    fp16 limit: the fp32-input kernels split each element into fp16 hi + lo,
+    so |x| >= 65504 would turn into inf or NaN in the output.  NaN inputs
+    pass (they give NaN rows, as an fp32 computation does).  The check reads
+    the device data and synchronises, so it is skipped for raw addresses,
+    for host tensors (rejected at launch) and while the current stream is
+    being captured into a graph."""
+    if (not isinstance(t, torch.Tensor) or t.device.type != "cuda"
+            or torch.cuda.is_current_stream_capturing()):
+        return
+    view = t.as_strided((bh, n, d), (s_bh, s_row, 1))
+    m = view.abs().amax().item()
+    if m >= 65504.0:
+        raise _lib.NesoArgumentError(
+            _lib.NESO_EINVAL, f"{name}: |x| reaches {m:g}; fp32 Q/K/V must lie within the fp16 "
+                              f"range (|x| < 65504)")
+
+
 def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scale: float, *,
                         head_dim: int | None = None, batch_heads: int = 1,
                         stride_bh_qo: int = 0, stride_bh_kv: int = 0, causal: bool = False,
-                        qkv_dtype: str | None = None, stream=None) -> None:
+                        qkv_dtype: str | None = None, check_range: bool = True,
+                        stream=None) -> None:
     """FA2 forward, O = softmax(Q K^T * scale) V.
 
     Positional arguments as the reference kernel (tests/test_flash_attention.py
@@ -104,6 +124,9 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
     ``batch_heads`` with ``stride_bh_qo`` / ``stride_bh_kv`` for B*H slices
     in one launch, and ``causal``.  ``qkv_dtype`` is 'f16' or 'f32' as in
     the reference's generator (:79-89); for tensors it follows Q's dtype.
+    fp32 tensors must hold |x| < 65504 (the kernel splits them into fp16
+    hi + lo); ``check_range`` verifies that before the launch (one device
+    reduction and a synchronisation per input, skipped under graph capture).
     """
     if head_dim is None:
         if not isinstance(Q, torch.Tensor):
@@ -119,6 +142,11 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
         for t, nm, sp in ((Q, "Q", span_q), (K, "K", span_kv), (V, "V", span_kv),
                           (O, "O", span_q)):
             _extent(t, nm, sp)
+        if qkv_dtype == "f32" and check_range:
+            for t, nm, sr, sb in ((Q, "Q", stride_qo, stride_bh_qo), (K, "K", stride_kv, stride_bh_kv),
+                                  (V, "V", stride_kv, stride_bh_kv)):
+                if isinstance(t, torch.Tensor) and t.dtype == torch.float32:
+                    _check_f16_range(t, nm, batch_heads, N, head_dim, sr, sb)
     lib = _lib.load()
     dt = torch.float32 if qkv_dtype == "f32" else torch.float16
     fn = lib.neso_flash_attention_f32_fwd if qkv_dtype == "f32" else lib.neso_flash_attention_fwd
@@ -232,7 +260,7 @@ def rel_pos_fa2_fwd(Q, K, V, bias, O, T: int, stride: int, scale: float, stride_
 
 
 def rel_pos_precompute(Q, K_rel, bias_u, bias_v, T: int, d: int, nh: int, scale: float, Q_u,
-                       rel_bias, *, stream=None) -> None:
+                       rel_bias, *, check_range: bool = True, stream=None) -> None:
     """Q_u = Q + bias_u and the unscaled dense rel_bias[h, i, j] = (Q + bias_v)_i .
     K_rel[T - 1 - i + j] on the GPU.
 
@@ -242,13 +270,27 @@ def rel_pos_precompute(Q, K_rel, bias_u, bias_v, T: int, d: int, nh: int, scale:
     the two outputs it returns: Q_u fp16 [nh, T, d] and rel_bias fp16
     [nh, T, T], the inputs of :func:`rel_pos_fa2_fwd` in the dense mode.
     Q, K_rel, bias_u, bias_v are contiguous fp32 [nh, T, d], [nh, 2T-1, d],
-    [nh, d], [nh, d].
+    [nh, d], [nh, d].  The bias is formed from fp16 hi + lo splits of
+    Q + bias_v and K_rel, so their elements must lie below 65504 in
+    magnitude; ``check_range`` verifies that before the launch (device
+    reductions and a synchronisation, skipped under graph capture).
     """
     if T > 0 and nh > 0:
         for t, nm, n in ((Q, "Q", nh * T * d), (K_rel, "K_rel", nh * (2 * T - 1) * d),
                          (bias_u, "bias_u", nh * d), (bias_v, "bias_v", nh * d),
                          (Q_u, "Q_u", nh * T * d), (rel_bias, "rel_bias", nh * T * T)):
             _extent(t, nm, n)
+        if check_range and all(isinstance(x, torch.Tensor) and x.device.type == "cuda"
+                               and x.dtype == torch.float32 for x in (Q, K_rel, bias_v)) \
+                and not torch.cuda.is_current_stream_capturing():
+            qv = (Q.reshape(-1)[:nh * T * d].view(nh, T, d)
+                  + bias_v.reshape(-1)[:nh * d].view(nh, 1, d))
+            for x, nm in ((qv, "Q + bias_v"), (K_rel.reshape(-1)[:nh * (2 * T - 1) * d], "K_rel")):
+                m = x.abs().amax().item()
+                if m >= 65504.0:
+                    raise _lib.NesoArgumentError(
+                        _lib.NESO_EINVAL, f"{nm}: |x| reaches {m:g}; the precompute needs "
+                                          f"|Q + bias_v|, |K_rel| < 65504 (fp16 hi + lo split)")
     lib = _lib.load()
     f32, f16 = torch.float32, torch.float16
     st = lib.neso_rel_pos_precompute(
@@ -355,9 +397,11 @@ def launch(name: str, *args, **kwargs) -> None:
 # Tensor-level conveniences over the launchers above.
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool = False,
-              scale: float | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+              scale: float | None = None, out: torch.Tensor | None = None,
+              check_range: bool = True) -> torch.Tensor:
     """FA2 forward over [..., N, d] fp16 or fp32 tensors (contiguous, one
-    dtype); returns fp32 [..., N, d]."""
+    dtype); returns fp32 [..., N, d].  ``check_range`` as in
+    flash_attention_fwd (fp32 inputs only)."""
     if q.shape != k.shape or q.shape != v.shape:
         raise ValueError("q, k, v must have the same shape [..., N, d]")
     if not (q.is_contiguous() and k.is_contiguous() and v.is_contiguous()):
@@ -372,7 +416,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, causal: bool
              f"out must be a contiguous fp32 tensor of shape {tuple(q.shape)}")
     scale = 1.0 / math.sqrt(d) if scale is None else scale
     flash_attention_fwd(q, k, v, out, n, d, d, scale, head_dim=d, batch_heads=bh,
-                        stride_bh_qo=n * d, stride_bh_kv=n * d, causal=causal)
+                        stride_bh_qo=n * d, stride_bh_kv=n * d, causal=causal,
+                        check_range=check_range)
     return out
 
 

@@ -114,6 +114,39 @@ def test_padded_strides_and_slices(gpu):
     assert (o.cpu()[..., d:] == 7.0).all()  # padding untouched
 
 
+def test_fp16_range_checked(gpu):
+    """fp32 inputs reaching the fp16 limit are rejected before the launch
+    (their fp16 hi part would be inf); row padding the kernel does not read
+    is not checked; NaN inputs are not rejected; under graph capture the
+    check is skipped."""
+    q, k, v = (x.to(DEV) for x in _inputs(1, 2, 64, 64, seed=3))
+    for bad in (7e4, -float("inf")):
+        k[0, 1, 5, 7] = bad
+        with pytest.raises(neso_amd.NesoArgumentError, match="K: "):
+            neso_amd.attention(q, k, v)
+    k[0, 1, 5, 7] = 0.5
+    v[0, 0, 3, 2] = 65503.0  # largest fp16 below the limit: accepted
+    neso_amd.attention(q, k, v)
+    n, d, stride = 64, 64, 68
+    buf = torch.randn(n, stride, device=DEV)
+    buf[:, d:] = 1e9
+    o = torch.zeros(n, stride, device=DEV)
+    neso_amd.flash_attention_fwd(buf, buf, buf, o, n, stride, stride, 0.125, head_dim=d)
+    q[0, 0, 0, 0] = float("nan")
+    out = neso_amd.attention(q, k, v)
+    torch.cuda.synchronize()
+    assert torch.isfinite(o[:, :d]).all()
+    assert torch.isfinite(out[0, 1]).all()  # the other head is untouched by the NaN
+    q[0, 0, 0, 0] = 1e6
+    out = torch.empty(q.shape, device=DEV)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        neso_amd.attention(q, k, v, out=out)  # no synchronisation inside capture
+    torch.cuda.synchronize()
+
+
 def test_f32_errors(gpu):
     x = torch.zeros(128, 128, device=DEV)
     o = torch.zeros(128, 128, device=DEV)

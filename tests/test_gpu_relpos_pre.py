@@ -98,6 +98,30 @@ def test_ragged(gpu, t, d, nh):
     _check_pre(Q, K_rel, bu, bv)
 
 
+def test_fp16_range_checked(gpu):
+    """Q + bias_v or K_rel elements at the fp16 limit (their hi part would
+    be inf) are rejected before the launch; Q large but Q + bias_v within
+    range is accepted."""
+    rs = np.random.RandomState(4)
+    t, d, nh = 40, 64, 2
+    Q = rs.randn(nh, t, d).astype(np.float32)
+    K_rel = rs.randn(nh, 2 * t - 1, d).astype(np.float32)
+    bu, bv = (rs.randn(nh, d).astype(np.float32) * 0.1 for _ in range(2))
+    bad = K_rel.copy()
+    bad[1, 7, 3] = 7e4
+    with pytest.raises(neso_amd.NesoArgumentError, match="K_rel: "):
+        _gpu_pre(Q, bad, bu, bv)
+    bad = Q.copy()
+    bad[0, 5, 9] = -7e4
+    with pytest.raises(neso_amd.NesoArgumentError, match="Q \\+ bias_v: "):
+        _gpu_pre(bad, K_rel, bu, bv)
+    Q2, bv2 = Q.copy(), bv.copy()
+    Q2[0, :, 9] += 7e4
+    bv2[0, 9] -= 7e4
+    q_u, rel = _gpu_pre(Q2, K_rel, bu, bv2)
+    assert torch.isfinite(rel).all()
+
+
 def test_diagonal_structure(gpu):
     """K_rel row r one-hot on feature r % d, zero biases: rel_bias[i, j] is
     Q[i, (T - 1 - i + j) % d] exactly, which pins the relative index and its
