@@ -65,6 +65,17 @@ constexpr int kNonTemporal = 2;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, bytes, 0x00020000);
 }
+// Byte offset of element idx of a buffer of n elements of `bytes` each, or
+// an offset past any buffer when idx is outside [0, n) (the load then
+// returns zero).  A negative idx must not reach the load as a wrapped
+// offset: the compiler may move a constant part of an offset into the
+// instruction's immediate field, and the range check of raw buffer loads
+// then sees the register part alone, so an in-range element whose register
+// part is a wrapped negative number would read as zero.
+__device__ __forceinline__ uint32_t elem_offset(int idx, int n, uint32_t bytes) {
+  return (uint32_t)idx < (uint32_t)n ? (uint32_t)idx * bytes : 0xFFFFFFF0u;
+}
+
 __device__ __forceinline__ half8v buf_load_half8(rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(half8v, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, 0));
 }

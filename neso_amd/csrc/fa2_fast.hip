@@ -33,6 +33,8 @@
 //   padding, 16-byte chunks swizzled against bank conflicts, and the V^T
 //   operand of P V is read with gfx950's transposing LDS load,
 //   ds_read_b64_tr_b16.
+#include <type_traits>
+
 #include "common.h"
 #include "fa2_tiles.h"
 #include "neso_internal.h"
@@ -237,6 +239,31 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   auto vslot = [&](int s) {
     return kLive ? gbase + 2 * KSLOT + s * VSLOT : gbase + s * (KSLOT + VSLOT) + KSLOT;
   };
+  // The slots as LDS byte addresses (the M0 operand of the LDS-direct
+  // loads), at this wave's first 1 KiB piece (x = LCH wave): a scalar base
+  // plus a constant.  The empty asm makes each use re-add the constant to
+  // the one base register in the scalar unit, instead of the compiler
+  // hoisting every slot's address out of the loop into VGPR lanes (a
+  // v_readlane per load).
+  const uint32_t wbase_lds = lds_addr(smem) + (uint32_t)(kg * GLDS * 2 + LCH * wave * RPI * D * 2);
+  auto lds_base = [&]() {
+    uint32_t b = wbase_lds;
+    asm volatile("" : "+s"(b));
+    return b;
+  };
+  auto kslot_lds = [&](int s) {
+    return lds_base() + (uint32_t)((kLive ? s * KSLOT : s * (KSLOT + VSLOT)) * 2);
+  };
+  auto vslot_lds = [&](int s) {
+    return lds_base() + (uint32_t)((kLive ? 2 * KSLOT + s * VSLOT : s * (KSLOT + VSLOT) + KSLOT) * 2);
+  };
+  // Bytes of K (or V) from key row kb0 to the end of the block (the
+  // descriptor's extent: rows past N read as zeros).  Scalar arithmetic
+  // only: a descriptor in VGPRs would wrap every load in a waterfall loop.
+  auto block_bytes = [&](int kb0) {
+    const int rem = N - kb0;
+    return (uint32_t)((rem < kKB ? rem : kKB) * p.stride_kv * 2);
+  };
 
   // Global -> LDS directly (buffer_load_dwordx4 ... lds).  One instruction
   // fills 1 KiB of LDS, lane l's 16 bytes at byte 16 l, i.e. RPI rows of a
@@ -250,30 +277,24 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     kgo[j] = (row * p.stride_kv + 8 * (pos ^ kswz<D>(row))) * 2;
     vgo[j] = (row * p.stride_kv + 8 * (pos ^ vswz<D>(row))) * 2;
   }
-  // Block i's K (or V) tile alone into its slot (two query waves).
-  auto tile_load = [&](int i, bool v) {
+  // Block i's K (or V) tile alone into slot s (two query waves; block i
+  // lives in slot i % 2).  Only issued for blocks that start before N.
+  auto tile_load = [&](int i, bool v, int s) {
     const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
-    const uint32_t bytes = __builtin_amdgcn_readfirstlane(max(0, min(N - kb0, kKB)) * p.stride_kv * 2);
-    const rsrc_t r = make_rsrc((v ? Vh : Kh) + (int64_t)kb0 * p.stride_kv, bytes);
-    half_t* const base = v ? vslot(i & 1) : kslot(i & 1);
+    const rsrc_t r = make_rsrc((v ? Vh : Kh) + (int64_t)kb0 * p.stride_kv, block_bytes(kb0));
 #pragma unroll
-    for (int j = 0; j < LCH; ++j) {
-      const int x = LCH * wave + j;
-      lds_dma16(r, __builtin_amdgcn_readfirstlane(lds_addr(base + x * RPI * D)), v ? vgo[j] : kgo[j]);
-    }
+    for (int j = 0; j < LCH; ++j)
+      lds_dma16(r, (v ? vslot_lds(s) : kslot_lds(s)) + (uint32_t)(j * RPI * D * 2), v ? vgo[j] : kgo[j]);
   };
   auto lds_load = [&](int i, int s) {
     const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
-    // readfirstlane: min/max of scalars may be formed on the VALU, and a
-    // descriptor in VGPRs would wrap every load in a waterfall loop.
-    const uint32_t bytes = __builtin_amdgcn_readfirstlane(max(0, min(N - kb0, kKB)) * p.stride_kv * 2);
+    const uint32_t bytes = block_bytes(kb0);
     const rsrc_t rk = make_rsrc(Kh + (int64_t)kb0 * p.stride_kv, bytes);
     const rsrc_t rv = make_rsrc(Vh + (int64_t)kb0 * p.stride_kv, bytes);
 #pragma unroll
     for (int j = 0; j < LCH; ++j) {
-      const int x = LCH * wave + j;
-      lds_dma16(rk, __builtin_amdgcn_readfirstlane(lds_addr(kslot(s) + x * RPI * D)), kgo[j]);
-      lds_dma16(rv, __builtin_amdgcn_readfirstlane(lds_addr(vslot(s) + x * RPI * D)), vgo[j]);
+      lds_dma16(rk, kslot_lds(s) + (uint32_t)(j * RPI * D * 2), kgo[j]);
+      lds_dma16(rv, vslot_lds(s) + (uint32_t)(j * RPI * D * 2), vgo[j]);
     }
   };
 
@@ -322,15 +343,16 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     BandRegs r{};
     if constexpr (BIAS) {
       const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
-      const uint32_t j0 = (uint32_t)(qw0 - kb0 - (kKB - 1) + N - 1 + lane);
-      r.t[0] = buf_load_f32(rsT, j0 * 4u);
-      if constexpr (BENT > 64) r.t[1] = buf_load_f32(rsT, (j0 + 64u) * 4u);
+      const int j0 = qw0 - kb0 - (kKB - 1) + N - 1 + lane;
+      r.t[0] = buf_load_f32(rsT, elem_offset(j0, 2 * N - 1, 4));
+      if constexpr (BENT > 64) r.t[1] = buf_load_f32(rsT, elem_offset(j0 + 64, 2 * N - 1, 4));
     }
     return r;
   };
-  auto band_store = [&](int i, const BandRegs& r) {
+  // Band slots by block parity: block i uses slot i % 2 (par).
+  auto band_store = [&](int par, const BandRegs& r) {
     if constexpr (BIAS) {
-      float* const slot = band + BSLOT * (i & 1) + BSLOT - 1;
+      float* const slot = band + BSLOT * par + BSLOT - 1;
       slot[-lane] = r.t[0] * tscale;
       if constexpr (BENT > 64) slot[-(lane + 64)] = r.t[1] * tscale;  // within the slot
     }
@@ -340,10 +362,10 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // entry ql - key + KB - 1 at position BSLOT - KB - ql + key: consecutive
   // registers read consecutive positions (pairs of them per ds_read2_b32,
   // straight into the accumulator registers).
-  auto band_acc = [&](int i, int t) {
+  auto band_acc = [&](int par, int t) {
     float16v a;
     if constexpr (BIAS) {
-      const float* b = band + BSLOT * (i & 1) + BSLOT - kKB - ql + 8 * g + 32 * t;
+      const float* b = band + BSLOT * par + BSLOT - kKB - ql + 8 * g + 32 * t;
 #pragma unroll
       for (int r = 0; r < 16; ++r) a[r] = b[16 * (r >> 3) + (r & 7)];
     } else {
@@ -352,13 +374,13 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     return a;
   };
 
-  // Scores of block i (K tile in k_l), with its bias band as initial
-  // accumulator.
-  auto qk = [&](float16v(&s)[NT], const half_t* k_l, int i) {
+  // Scores of a block (K tile in k_l), with its bias band (slot par) as
+  // initial accumulator.
+  auto qk = [&](float16v(&s)[NT], const half_t* k_l, int par) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       s[t] = mfma32x32x16(load_half8(k_l + koff[0] + 32 * t * D), qf[0],
-                          BIAS ? band_acc(i, t) : float16v{});
+                          BIAS ? band_acc(par, t) : float16v{});
 #pragma unroll
       for (int ks = 1; ks < KS; ++ks)
         s[t] = mfma32x32x16(load_half8(k_l + koff[ks] + 32 * t * D), qf[ks], s[t]);
@@ -407,7 +429,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // sum of fp16 pcur.
   auto fused = [&](const float16v(&s)[NT], float16v(&sn)[NT], const half_t* k_l,
                    const half_t* v_l, const half8v(&pprev)[2 * NT], half8v(&pcur)[2 * NT],
-                   int inext) {
+                   int npar) {
     constexpr int NQ = KS * NT;       // score MFMAs
     constexpr int NP = DT * 2 * NT;   // P V MFMAs
     constexpr int NJ = NQ + NP;       // slots
@@ -425,16 +447,15 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       const int cc = sc / 8;
       return s[cc >> 1][8 * (cc & 1) + sc % 8];
     };
-    float16v binit[NT];  // bias band of block inext, read ahead of the K fragments
+    float16v binit[NT];  // bias band of the next block (slot npar), read ahead of the K fragments
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      if constexpr (BIAS) binit[t] = band_acc(inext, t);
+      if constexpr (BIAS) binit[t] = band_acc(npar, t);
     half8v fr[NJ];
 #pragma unroll
     for (int j = 0; j < AHEAD; ++j) fr[j] = frag(j);
-    float acc[2 * NT];
-#pragma unroll
-    for (int cc = 0; cc < 2 * NT; ++cc) acc[cc] = 0.f;
+    // Two sum chains (chunk parity), added at the end.
+    float acc[2] = {0.f, 0.f};
     float ev[NJ][SPJ], pv[NJ][SPJ];
     // Scores sc, sc + 1 into pcur (fp16) and the lane's sum.
     auto pack = [&](int sc, float x0, float x1) {
@@ -442,7 +463,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       const half2v h = {(half_t)x0, (half_t)x1};
       pcur[cc][e] = h[0];
       pcur[cc][e + 1] = h[1];
-      dot2_acc(acc[cc], h);
+      dot2_acc(acc[cc & 1], h);
     };
 #pragma unroll
     for (int e = 0; e < SPJ; ++e) ev[0][e] = __builtin_fmaf(score(e), c, -m_use);
@@ -475,11 +496,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       pack(2 * (NJ - 1), pv[NJ - 1][0], pv[NJ - 1][SPJ - 1]);
     else
       pack(NJ - 2, pv[NJ - 2][0], pv[NJ - 1][0]);
-#pragma unroll
-    for (int w = 1; w < 2 * NT; w *= 2)
-#pragma unroll
-      for (int cc = 0; cc + w < 2 * NT; cc += 2 * w) acc[cc] += acc[cc + w];
-    return acc[0];
+    return acc[0] + acc[1];
   };
 
   // Slow path on the scores s of the block at kb0 (raw Q K^T, modified in
@@ -527,11 +544,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     return expsum(s, pb);
   };
 
-  // Slow path for block i of a step (K in slot si): its scores are
-  // recomputed from LDS, so the fused step need not keep them live.
-  auto slow = [&](int i, int kb0, bool masked, half8v(&pb)[2 * NT]) {
+  // Slow path for the block of a step (its K in ring slot ks, its band in
+  // slot par): its scores are recomputed from LDS, so the fused step need
+  // not keep them live.
+  auto slow = [&](int ks, int par, int kb0, bool masked, half8v(&pb)[2 * NT]) {
     float16v s[NT];
-    qk(s, kslot(i & 3), i);
+    qk(s, kslot(ks), par);
     return slow_scores(s, kb0, masked, pb);
   };
 
@@ -554,8 +572,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // block i had its scores formed in step i-1 (the slow path of block i
   // uses those scores, kept in s), and V of block i into V slot i % 2, whose
   // block i-2 had its P V in step i-1.
-  auto body = [&](int i, float16v(&s)[NT], float16v(&sn)[NT], half8v(&pprev)[2 * NT],
+  // R = i % 4, a compile-time constant: every slot and band address of the
+  // step is then a fixed offset from the lane's base address.
+  auto body = [&](int i, auto Rc, float16v(&s)[NT], float16v(&sn)[NT], half8v(&pprev)[2 * NT],
                   half8v(&pcur)[2 * NT]) {
+    constexpr int R = decltype(Rc)::value;
+    constexpr int P0 = R & 1, P1 = (R + 1) & 1;  // slot parity of blocks i (and i+2), i+1
     BandRegs bload{};  // bias band of block i + 2
     if constexpr (kLive) {
 #ifdef NESO_FA2_SERIAL_LDS
@@ -563,24 +585,24 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       // differs between key groups), so the loads are issued outside the
       // branch.
       if (i + 2 < my_n) {
-        tile_load(i + 2, false);
+        tile_load(i + 2, false, P0);
         bload = band_load(i + 2);
       }
-      if (i < my_n) tile_load(i, true);
+      if (i < my_n) tile_load(i, true, P0);
       serial_lds_point();
       if (i < my_n) {
 #else
       if (i < my_n) {
         if (i + 2 < my_n) {
-          tile_load(i + 2, false);
+          tile_load(i + 2, false, P0);
           bload = band_load(i + 2);
         }
-        tile_load(i, true);
+        tile_load(i, true, P0);
 #endif
         const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
         const bool masked =
             (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
-        float ls = fused(s, sn, kslot((i + 1) & 1), vslot((i + 1) & 1), pprev, pcur, i + 1);
+        float ls = fused(s, sn, kslot(P1), vslot(P1), pprev, pcur, P1);
         if (__any(masked || !(ls <= thr))) ls = slow_scores(s, kb0, masked, pcur);
         l_run += ls;
       }
@@ -589,12 +611,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     // The debug build's barrier must be reached by every wave (my_n differs
     // between key groups), so the loads are issued outside the branch.
     if (i + 2 < my_n) {
-      lds_load(i + 2, (i + 2) & 3);
+      lds_load(i + 2, (R + 2) & 3);
       bload = band_load(i + 2);
     }
     serial_lds_point();
     if constexpr (HALVES) {
-      if (i == my_nw && i < my_n) pv_only(pprev, vslot((i - 1) & 3));
+      if (i == my_nw && i < my_n) pv_only(pprev, vslot((R + 3) & 3));
     }
     if (i < (HALVES ? my_nw : my_n)) {
 #else
@@ -602,13 +624,13 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       // The group's loads go on past this wave's last block; the P V of
       // that block comes in the step after it (later loads reuse its slot).
       if (i < my_n) {
-        if (i + 2 < my_n) lds_load(i + 2, (i + 2) & 3);
-        if (i == my_nw) pv_only(pprev, vslot((i - 1) & 3));
+        if (i + 2 < my_n) lds_load(i + 2, (R + 2) & 3);
+        if (i == my_nw) pv_only(pprev, vslot((R + 3) & 3));
       }
     }
     if (i < (HALVES ? my_nw : my_n)) {
       if (!HALVES && i + 2 < my_n) {
-        lds_load(i + 2, (i + 2) & 3);
+        lds_load(i + 2, (R + 2) & 3);
         bload = band_load(i + 2);
       }
 #endif
@@ -618,9 +640,9 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
           (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
       // After the group's last block the next scores come from a stale
       // slot and are never used.
-      float ls = fused(s, sn, kslot((i + 1) & 3), vslot((i + 3) & 3), pprev, pcur, i + 1);
+      float ls = fused(s, sn, kslot((R + 1) & 3), vslot((R + 3) & 3), pprev, pcur, P1);
       // ls enters the condition so that the softmax cannot sink below it.
-      if (__any(masked || !(ls <= thr))) ls = slow(i, kb0, masked, pcur);
+      if (__any(masked || !(ls <= thr))) ls = slow(R, P0, kb0, masked, pcur);
       l_run += ls;
     }
     }
@@ -629,7 +651,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     // stays in place.
     serial_lds_point();
     wait_vmem();
-    if (BIAS && i + 2 < my_n) band_store(i + 2, bload);
+    if (BIAS && i + 2 < my_n) band_store(P0, bload);
     lds_barrier();
   };
 
@@ -644,8 +666,8 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       // (measured: H16 N1024 d64 10.25 -> 10.05 us; with the bias band the
       // longer prologue cost more, rel-pos 14.21 -> 14.52, so step 0 loads
       // it there).
-      tile_load(0, false);
-      if constexpr (!BIAS) tile_load(0, true);
+      tile_load(0, false, 0);
+      if constexpr (!BIAS) tile_load(0, true, 0);
     } else {
       lds_load(0, 0);
     }
@@ -653,7 +675,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   }
   if (my_n > 1) {
     if constexpr (kLive)
-      tile_load(1, false);
+      tile_load(1, false, 1);
     else
       lds_load(1, 1);
     bpro[1] = band_load(1);
@@ -668,7 +690,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     qk(sa, kslot(0), 0);
     lds_barrier();
     if (my_n > 2) {
-      tile_load(2, false);
+      tile_load(2, false, 0);
       bpro[2] = band_load(2);
     }
     qk(sb, kslot(1), 1);
@@ -683,7 +705,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     lds_load(2, 2);
     bpro[2] = band_load(2);
   }
-  if (kLive && BIAS && my_n > 0) tile_load(0, true);
+  if (kLive && BIAS && my_n > 0) tile_load(0, true, 0);
   serial_lds_point();
   if constexpr (!kLive) qk(sa, kslot(0), 0);
   if (HALVES ? my_nw > 0 : my_n > 0) {
@@ -694,14 +716,20 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     l_run += slow_scores(sa, kb0, masked, pb2);
   }
   wait_vmem();
-  if (BIAS && my_n > 2) band_store(2, bpro[2]);
+  if (BIAS && my_n > 2) band_store(0, bpro[2]);
   lds_barrier();
 
-  // Steps 1, 2, ...: unrolled by two so that the score and P arrays swap
-  // roles without copies.
-  for (int i = 1; i < iters; i += 2) {
-    body(i, sb, sa, pb2, pa);
-    body(i + 1, sa, sb, pa, pb2);
+  // Steps 1, 2, ...: unrolled by four, so that the score and P arrays swap
+  // roles without copies and each copy knows its ring slots (i % 4).
+  using R0 = std::integral_constant<int, 0>;
+  using R1 = std::integral_constant<int, 1>;
+  using R2 = std::integral_constant<int, 2>;
+  using R3 = std::integral_constant<int, 3>;
+  for (int i = 1; i < iters; i += 4) {
+    body(i, R1{}, sb, sa, pb2, pa);
+    body(i + 1, R2{}, sa, sb, pa, pb2);
+    body(i + 2, R3{}, sb, sa, pb2, pa);
+    body(i + 3, R0{}, sa, sb, pa, pb2);
   }
   // P V of the group's last block.  Step j writes block j's P into pb2
   // when j is even, into pa when j is odd.  (A HALVES wave that stopped

@@ -209,7 +209,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
       const int idx = q0 - kb0 - (kKB - 1) + N - 1 + gtid;
       const rsrc_t rb = make_rsrc(static_cast<const float*>(p.bias) + (int64_t)bh * p.bias_stride_h,
                                   (uint32_t)(2 * N - 1) * 4);
-      st.b = buf_load_f32(rb, (uint32_t)idx * 4u);
+      st.b = buf_load_f32(rb, elem_offset(idx, 2 * N - 1, 4));
     }
   };
 

@@ -184,7 +184,13 @@ __global__ __launch_bounds__(256) void relpos_precompute_kernel(RelPreArgs a) {
     // rel_bias[iw + a][r0 + c - (T - 1) + iw + a].
     const bool inside = iw + 31 < T && r0 - (T - 1) + iw >= 0 && r0 + 62 - (T - 1) + iw < T;
     if (inside) {
-      const uint32_t voff = (uint32_t)(lane_base + r0) * 2u;
+      // The empty asm keeps the whole offset in the register: the compiler
+      // would otherwise move the tile's part (32 t) into the immediate
+      // field, leaving a register part that can be a wrapped negative
+      // number, which the range check of raw buffer stores treats as out of
+      // range although the whole offset is in range.
+      uint32_t voff = (uint32_t)(lane_base + r0) * 2u;
+      asm volatile("" : "+v"(voff));
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const uint32_t soff = (uint32_t)((8 * (q >> 2) + (q & 3)) * (T + 1)) * 2u;

@@ -88,6 +88,29 @@ def test_rel_pos_table(gpu, fast, qw, ksplit, h, n, d):
     assert (out - ref).abs().max().item() <= TOL
 
 
+@pytest.mark.parametrize("path", ["fast-2-1", "fast-2-2", "fast-4-1", "fast-4-2", "generic"])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("n", [129, 161, 193, 225, 257, 289, 321, 385])
+def test_rel_pos_table_entry_zero(gpu, monkeypatch, path, d, n):
+    """Row 0 against key N-1 is the only pair that uses table entry 0.  Every
+    key-block count and unrolled-step position of the group's last block:
+    the band load of that entry must not read as zero (regression: its
+    offset was once split into a wrapped negative register part plus an
+    immediate, which the buffer range check rejects)."""
+    if path == "generic":
+        monkeypatch.setenv("NESO_AMD_FA2_FAST", "0")
+    else:
+        _, qw, ks = path.split("-")
+        monkeypatch.setenv("NESO_AMD_FA2_FAST", "2")
+        monkeypatch.setenv("NESO_AMD_FA2_QW", qw)
+        monkeypatch.setenv("NESO_AMD_FA2_KSPLIT", ks)
+    q, k, v, table = I.relpos_inputs(2, n, d, seed=n + d)
+    table[:, 0] = 3.0  # a large entry 0: dropping it moves row 0 by far more than the bar
+    out = table_gpu(q, k, v, table)
+    ref = A.rel_pos_attention_table(q, k, v, table, 1 / math.sqrt(d))
+    assert (out - ref).abs().max().item() <= TOL
+
+
 @pytest.mark.parametrize("qw", [2, 4])
 def test_rel_pos_table_fp16_out(gpu, fast, qw):
     fast(qw)

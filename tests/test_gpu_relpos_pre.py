@@ -89,7 +89,8 @@ def test_reference_configs(gpu, t, d, nh):
 
 
 @pytest.mark.parametrize("t,d,nh", [(1, 64, 1), (2, 32, 3), (33, 64, 2), (100, 128, 1),
-                                    (1500, 64, 2)])
+                                    (1500, 64, 2), (95, 64, 1), (129, 64, 1), (161, 128, 1),
+                                    (200, 64, 1), (321, 64, 1)])
 def test_ragged(gpu, t, d, nh):
     rs = np.random.RandomState(t + d)
     Q = rs.randn(nh, t, d).astype(np.float32)
