@@ -25,7 +25,10 @@ The same line carries:
 * ``qmatmul``: the int4 qmatmul at M=1, K=4096, N=11008 in HBM GB/s
   (algorithmic bytes K*N/2 + (K/32)*N*2 + M*K*2 + M*N*2), over 16 rotated
   weight copies (> 256 MiB, more than the Infinity Cache holds), with its
-  own roofline against 8 TB/s and its CPU baseline;
+  own roofline against 8 TB/s and its CPU baseline, and ``roofline.floor``:
+  at the GEMV's grid, in the same run, an empty kernel and a read-only
+  stream of the same bytes over 16 rotated buffers (what the launch costs
+  when it only moves its bytes);
 * ``sweep``: every other BASELINE config (FA2 config 1 and the N sweep,
   d=128 causal, rel-pos N=1500, qmatmul M=16/256), the GPU rel-pos bias
   precompute at config 4's shape, the fp32-input FA2 at d=64 and d=128 and
@@ -386,6 +389,65 @@ def relpos_precompute_workload(neso_amd, torch, I, want_cpu):
     return launch, 2.0 * h * t * t * d, "flop", cfg, cpu
 
 
+def relpos_dense_workload(neso_amd, torch, I, T, want_cpu, nh=8, d=128):
+    """The reference's own rel-pos bench (tests/test_rel_pos_fa2.py:377-426,
+    configs :466-472): dense fp16 bias [nh][T][T], logits (QK^T + B) * scale,
+    fp16 O, d = 128, nh = 8.  FLOP = 4 nh T^2 d as for BASELINE (the
+    reference's own formula adds nh T^2 for the bias, :424)."""
+    from neso_amd import _lib
+    from oracle import attention as A
+    g = torch.Generator().manual_seed(T)
+    q, k, v = (torch.randn(nh, T, d, generator=g).half() for _ in range(3))
+    bias = (torch.randn(nh, T, T, generator=g) * 2.0).half()
+    qd, kd, vd, bd = (x.cuda() for x in (q, k, v, bias))
+    o = torch.empty(nh, T, d, dtype=torch.float16, device="cuda")
+    scale = d ** -0.5
+    launch = lambda i: neso_amd.rel_pos_fa2_fwd(qd, kd, vd, bd, o, T, d, scale, T * d, T * T,
+                                                num_heads=nh, head_dim=d,
+                                                bias_mode=_lib.NESO_BIAS_DENSE_SCALED_F16)
+    cpu = (lambda: A.rel_pos_attention_dense(q, k, v, bias, scale)) if want_cpu else None
+    cfg = {"H": nh, "T": T, "d": d, "bias": "dense f16 [H][T][T]", "out": "f16"}
+    return launch, 4.0 * nh * T * T * d, "flop", cfg, cpu
+
+
+def fa2_io_workload(neso_amd, torch, N, d, want_cpu, f32=False):
+    """The reference's hand-written FA2 bench (bench/bench_flash_attention.py
+    :142-152, configs :498-508): one head, Q/K/V/O all fp16 (or fp32)."""
+    from oracle import attention as A
+    g = torch.Generator().manual_seed(N + d)
+    dt = torch.float32 if f32 else torch.float16
+    q, k, v = (torch.randn(N, d, generator=g).to(dt) for _ in range(3))
+    qd, kd, vd = (x.cuda() for x in (q, k, v))
+    o = torch.empty(N, d, dtype=dt, device="cuda")
+    scale = d ** -0.5
+    launch = lambda i: neso_amd.flash_attention_io_fwd(qd, kd, vd, o, N, d, scale,
+                                                       check_range=False)
+    cpu = (lambda: A.attention(q, k, v, scale)) if want_cpu else None
+    cfg = {"B": 1, "H": 1, "N": N, "d": d, "io": "f32" if f32 else "f16"}
+    return launch, 4.0 * N * N * d, "flop", cfg, cpu
+
+
+def window_workload(neso_amd, torch, N, H, d, wl, wr, want_cpu):
+    """The reference's sliding-window kernel (debug/fa2_correctness_legacy.py
+    :92-102) at a larger shape: [seq][heads][d] fp16, fp16 O.  FLOP counts
+    the visible (query, key) pairs, 4 d per pair."""
+    from oracle import attention as A
+    g = torch.Generator().manual_seed(N + wl)
+    q, k, v = (torch.randn(N, H, d, generator=g).half() for _ in range(3))
+    qd, kd, vd = (x.cuda() for x in (q, k, v))
+    o = torch.empty(N, H, d, dtype=torch.float16, device="cuda")
+    launch = lambda i: neso_amd.window_attention(qd, kd, vd, wl, wr, out=o)
+    cpu = None
+    if want_cpu:
+        qh, kh, vh = (x.permute(1, 0, 2) for x in (q, k, v))
+        cpu = lambda: A.attention(qh, kh, vh, d ** -0.5, window=(wl, wr))
+    i = torch.arange(N)
+    pairs = int(((torch.minimum(i + wr, torch.tensor(N - 1)) - torch.clamp(i - wl, min=0)) + 1)
+                .clamp(min=0).sum())
+    cfg = {"N": N, "H": H, "d": d, "window_left": wl, "window_right": wr, "visible_pairs": pairs}
+    return launch, 4.0 * H * pairs * d, "flop", cfg, cpu
+
+
 def w4a16_workload(neso_amd, torch, I, M, want_cpu, rotate=ROTATE):
     from oracle import qmatmul as Q
     import numpy as np
@@ -410,8 +472,50 @@ def w4a16_workload(neso_amd, torch, I, M, want_cpu, rotate=ROTATE):
     return launch, Q.algorithmic_bytes(M, N, K), "bytes", cfg, cpu
 
 
-def w8a16_workload(neso_amd, torch, scaled, want_cpu):
-    m = n = k = 4096
+def w4a16_floor(neso_amd, torch, steps, warmup, rotate=ROTATE):
+    """The streaming floor of the M=1 GEMV, timed like it: at the GEMV's own
+    grid (from its launch plan), an empty kernel (dispatch and the kernel
+    boundary alone) and a read-only stream of the same algorithmic bytes
+    (16-byte non-temporal loads, four in flight per lane) over ``rotate``
+    distinct buffers (more than the Infinity Cache holds), one per launch
+    in turn.  Both through ``neso_stream_probe``."""
+    from neso_amd import _lib
+    K, N = 4096, 11008
+    nbytes = K * N // 2 + (K // 32) * N * 2 + K * 2 + N * 2  # the GEMV's algorithmic bytes, M = 1
+    nbytes -= nbytes % 16
+    x = torch.zeros(1, K, dtype=torch.float16, device="cuda")
+    w = torch.zeros(N, K // 8, dtype=torch.int32, device="cuda")
+    sc = torch.zeros(N, K // 32, dtype=torch.float16, device="cuda")
+    y = torch.empty(1, N, dtype=torch.float16, device="cuda")
+    plan = neso_amd.launch_plan("w4a16_matmul", x, w, sc, y, 1, N, K, K, N)
+    grid = int(plan[0]["grid"][0])
+    del w, sc
+    bufs = [torch.randint(0, 1 << 30, (nbytes // 4,), dtype=torch.int32, device="cuda")
+            for _ in range(rotate)]
+    sink = torch.zeros(4, dtype=torch.int32, device="cuda")
+    lib = _lib.load()
+
+    def probe(mode):
+        def launch(i):
+            st = torch.cuda.current_stream().cuda_stream
+            _lib.check(lib.neso_stream_probe(bufs[i % rotate].data_ptr(), nbytes, grid, mode,
+                                             0xFFFFFFFF, sink.data_ptr(), st))
+        return launch
+    ms_read, t_read = time_case(probe(1), steps, warmup, torch)
+    ms_empty, t_empty = time_case(probe(0), steps, warmup, torch)
+    del bufs
+    return {"kernel": f"stream_read_kernel / stream_empty_kernel, grid {grid} x 256 "
+                      f"(the GEMV's: {plan[0]['device_kernel']})",
+            "bytes": nbytes, "rotated_buffers": rotate, "grid": grid,
+            "stream_us": round(ms_read * 1e3, 3),
+            "stream_gbs": round(nbytes / (ms_read * 1e-3) / 1e9, 1),
+            "stream_median_us": round(t_read["median_ms"] * 1e3, 3),
+            "empty_us": round(ms_empty * 1e3, 3),
+            "empty_median_us": round(t_empty["median_ms"] * 1e3, 3)}
+
+
+def w8a16_workload(neso_amd, torch, scaled, want_cpu, size=4096):
+    m = n = k = size
     g = torch.Generator().manual_seed(0)
     a = torch.randn(m, k, generator=g).half()
     b = torch.randint(-128, 128, (k, n), generator=g, dtype=torch.int8)
@@ -429,11 +533,28 @@ def w8a16_workload(neso_amd, torch, scaled, want_cpu):
     return launch, 2.0 * m * n * k, "flop", {"M": m, "N": n, "K": k}, cpu
 
 
+def launched_kernels(launch):
+    """The device kernels (with template arguments) and grids that one call of
+    ``launch`` issues, from the library's launch plan (recorded, not run)."""
+    import json as _json
+    from neso_amd import _lib
+    lib = _lib.load()
+    _lib.check(lib.neso_plan_begin(0))
+    try:
+        launch(0)
+    finally:
+        plan = _json.loads(lib.neso_plan_end().decode())["launches"]
+    return [f"{p['device_kernel']}<{','.join(str(x) for x in p['template_args'])}> grid "
+            f"{p['grid']} x {p['threadgroup_size']}" for p in plan]
+
+
 def run_case(workload, steps, warmup, torch, want_cpu, power=False):
     """Time one workload; returns a result row."""
     launch, work, kind, cfg, cpu = workload
+    kernels = launched_kernels(launch)
     ms, timing = time_case(launch, steps, warmup, torch, power)
     row = dict(cfg)
+    row["device_kernels"] = kernels
     row["us"] = round(ms * 1e3, 3)
     row["timing"] = timing
     if kind == "flop":
@@ -481,13 +602,39 @@ def cases(neso_amd, torch, I, want_cpu):
                                                 cfg["d"], cfg["causal"], want_cpu))
     for m in (1, 16, 256):
         c[f"w4a16_m{m}"] = lambda m=m: w4a16_workload(neso_amd, torch, I, m, want_cpu)
+    # The reference's own benchmark configs (kernels it times itself).
+    for t in REF_RELPOS_T:
+        c[f"ref_relpos_dense_T{t}"] = lambda t=t: relpos_dense_workload(neso_amd, torch, I, t,
+                                                                      want_cpu)
+    for n, d in REF_FA2_IO:
+        c[f"ref_fa2_io_f16_N{n}_d{d}"] = lambda n=n, d=d: fa2_io_workload(neso_amd, torch, n, d,
+                                                                         want_cpu)
+    for n, d in ((4096, 64), (4096, 128)):
+        c[f"ref_fa2_io_f32_N{n}_d{d}"] = lambda n=n, d=d: fa2_io_workload(neso_amd, torch, n, d,
+                                                                         want_cpu, f32=True)
+    c["fa2_d32"] = lambda: fa2_workload(neso_amd, torch, I, 1, 16, 2048, 32, False, want_cpu)
+    c["fa2_window"] = lambda: window_workload(neso_amd, torch, 4096, 16, 64, 256, 0, want_cpu)
+    for size in (1024, 2048):
+        c[f"w8a16_{size}"] = lambda size=size: w8a16_workload(neso_amd, torch, False, want_cpu,
+                                                             size)
+        c[f"w8a16_scaled_{size}"] = lambda size=size: w8a16_workload(neso_amd, torch, True,
+                                                                    want_cpu, size)
     return c
+
+
+REF_RELPOS_T = (128, 256, 384, 448, 512)  # tests/test_rel_pos_fa2.py:466-472
+REF_FA2_IO = ((256, 64), (512, 64), (1024, 64), (2048, 64), (4096, 64), (512, 128), (1024, 128),
+              (2048, 128), (4096, 128))  # bench/bench_flash_attention.py:498-508
 
 
 SWEEP_ORDER = ["fa2_config1"] + [f"fa2_n{n}{s}" for n in (128, 256, 512, 1024, 2048)
                                  for s in ("", "_causal")] + [
     "fa2_d128", "relpos", "relpos_precompute", "fa2_f32_qkv", "fa2_f32_qkv_d128", "w8a16",
-    "w8a16_scaled", "w4a16_m16", "w4a16_m256"]
+    "w8a16_scaled", "w4a16_m16", "w4a16_m256", "fa2_d32", "fa2_window"] + [
+    f"ref_relpos_dense_T{t}" for t in REF_RELPOS_T] + [
+    f"ref_fa2_io_f16_N{n}_d{d}" for n, d in REF_FA2_IO] + [
+    "ref_fa2_io_f32_N4096_d64", "ref_fa2_io_f32_N4096_d128", "w8a16_1024", "w8a16_scaled_1024",
+    "w8a16_2048", "w8a16_scaled_2048"]
 KERNEL_OF = {  # device kernel each sweep row's time is dominated by (for readers)
     "fa2_f32_qkv": "fa2_fwd_kernel (F32IN: 3 fp16 MFMAs per product)",
     "fa2_f32_qkv_d128": "fa2_fwd_kernel (F32IN, 32-key blocks)",
@@ -495,6 +642,14 @@ KERNEL_OF = {  # device kernel each sweep row's time is dominated by (for reader
     "relpos_precompute": "relpos_precompute_kernel (fp16 hi/lo MFMA; HBM-bound, hbm_frac)",
     "w8a16": "w8a16_gemm_kernel", "w8a16_scaled": "w8a16_gemm_kernel",
     "w4a16_m16": "w4a16_skinny_lds_kernel", "w4a16_m256": "w4a16_tile_gemm_kernel",
+    "fa2_window": "neso_flash_attention_window_fwd (fast kernel, sliding window)",
+    "w8a16_1024": "w8a16_gemm_kernel", "w8a16_scaled_1024": "w8a16_gemm_kernel",
+    "w8a16_2048": "w8a16_gemm_kernel", "w8a16_scaled_2048": "w8a16_gemm_kernel",
+    **{f"ref_relpos_dense_T{t}": "neso_rel_pos_fa2_fwd, NESO_BIAS_DENSE_SCALED_F16, fp16 O"
+       for t in REF_RELPOS_T},
+    **{f"ref_fa2_io_f16_N{n}_d{d}": "neso_flash_attention_io_fwd (fp16 io)" for n, d in REF_FA2_IO},
+    "ref_fa2_io_f32_N4096_d64": "neso_flash_attention_io_fwd (fp32 io: F32IN kernel)",
+    "ref_fa2_io_f32_N4096_d128": "neso_flash_attention_io_fwd (fp32 io: F32IN kernel)",
 }
 
 
@@ -595,7 +750,11 @@ def main():
                       "weights dequantised beforehand",
             "seconds_per_step": qm["cpu_seconds"],
             "matmul_only_gbs": qm.get("cpu_matmul_only_gbs")}
-    log(f"qmm M=1 {gbs:.1f} GB/s")
+    floor = w4a16_floor(neso_amd, torch, args.steps, args.warmup)
+    floor["gemv_minus_stream_us"] = round(qm["us"] - floor["stream_us"], 3)
+    result["qmatmul"]["roofline"]["floor"] = floor
+    log(f"qmm M=1 {gbs:.1f} GB/s; floor: stream {floor['stream_us']:.2f} us "
+        f"({floor['stream_gbs']:.0f} GB/s), empty {floor['empty_us']:.2f} us")
 
     if not args.no_sweep:
         rows = []

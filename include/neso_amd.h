@@ -84,6 +84,22 @@ const char* neso_plan_end(void);
 int neso_clock_sample(uint64_t* out, int32_t samples, int32_t gap_ticks, void* stream);
 
 /*
+ * Streaming-floor probe, a measurement aid with no counterpart in the
+ * reference: what a launch of an HBM-bound kernel costs when it only moves
+ * its bytes.  mode 0 launches `grid` workgroups of 256 threads that do
+ * nothing (dispatch and the kernel boundary alone); mode 1 reads `bytes`
+ * bytes from `src` with 16-byte non-temporal loads, a rolling window of four
+ * in flight per lane, thread t of the grid's T threads reading pieces t,
+ * t + T, ..., and writes sink[0] only if the XOR of everything read equals
+ * `key` (which keeps the loads live).  1 <= grid <= 2^20; mode 1: src
+ * 16-byte aligned, bytes a positive multiple of 16 needing at most 16
+ * pieces per thread (bytes <= 16 * 16 * 256 * grid) and below 4 GiB, sink
+ * 4-byte aligned.
+ */
+int neso_stream_probe(const void* src, int64_t bytes, int32_t grid, int32_t mode, uint32_t key,
+                      uint32_t* sink, void* stream);
+
+/*
  * Flash-Attention-2 forward.  Replaces the `flash_attention_fwd` kernel of
  * tests/test_flash_attention.py:149-153 (launched at :287-290 and by
  * macos/harness.rs:149-169 with buffers 0-3 = Q, K, V, O and scalars 4-7 =
@@ -192,8 +208,13 @@ int neso_rel_pos_fa2_fwd(const void* Q, const void* K, const void* V, const void
  * Outputs fp16, contiguous, ready for neso_rel_pos_fa2_fwd with
  * NESO_BIAS_DENSE_SCALED_F16:
  *   Q_u [nh][T][d]      = Q + bias_u
- *   rel_bias [nh][T][T] = (Q + bias_v)_i . K_rel[T-1-i+j]   (fp32 products
- *                         and accumulation, rounded to fp16 once)
+ *   rel_bias [nh][T][T] = (Q + bias_v)_i . K_rel[T-1-i+j]   rounded to fp16
+ *                         once
+ * The dot products run on fp16 MFMAs: each fp32 factor x is split into
+ * fp16 hi = fp16(x) and lo = fp16(x - hi), and hi*hi + hi*lo + lo*hi is
+ * summed in fp32 (lo*lo dropped).  This needs |Q + bias_v| and |K_rel| below
+ * 65504, the fp16 limit (larger elements give inf/NaN bias rows); the
+ * result is fp32-class for elements above about 2^-10 in magnitude.
  * d 32, 64 or 128; Q, K_rel, bias_v and Q_u 16-byte aligned.
  */
 int neso_rel_pos_precompute(const float* Q, const float* K_rel, const float* bias_u,

@@ -42,6 +42,7 @@ SIGNATURES = {
     "neso_plan_begin": (ctypes.c_int, [_i32]),
     "neso_plan_end": (ctypes.c_char_p, []),
     "neso_clock_sample": (ctypes.c_int, [_p, _i32, _i32, _p]),
+    "neso_stream_probe": (ctypes.c_int, [_p, _i64, _i32, _i32, ctypes.c_uint32, _p, _p]),
     "neso_flash_attention_fwd": (
         ctypes.c_int,
         [_p, _p, _p, _p, _i32, _i32, _i32, _f32, _i32, _i32, _i64, _i64, _i32, _p],

@@ -162,7 +162,8 @@ def _compile(src: Path, obj: Path, extra: list[str]) -> None:
 
 
 def _device_asm(src: Path, extra: list[str]) -> str:
-    out = BUILD_DIR / (src.stem + ".gfx950.s")
+    tag = "_serial" if "-DNESO_FA2_SERIAL_LDS" in extra else ""
+    out = BUILD_DIR / (src.stem + tag + ".gfx950.s")
     cmd = [hipcc(), *COMMON_FLAGS, *extra, "--offload-device-only", "-S", str(src), "-o", str(out)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
@@ -204,15 +205,20 @@ def build(extra_flags: list[str] | None = None, jobs: int | None = None) -> Path
     objs = [BUILD_DIR / (Path(s).stem + ".o") for s in SOURCES]
     serial_obj = BUILD_DIR / "fa2_fast_serial.o"
     jobs = jobs or min(len(SOURCES) + 2, os.cpu_count() or 1)
+    fast_flags = extra + SOURCE_FLAGS.get("fa2_fast.hip", [])
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        asm = ex.submit(_device_asm, CSRC / "fa2_fast.hip", extra)
+        # Both builds of the fast kernel are checked: the serialised one
+        # carries the same LDS-DMA asm.
+        asm = ex.submit(_device_asm, CSRC / "fa2_fast.hip", fast_flags)
+        asm_serial = ex.submit(_device_asm, CSRC / "fa2_fast.hip",
+                               fast_flags + ["-DNESO_FA2_SERIAL_LDS"])
         futs = [ex.submit(_compile, CSRC / s, o, extra + SOURCE_FLAGS.get(s, []))
                 for s, o in zip(SOURCES, objs)]
         futs.append(ex.submit(_compile, CSRC / "fa2_fast.hip", serial_obj,
                               extra + ["-DNESO_FA2_SERIAL_LDS"]))
         for f in futs:
             f.result()
-        problems = m0_check(asm.result())
+        problems = m0_check(asm.result()) + m0_check(asm_serial.result())
     if problems:
         sys.stderr.write("neso_amd build: the fast FA2 kernel's LDS-DMA M0 assumption does not "
                          "hold for this compiler; building without the fast kernel:\n  "

@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <atomic>
 #include <string>
+#include <utility>
 
 #include "../../include/neso_amd.h"
 #include "manifest.h"
@@ -220,6 +221,57 @@ __global__ __launch_bounds__(64) void clock_sample_kernel(uint64_t* out, int sam
   }
 }
 
+// Streaming-floor probes (measurement aids): an empty kernel, and a
+// read-only stream of 16-byte non-temporal loads in which thread t of the
+// grid (T threads) reads pieces t, t + T, ..., t + (NP - 1) T, the layout of
+// a persistent grid streaming one contiguous buffer.  Straight-line code
+// with a rolling window of DEPTH loads in flight per lane: piece k is folded
+// into an XOR as piece k + DEPTH is requested.  The XOR is written only if
+// it equals `key`, which keeps every load live.
+__global__ __launch_bounds__(256) void stream_empty_kernel() {}
+
+template <int NP, int DEPTH>
+__global__ __launch_bounds__(256) void stream_read_kernel(const void* src, uint32_t bytes,
+                                                          uint32_t key, uint32_t* sink) {
+  const rsrc_t r = make_rsrc(src, bytes);
+  const uint32_t T = gridDim.x * 256u;
+  const uint32_t t = blockIdx.x * 256u + threadIdx.x;
+  uint4v v[NP];
+  uint32_t acc = 0;
+#pragma unroll
+  for (int k = 0; k < NP + DEPTH; ++k) {
+    // Pieces past the buffer read as zeros (offsets stay below 2^32: the
+    // entry point bounds NP T * 16).
+    if (k < NP)
+      v[k] = __builtin_bit_cast(uint4v, __builtin_amdgcn_raw_buffer_load_b128(
+                                            r, (t + (uint32_t)k * T) * 16u, 0, kNonTemporal));
+    if (k >= DEPTH) {
+      const uint4v& x = v[k - DEPTH];
+      acc ^= x[0] ^ x[1] ^ x[2] ^ x[3];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (acc == key) sink[0] = acc;
+}
+
+template <int NP>
+hipError_t launch_stream_read(int grid, hipStream_t st, const void* src, uint32_t bytes,
+                              uint32_t key, uint32_t* sink) {
+  return launch<&stream_read_kernel<NP, 4>>(ktag("stream_read_kernel", NP, 4), dim3(grid),
+                                             dim3(256), st, src, bytes, key, sink);
+}
+
+template <int... NPS>
+hipError_t launch_stream_read_np(int np, int grid, hipStream_t st, const void* src,
+                                 uint32_t bytes, uint32_t key, uint32_t* sink,
+                                 std::integer_sequence<int, NPS...>) {
+  hipError_t err = hipErrorInvalidValue;
+  ((np == NPS + 1 ? (err = launch_stream_read<NPS + 1>(grid, st, src, bytes, key, sink), 0) : 0),
+   ...);
+  return err;
+}
+constexpr int kStreamMaxPieces = 16;  // pieces per thread
+
 }  // namespace neso
 
 extern "C" {
@@ -263,6 +315,33 @@ int neso_clock_sample(uint64_t* out, int32_t samples, int32_t gap_ticks, void* s
                       neso::ktag("clock_sample_kernel"), dim3(1), dim3(64),
                       static_cast<hipStream_t>(stream), out, (int)samples, (int)gap_ticks),
                   "clock_sample");
+}
+
+int neso_stream_probe(const void* src, int64_t bytes, int32_t grid, int32_t mode, uint32_t key,
+                      uint32_t* sink, void* stream) {
+  if (grid < 1 || grid > (1 << 20))
+    return fail(NESO_EINVAL, "stream_probe: grid=%d outside [1, 2^20]", grid);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (mode == 0)
+    return launched(neso::launch<&neso::stream_empty_kernel>(neso::ktag("stream_empty_kernel"),
+                                                             dim3(grid), dim3(256), st),
+                    "stream_probe");
+  if (mode != 1) return fail(NESO_EINVAL, "stream_probe: mode=%d not 0 or 1", mode);
+  if (!src || !aligned16(src) || !sink || (reinterpret_cast<uintptr_t>(sink) & 3u))
+    return fail(NESO_EINVAL, "stream_probe: null or misaligned src/sink");
+  const int64_t threads = (int64_t)grid * 256;
+  if (bytes <= 0 || bytes % 16)
+    return fail(NESO_EINVAL, "stream_probe: bytes=%lld must be a positive multiple of 16",
+                (long long)bytes);
+  const int64_t np = (bytes / 16 + threads - 1) / threads;  // pieces per thread
+  // Every piece offset (np T pieces of 16 bytes) must stay below 2^32.
+  if (np > neso::kStreamMaxPieces || np * threads * 16 >= ((int64_t)1 << 32))
+    return fail(NESO_EINVAL, "stream_probe: bytes=%lld needs %lld pieces per thread at grid "
+                "%d (at most %d, and below 4 GiB)", (long long)bytes, (long long)np, grid,
+                neso::kStreamMaxPieces);
+  return launched(neso::launch_stream_read_np((int)np, grid, st, src, (uint32_t)bytes, key, sink,
+                                              std::make_integer_sequence<int, neso::kStreamMaxPieces>()),
+                  "stream_probe");
 }
 
 const char* neso_plan_end(void) {
@@ -366,6 +445,10 @@ int neso_rel_pos_precompute(const float* Q, const float* K_rel, const float* bia
   return launched(neso::launch_relpos_precompute(a, d, static_cast<hipStream_t>(stream)), name);
 }
 
+// True when a buffer of `bytes` bytes can be addressed with 32-bit offsets
+// (the kernels' buffer resources and per-lane offsets are 32-bit).
+static bool extent32(int64_t bytes) { return bytes < ((int64_t)1 << 32); }
+
 int neso_w4a16_matmul(const void* X, const int32_t* W, const void* scales, void* Y, int32_t M,
                       int32_t N, int32_t K, int32_t stride_xm, int32_t stride_ym,
                       int32_t group_size, int32_t zero_point, void* stream) {
@@ -386,6 +469,11 @@ int neso_w4a16_matmul(const void* X, const int32_t* W, const void* scales, void*
     return fail(NESO_EINVAL, "%s: X/W must be 16-byte aligned, scales/Y 2-byte", name);
   if (M == 0 || N == 0) return ok();
   if (K == 0) return fail(NESO_EINVAL, "%s: K=0 with non-empty output", name);
+  // The kernels address X and Y with 32-bit buffer offsets.
+  if (!extent32(((int64_t)(M - 1) * stride_xm + K) * 2) ||
+      !extent32(((int64_t)(M - 1) * stride_ym + N) * 2))
+    return fail(NESO_EINVAL, "%s: X or Y spans 4 GiB or more (M=%d, stride_xm=%d, stride_ym=%d)",
+                name, M, stride_xm, stride_ym);
   neso::W4Args a{};
   a.X = static_cast<const neso::half_t*>(X);
   a.W = reinterpret_cast<const uint32_t*>(W);
@@ -412,6 +500,11 @@ static int w8a16_common(const void* A, const int8_t* B, float* C, const void* sc
     return fail(NESO_EINVAL, "%s: misaligned A/C/scale", name);
   if (M == 0 || N == 0) return ok();
   if (K == 0) return fail(NESO_EINVAL, "%s: K=0 with non-empty output", name);
+  // The kernels address A (fp16) and B (int8) with 32-bit buffer offsets.
+  if (!extent32(((int64_t)(M - 1) * stride_am + K) * 2) ||
+      !extent32((int64_t)(K - 1) * stride_bk + N))
+    return fail(NESO_EINVAL, "%s: A or B spans 4 GiB or more (M=%d, K=%d, stride_am=%d, "
+                "stride_bk=%d)", name, M, K, stride_am, stride_bk);
   neso::W8Args a{};
   a.A = static_cast<const neso::half_t*>(A);
   a.B = B;

@@ -271,7 +271,7 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_kernel(W4Args a) {
   const rsrc_t rw = make_rsrc(a.W + (int64_t)n0 * KW, (uint32_t)nrows * (uint32_t)KW * 4u);
   const rsrc_t rs = make_rsrc(a.S + (int64_t)n0 * SG, (uint32_t)nrows * (uint32_t)SG * 2u);
   const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx,
-                              (uint32_t)((mrows - 1) * a.ldx + a.K) * 2u);
+                              (uint32_t)(((int64_t)(mrows - 1) * a.ldx + a.K) * 2));
   const ZeroPoint zp = zero_point(a.zero);
   const Nibbles nib = nibble_consts();
   const uint32_t gm = (uint32_t)a.group >> 5;  // chunks per scale group
@@ -444,7 +444,7 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
   // built from them as divergent and wrap every load in a waterfall loop.
   const int nw0 = __builtin_amdgcn_readfirstlane(n0 + 32 * NT * wn);
   const int nwrows = __builtin_amdgcn_readfirstlane(max(0, min(32 * NT, a.N - nw0)));
-  const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)((mrows - 1) * a.ldx + a.K) * 2u);
+  const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)(((int64_t)(mrows - 1) * a.ldx + a.K) * 2));
   const rsrc_t rw = make_rsrc(a.W + (int64_t)(nwrows ? nw0 : 0) * KW, (uint32_t)nwrows * KW * 4u);
   const rsrc_t rs = make_rsrc(a.S + (int64_t)(nwrows ? nw0 : 0) * SG, (uint32_t)nwrows * SG * 2u);
   const ZeroPoint zp = zero_point(a.zero);
@@ -595,7 +595,7 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   const int KW = a.K >> 3, SG = a.K / a.group;
   const int mrows = __builtin_amdgcn_readfirstlane(min(kTT, a.M - m0));
   const int nrows = __builtin_amdgcn_readfirstlane(min(kTT, a.N - n0));
-  const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)((mrows - 1) * a.ldx + a.K) * 2u);
+  const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)(((int64_t)(mrows - 1) * a.ldx + a.K) * 2));
   const rsrc_t rw = make_rsrc(a.W + (int64_t)n0 * KW, (uint32_t)nrows * KW * 4u);
   const rsrc_t rs = make_rsrc(a.S + (int64_t)n0 * SG, (uint32_t)nrows * SG * 2u);
   const ZeroPoint zp = zero_point(a.zero);
@@ -734,7 +734,7 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   // column 64 wn + 32 nj + li of the tile at (m0, n0).  Rows past M fall
   // outside the buffer resource (ldy >= N >= n0 + nrows); columns past N
   // get an out-of-range offset.
-  const rsrc_t ry = make_rsrc(a.Y + (int64_t)m0 * a.ldy + n0, (uint32_t)((mrows - 1) * a.ldy + nrows) * 2u);
+  const rsrc_t ry = make_rsrc(a.Y + (int64_t)m0 * a.ldy + n0, (uint32_t)(((int64_t)(mrows - 1) * a.ldy + nrows) * 2));
 #pragma unroll
   for (int nj = 0; nj < 2; ++nj) {
     const int nl = 64 * wn + 32 * nj + li;
@@ -882,7 +882,7 @@ __global__ __launch_bounds__(2 * T) void w8a16_gemm_kernel(W8Args a) {
   const int m0 = (first + in % gm) * T, n0 = (in / gm) * T;
   const int mrows = min(T, a.M - m0);
   constexpr uint32_t kOut = 0x80000000u;
-  const rsrc_t ra = make_rsrc(a.A + (int64_t)m0 * a.lda, (uint32_t)((mrows - 1) * a.lda + a.K) * 2u);
+  const rsrc_t ra = make_rsrc(a.A + (int64_t)m0 * a.lda, (uint32_t)(((int64_t)(mrows - 1) * a.lda + a.K) * 2));
   // K >= 1 (the ABI rejects K = 0 with a non-empty output); the extent is
   // clamped at 0 anyway so a bad call cannot wrap it to ~4 GiB.
   const rsrc_t rb = make_rsrc(

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(WV * kWave) void w4a16_skinny_lds_kernel(W4Args a) 
   // same-row stores of an instruction and the 16-lane fragment reads both
   // spread over all banks.
   constexpr int kXPer = (kLdsQuads * 4 * kWave) / (WV * kWave);
-  const rsrc_t rx = make_rsrc(a.X, (uint32_t)((a.M - 1) * a.ldx + a.K) * 2u);
+  const rsrc_t rx = make_rsrc(a.X, (uint32_t)(((int64_t)(a.M - 1) * a.ldx + a.K) * 2));
   half8v xv[kXPer];
   uint32_t xslot[kXPer];
 #pragma unroll

@@ -16,6 +16,8 @@ without a GPU, these functions raise.
 """
 from __future__ import annotations
 
+import contextlib
+
 import math
 from typing import Any
 
@@ -91,23 +93,40 @@ def _stream(stream: Any, *tensors: Any) -> int:
     return 0
 
 
-def _check_f16_range(t: Any, name: str, bh: int, n: int, d: int, s_row: int, s_bh: int) -> None:
+def _on_stream(stream: int, device):
+    """Context that makes ``stream`` (a raw HIP stream handle) torch's current
+    stream, so that torch work in it is ordered with the launch."""
+    if torch.cuda.current_stream(device).cuda_stream == stream:
+        return contextlib.nullcontext()
+    return torch.cuda.stream(torch.cuda.ExternalStream(stream, device=device))
+
+
+def _check_f16_range(inputs, stream: int) -> None:
     """Raise NesoArgumentError if an fp32 input the kernel reads reaches the
     fp16 limit: the fp32-input kernels split each element into fp16 hi + lo,
     so |x| >= 65504 would turn into inf or NaN in the output.  NaN inputs
-    pass (they give NaN rows, as an fp32 computation does).  The check reads
-    the device data and synchronises, so it is skipped for raw addresses,
-    for host tensors (rejected at launch) and while the current stream is
+    pass (they give NaN rows, as an fp32 computation does).
+
+    ``inputs`` holds (tensor, name, view shape, view strides) for the
+    elements the kernel reads.  One reduction per input and one
+    synchronisation for all of them, on ``stream`` (the launch stream), so
+    data written there before the call is what is checked.  Skipped for raw
+    addresses, for host tensors (rejected at launch) and while the stream is
     being captured into a graph."""
-    if (not isinstance(t, torch.Tensor) or t.device.type != "cuda"
-            or torch.cuda.is_current_stream_capturing()):
+    views = [(t.as_strided(shape, strides), name) for t, name, shape, strides in inputs
+             if isinstance(t, torch.Tensor) and t.device.type == "cuda"]
+    if not views or torch.cuda.is_current_stream_capturing():
         return
-    view = t.as_strided((bh, n, d), (s_bh, s_row, 1))
-    m = view.abs().amax().item()
-    if m >= 65504.0:
-        raise _lib.NesoArgumentError(
-            _lib.NESO_EINVAL, f"{name}: |x| reaches {m:g}; fp32 Q/K/V must lie within the fp16 "
-                              f"range (|x| < 65504)")
+    dev = views[0][0].device
+    with _on_stream(stream, dev):
+        if torch.cuda.is_current_stream_capturing():
+            return
+        maxima = torch.stack([v.abs().amax() for v, _ in views]).cpu()
+    for (_, name), m in zip(views, maxima.tolist()):
+        if m >= 65504.0:
+            raise _lib.NesoArgumentError(
+                _lib.NESO_EINVAL, f"{name}: |x| reaches {m:g}; fp32 inputs must lie within the "
+                                  f"fp16 range (|x| < 65504)")
 
 
 def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scale: float, *,
@@ -143,10 +162,13 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
                           (O, "O", span_q)):
             _extent(t, nm, sp)
         if qkv_dtype == "f32" and check_range:
-            for t, nm, sr, sb in ((Q, "Q", stride_qo, stride_bh_qo), (K, "K", stride_kv, stride_bh_kv),
-                                  (V, "V", stride_kv, stride_bh_kv)):
-                if isinstance(t, torch.Tensor) and t.dtype == torch.float32:
-                    _check_f16_range(t, nm, batch_heads, N, head_dim, sr, sb)
+            _check_f16_range(
+                [(t, nm, (batch_heads, N, head_dim), (sb, sr, 1))
+                 for t, nm, sr, sb in ((Q, "Q", stride_qo, stride_bh_qo),
+                                       (K, "K", stride_kv, stride_bh_kv),
+                                       (V, "V", stride_kv, stride_bh_kv))
+                 if isinstance(t, torch.Tensor) and t.dtype == torch.float32],
+                _stream(stream, Q, O))
     lib = _lib.load()
     dt = torch.float32 if qkv_dtype == "f32" else torch.float16
     fn = lib.neso_flash_attention_f32_fwd if qkv_dtype == "f32" else lib.neso_flash_attention_fwd
@@ -160,7 +182,7 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
 
 def flash_attention_io_fwd(Q, K, V, O, N: int, d_head: int, scale: float, *,
                            batch_heads: int = 1, io_dtype: str | None = None,
-                           stream=None) -> None:
+                           check_range: bool = True, stream=None) -> None:
     """FA2 forward with O in the input type, O = softmax(Q K^T * scale) V.
 
     Positional arguments as the hand-written reference kernel
@@ -168,6 +190,10 @@ def flash_attention_io_fwd(Q, K, V, O, N: int, d_head: int, scale: float, *,
     one type (``io_type`` half or float there), N, d_head, scale.  Keyword
     extensions: ``batch_heads`` contiguous [batch_heads, N, d_head] slices in
     one launch; ``io_dtype`` 'f16' or 'f32' (inferred from Q for tensors).
+    fp32 tensors must hold |x| < 65504 (the kernel splits them into fp16
+    hi + lo); ``check_range`` verifies that before the launch (one device
+    reduction per input and one synchronisation, skipped under graph
+    capture).
     """
     if io_dtype is None:
         if not isinstance(Q, torch.Tensor):
@@ -178,6 +204,11 @@ def flash_attention_io_fwd(Q, K, V, O, N: int, d_head: int, scale: float, *,
     if N > 0 and batch_heads > 0:
         for t, nm in ((Q, "Q"), (K, "K"), (V, "V"), (O, "O")):
             _extent(t, nm, batch_heads * N * d_head)
+        if io_dtype == "f32" and check_range:
+            _check_f16_range(
+                [(t, nm, (batch_heads * N * d_head,), (1,)) for t, nm in ((Q, "Q"), (K, "K"), (V, "V"))
+                 if isinstance(t, torch.Tensor) and t.dtype == torch.float32],
+                _stream(stream, Q, O))
     dt = torch.float32 if io_dtype == "f32" else torch.float16
     lib = _lib.load()
     st = lib.neso_flash_attention_io_fwd(
@@ -283,10 +314,13 @@ def rel_pos_precompute(Q, K_rel, bias_u, bias_v, T: int, d: int, nh: int, scale:
         if check_range and all(isinstance(x, torch.Tensor) and x.device.type == "cuda"
                                and x.dtype == torch.float32 for x in (Q, K_rel, bias_v)) \
                 and not torch.cuda.is_current_stream_capturing():
-            qv = (Q.reshape(-1)[:nh * T * d].view(nh, T, d)
-                  + bias_v.reshape(-1)[:nh * d].view(nh, 1, d))
-            for x, nm in ((qv, "Q + bias_v"), (K_rel.reshape(-1)[:nh * (2 * T - 1) * d], "K_rel")):
-                m = x.abs().amax().item()
+            st = _stream(stream, Q, Q_u)
+            with _on_stream(st, Q.device):
+                qv = (Q.reshape(-1)[:nh * T * d].view(nh, T, d)
+                      + bias_v.reshape(-1)[:nh * d].view(nh, 1, d))
+                kr = K_rel.reshape(-1)[:nh * (2 * T - 1) * d]
+                maxima = torch.stack([qv.abs().amax(), kr.abs().amax()]).cpu().tolist()
+            for m, nm in zip(maxima, ("Q + bias_v", "K_rel")):
                 if m >= 65504.0:
                     raise _lib.NesoArgumentError(
                         _lib.NESO_EINVAL, f"{nm}: |x| reaches {m:g}; the precompute needs "

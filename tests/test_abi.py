@@ -262,6 +262,16 @@ def test_clock_sample_arguments(lib):
         ("clock_sample_kernel", [1, 1, 1], 64)]
 
 
+def test_stream_probe_arguments(lib):
+    """The streaming-floor probe validates before any launch."""
+    for args in ((A16, 1024, 0, 1), (A16, 1024, 1 << 21, 1), (A16, 1024, 4, 2), (None, 1024, 4, 1),
+                 (A16 + 8, 1024, 4, 1), (A16, 1000, 4, 1), (A16, 0, 4, 1),
+                 (A16, 16 * 16 * 256 * 4 + 16, 4, 1)):  # 17 pieces per thread
+        assert lib.neso_stream_probe(args[0], args[1], args[2], args[3], 0, A16, None) \
+            == _lib.NESO_EINVAL, args
+    assert lib.neso_stream_probe(A16, 1024, 4, 1, 0, None, None) == _lib.NESO_EINVAL
+
+
 def test_status_strings(lib):
     for code in (_lib.NESO_OK, _lib.NESO_EINVAL, _lib.NESO_EUNSUPPORTED, _lib.NESO_ELAUNCH):
         assert lib.neso_status_string(code).startswith(b"NESO_")
@@ -428,6 +438,30 @@ def test_w8a16_validation(lib, scaled):
     assert b"K=0" in lib.neso_last_error()
     bad[-3] = 0
     assert fn(*bad) == _lib.NESO_OK
+
+
+def test_qmatmul_4gib_extents_rejected(lib):
+    """The int4 and W8A16 kernels address X / Y / A / B with 32-bit buffer
+    offsets: a call whose byte extent reaches 2^32 is rejected before any
+    launch (it would otherwise wrap and read zeros past the wrapped end).
+    Extents just below the limit pass validation (M = 0: no launch)."""
+    # int4: X spans (M-1) * ldx + K halves; 2^31 halves is 4 GiB.
+    m = (1 << 31) // 4096 + 1
+    assert w4(lib, M=m, ldx=4096, ldy=11008) == _lib.NESO_EINVAL
+    assert b"4 GiB" in lib.neso_last_error()
+    assert w4(lib, M=2, ldx=(1 << 31) - 8) == _lib.NESO_EINVAL
+    assert w4(lib, M=2, N=64, ldy=(1 << 31) - 1, ldx=4096) == _lib.NESO_EINVAL
+    assert w4(lib, M=0, ldx=(1 << 31) - 8) == _lib.NESO_OK
+    for scaled in (False, True):
+        fn = lib.neso_w8a16_scaled_matmul if scaled else lib.neso_w8a16_matmul
+        extra = [A16] if scaled else []
+        # B int8 [K][N]: (K - 1) * ldb + N bytes; ldb = 2^23 with K = 513 is 4 GiB + N.
+        args = [A16, A16, A16, *extra, 513, 513, 1 << 23, 64, 64, 64, None]
+        assert fn(*args) == _lib.NESO_EINVAL
+        assert b"4 GiB" in lib.neso_last_error()
+        # A fp16 [M][K]: 2^31 halves.
+        args = [A16, A16, A16, *extra, 64, 1 << 26, 64, 64, 33, 64, None]
+        assert fn(*args) == _lib.NESO_EINVAL
 
 
 def test_python_wrappers_raise():
