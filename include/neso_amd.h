@@ -90,11 +90,14 @@ int neso_clock_sample(uint64_t* out, int32_t samples, int32_t gap_ticks, void* s
  * nothing (dispatch and the kernel boundary alone); mode 1 reads `bytes`
  * bytes from `src` with 16-byte non-temporal loads, a rolling window of four
  * in flight per lane, thread t of the grid's T threads reading pieces t,
- * t + T, ..., and writes sink[0] only if the XOR of everything read equals
- * `key` (which keeps the loads live).  1 <= grid <= 2^20; mode 1: src
- * 16-byte aligned, bytes a positive multiple of 16 needing at most 16
- * pieces per thread (bytes <= 16 * 16 * 256 * grid) and below 4 GiB, sink
- * 4-byte aligned.
+ * t + T, ..., and writes sink[0] only if the XOR of everything that lane
+ * read equals `key` (which keeps the loads live without stores); mode 2
+ * reads the same way and writes every lane's XOR to sink[t], so that the
+ * XOR of sink[0 .. T-1] is the XOR of the buffer (a coverage check).
+ * 1 <= grid <= 2^20; modes 1 and 2: src 16-byte aligned, bytes a positive
+ * multiple of 16 needing at most 16 pieces per thread
+ * (bytes <= 16 * 16 * 256 * grid) and below 4 GiB, sink 4-byte aligned and,
+ * for mode 2, holding 256 * grid uint32 values.
  */
 int neso_stream_probe(const void* src, int64_t bytes, int32_t grid, int32_t mode, uint32_t key,
                       uint32_t* sink, void* stream);

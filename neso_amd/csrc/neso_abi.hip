@@ -226,11 +226,13 @@ __global__ __launch_bounds__(64) void clock_sample_kernel(uint64_t* out, int sam
 // grid (T threads) reads pieces t, t + T, ..., t + (NP - 1) T, the layout of
 // a persistent grid streaming one contiguous buffer.  Straight-line code
 // with a rolling window of DEPTH loads in flight per lane: piece k is folded
-// into an XOR as piece k + DEPTH is requested.  The XOR is written only if
-// it equals `key`, which keeps every load live.
+// into the lane's XOR as piece k + DEPTH is requested.  The timed form
+// (ALL = false) writes a lane's XOR only if it equals `key`, which keeps
+// every load live without stores; the checking form (ALL = true) writes
+// every lane's XOR to sink[t], so the host can XOR them into the buffer's.
 __global__ __launch_bounds__(256) void stream_empty_kernel() {}
 
-template <int NP, int DEPTH>
+template <int NP, int DEPTH, bool ALL>
 __global__ __launch_bounds__(256) void stream_read_kernel(const void* src, uint32_t bytes,
                                                           uint32_t key, uint32_t* sink) {
   const rsrc_t r = make_rsrc(src, bytes);
@@ -251,22 +253,31 @@ __global__ __launch_bounds__(256) void stream_read_kernel(const void* src, uint3
     }
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (acc == key) sink[0] = acc;
+  if (ALL)
+    sink[t] = acc;
+  else if (acc == key)
+    sink[0] = acc;
 }
 
 template <int NP>
-hipError_t launch_stream_read(int grid, hipStream_t st, const void* src, uint32_t bytes,
+hipError_t launch_stream_read(bool all, int grid, hipStream_t st, const void* src, uint32_t bytes,
                               uint32_t key, uint32_t* sink) {
-  return launch<&stream_read_kernel<NP, 4>>(ktag("stream_read_kernel", NP, 4), dim3(grid),
-                                             dim3(256), st, src, bytes, key, sink);
+  if (all)
+    return launch<&stream_read_kernel<NP, 4, true>>(ktag("stream_read_kernel", NP, 4, 1),
+                                                    dim3(grid), dim3(256), st, src, bytes, key,
+                                                    sink);
+  return launch<&stream_read_kernel<NP, 4, false>>(ktag("stream_read_kernel", NP, 4, 0),
+                                                   dim3(grid), dim3(256), st, src, bytes, key,
+                                                   sink);
 }
 
 template <int... NPS>
-hipError_t launch_stream_read_np(int np, int grid, hipStream_t st, const void* src,
+hipError_t launch_stream_read_np(int np, bool all, int grid, hipStream_t st, const void* src,
                                  uint32_t bytes, uint32_t key, uint32_t* sink,
                                  std::integer_sequence<int, NPS...>) {
   hipError_t err = hipErrorInvalidValue;
-  ((np == NPS + 1 ? (err = launch_stream_read<NPS + 1>(grid, st, src, bytes, key, sink), 0) : 0),
+  ((np == NPS + 1 ? (err = launch_stream_read<NPS + 1>(all, grid, st, src, bytes, key, sink), 0)
+                  : 0),
    ...);
   return err;
 }
@@ -326,7 +337,8 @@ int neso_stream_probe(const void* src, int64_t bytes, int32_t grid, int32_t mode
     return launched(neso::launch<&neso::stream_empty_kernel>(neso::ktag("stream_empty_kernel"),
                                                              dim3(grid), dim3(256), st),
                     "stream_probe");
-  if (mode != 1) return fail(NESO_EINVAL, "stream_probe: mode=%d not 0 or 1", mode);
+  if (mode != 1 && mode != 2)
+    return fail(NESO_EINVAL, "stream_probe: mode=%d not 0, 1 or 2", mode);
   if (!src || !aligned16(src) || !sink || (reinterpret_cast<uintptr_t>(sink) & 3u))
     return fail(NESO_EINVAL, "stream_probe: null or misaligned src/sink");
   const int64_t threads = (int64_t)grid * 256;
@@ -339,7 +351,8 @@ int neso_stream_probe(const void* src, int64_t bytes, int32_t grid, int32_t mode
     return fail(NESO_EINVAL, "stream_probe: bytes=%lld needs %lld pieces per thread at grid "
                 "%d (at most %d, and below 4 GiB)", (long long)bytes, (long long)np, grid,
                 neso::kStreamMaxPieces);
-  return launched(neso::launch_stream_read_np((int)np, grid, st, src, (uint32_t)bytes, key, sink,
+  return launched(neso::launch_stream_read_np((int)np, mode == 2, grid, st, src, (uint32_t)bytes,
+                                              key, sink,
                                               std::make_integer_sequence<int, neso::kStreamMaxPieces>()),
                   "stream_probe");
 }

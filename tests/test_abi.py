@@ -264,7 +264,7 @@ def test_clock_sample_arguments(lib):
 
 def test_stream_probe_arguments(lib):
     """The streaming-floor probe validates before any launch."""
-    for args in ((A16, 1024, 0, 1), (A16, 1024, 1 << 21, 1), (A16, 1024, 4, 2), (None, 1024, 4, 1),
+    for args in ((A16, 1024, 0, 1), (A16, 1024, 1 << 21, 1), (A16, 1024, 4, 3), (None, 1024, 4, 2),
                  (A16 + 8, 1024, 4, 1), (A16, 1000, 4, 1), (A16, 0, 4, 1),
                  (A16, 16 * 16 * 256 * 4 + 16, 4, 1)):  # 17 pieces per thread
         assert lib.neso_stream_probe(args[0], args[1], args[2], args[3], 0, A16, None) \
