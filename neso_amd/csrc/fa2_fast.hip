@@ -141,6 +141,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // K and V slots of the live layout, scores kept for the slow path (see
   // fast_live).
   constexpr bool kLive = fast_live<D, QW, BIAS, HALVES, PAIR, KSPLIT>();
+  // Ring layout at head_dim 64 without a bias or halves: Q arrives by LDS-DMA
+  // into ring slot 3 of key group 0 (free until step 1 loads block 3), so
+  // that no load the compiler tracks is in flight and the prologue can wait
+  // for Q and the first K tiles alone (counted vmcnt) while the later tiles
+  // land under block 0's softmax.
+  constexpr bool kQLds = !kLive && !HALVES && !BIAS && D == 64;
   constexpr int BSLOT = fast_band_slot<D, QW, BIAS, HALVES, PAIR, KSPLIT>();
   static_assert(!BIAS || 32 + kKB - 1 <= 2 * 64, "two band entries per lane");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
@@ -205,10 +211,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   const int qrows = HALVES ? max(0, min(N - qw0, 32)) : min(N - q0, kBMq);
   const rsrc_t rsQ = make_rsrc(Qh + (int64_t)qb * p.stride_q, (uint32_t)qrows * p.stride_q * 2);
   half8v qf[KS];
+  if constexpr (!kQLds) {
 #pragma unroll
-  for (int ks = 0; ks < KS; ++ks) {
-    const half8v t = buf_load_half8(rsQ, ((q - qb) * p.stride_q + 16 * ks + 8 * g) * 2);
-    qf[ks] = neg ? -t : t;
+    for (int ks = 0; ks < KS; ++ks) {
+      const half8v t = buf_load_half8(rsQ, ((q - qb) * p.stride_q + 16 * ks + 8 * g) * 2);
+      qf[ks] = neg ? -t : t;
+    }
   }
 
   // Key blocks of this workgroup: [blk0, blk0 + nblk); group kg takes blocks
@@ -659,6 +667,72 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   BandRegs bpro[3] = {};  // bias bands of blocks 0..2
   float16v sa[NT], sb[NT];
   half8v pa[2 * NT], pb2[2 * NT];
+  if constexpr (kQLds) {
+    // Q rows qb .. qb + kBMq - 1 (rows past N read as zeros) into ring slot 3
+    // of key group 0, row-major with the K chunk swizzle: 1 KiB instruction
+    // x holds rows RPI x .., QLC instructions per wave of the workgroup.
+    constexpr int QLC = kBMq * D * 2 / 1024 / (QW * KSPLIT);
+    static_assert(QLC >= 1 && QLC * QW * KSPLIT * 1024 == kBMq * D * 2 &&
+                  kBMq * D <= KSLOT + VSLOT, "Q staging");
+    const int wwg = kg * QW + wave;  // wave of the workgroup (scalar)
+    const uint32_t qslot_lds = lds_addr(smem) + (uint32_t)(3 * (KSLOT + VSLOT) * 2);
+#pragma unroll
+    for (int j = 0; j < QLC; ++j) {
+      const int x = wwg * QLC + j;
+      const int row = RPI * x + lane / CPR, pos = lane % CPR;
+      lds_dma16(rsQ, qslot_lds + (uint32_t)(x * 1024),
+                (uint32_t)((row * p.stride_q + 8 * (pos ^ kswz<D>(row))) * 2));
+    }
+    // K of blocks 0 and 1 first, then their V and block 2: the first wait
+    // covers Q, K0 and K1 only.
+    auto k_load = [&](int i, int s) {
+      const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
+      const rsrc_t rk = make_rsrc(Kh + (int64_t)kb0 * p.stride_kv, block_bytes(kb0));
+#pragma unroll
+      for (int j = 0; j < LCH; ++j) lds_dma16(rk, kslot_lds(s) + (uint32_t)(j * RPI * D * 2), kgo[j]);
+    };
+    auto v_load = [&](int i, int s) {
+      const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
+      const rsrc_t rv = make_rsrc(Vh + (int64_t)kb0 * p.stride_kv, block_bytes(kb0));
+#pragma unroll
+      for (int j = 0; j < LCH; ++j) lds_dma16(rv, vslot_lds(s) + (uint32_t)(j * RPI * D * 2), vgo[j]);
+    };
+    if (my_n > 0) k_load(0, 0);
+    if (my_n > 1) k_load(1, 1);
+    if (my_n > 0) v_load(0, 0);
+    if (my_n > 1) v_load(1, 1);
+    if (my_n > 2) {
+      k_load(2, 2);
+      v_load(2, 2);
+    }
+    serial_lds_point();
+    if (my_n > 2)
+      wait_vmem_n<4 * LCH>();  // V0, V1, K2, V2 still in flight
+    else
+      wait_vmem();
+    lds_barrier();
+    {
+      const half_t* qs = smem + 3 * (KSLOT + VSLOT);
+      const int row = wave * 32 + ql;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const half8v t = load_half8(qs + row * D + 8 * ((2 * ks + g) ^ kswz<D>(row)));
+        qf[ks] = neg ? -t : t;
+      }
+    }
+    // ---- step 0: scores of blocks 0 and 1, block 0's exact softmax ----
+    qk(sa, kslot(0), 0);
+    qk(sb, kslot(1), 1);
+    if (my_n > 0) {
+      const int kb0 = (blk0 + kg) * kKB;
+      const bool masked =
+          (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
+      l_run += slow_scores(sa, kb0, masked, pb2);
+    }
+    serial_lds_point();
+    wait_vmem();
+    lds_barrier();
+  } else {
   if (my_n > 0) {
     if constexpr (kLive) {
       // Without a bias, V of block 0 too: the V slots are free until step
@@ -718,6 +792,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   wait_vmem();
   if (BIAS && my_n > 2) band_store(0, bpro[2]);
   lds_barrier();
+  }  // kQLds
 
   // Steps 1, 2, ...: unrolled by four, so that the score and P arrays swap
   // roles without copies and each copy knows its ring slots (i % 4).

@@ -102,6 +102,14 @@ __device__ __forceinline__ int kswz(int r) {
 // s_waitcnt vmcnt(0) (expcnt and lgkmcnt left at their maxima).
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// s_waitcnt vmcnt(N): at most the N most recent vector-memory instructions
+// of this wave still in flight (gfx9 encoding: vmcnt bits 3:0 and 15:14).
+template <int N>
+__device__ __forceinline__ void wait_vmem_n() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
+}
+
 // 16 bytes per lane from the buffer into LDS (buffer_load_dwordx4 ... lds):
 // lane l's bytes land at LDS byte address lds + 16 l.  Written as asm so
 // that the compiler does not make the kernel's LDS reads wait for it (it
