@@ -138,7 +138,12 @@ int neso_flash_attention_fwd(const void* Q, const void* K, const void* V, float*
  * as hi*hi + hi*lo + lo*hi on the fp16 MFMA with fp32 accumulation, as is P
  * for P V, so results track an fp32 computation (about 1e-6 absolute for
  * unit-scale inputs).  Q, K, V elements must lie within the fp16 range
- * (|x| < 65504).
+ * (|x| < 65504), and a tensor whose largest |x| is below about 2^-2 loses
+ * relative accuracy (its lo parts fall into fp16 subnormals).  A caller
+ * brings either case into range exactly with power-of-two factors: Q * 2^a
+ * and K * 2^b with scale * 2^-(a+b), V * 2^c with O * 2^-c afterwards (the
+ * Python layer, neso_amd.flash_attention_fwd, does this from one device
+ * reduction per input).
  */
 int neso_flash_attention_f32_fwd(const float* Q, const float* K, const float* V, float* O,
                                  int32_t N, int32_t stride_qo, int32_t stride_kv, float scale,

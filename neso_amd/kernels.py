@@ -101,32 +101,89 @@ def _on_stream(stream: int, device):
     return torch.cuda.stream(torch.cuda.ExternalStream(stream, device=device))
 
 
-def _check_f16_range(inputs, stream: int) -> None:
-    """Raise NesoArgumentError if an fp32 input the kernel reads reaches the
-    fp16 limit: the fp32-input kernels split each element into fp16 hi + lo,
-    so |x| >= 65504 would turn into inf or NaN in the output.  NaN inputs
-    pass (they give NaN rows, as an fp32 computation does).
+# fp32 inputs of the split-precision kernels (fp16 hi + lo per element) keep
+# fp32-class accuracy while their largest magnitude lies in this range: below
+# it the lo parts (and the hi parts of small elements) fall into fp16
+# subnormals, from 2^15 up the hi parts approach the fp16 limit (65504).
+_SPLIT_RANGE = (2.0 ** -2, 2.0 ** 15)
+_SPLIT_TOP = 14     # rescaled inputs get their largest |x| in [2^13, 2^14)
+_QK_EXP_CAP = 50    # |exponent| of a Q or K rescale, so that the folded scale stays normal
+
+
+def _split_exponents(inputs, stream: int) -> dict[str, int]:
+    """Power-of-two exponents for the fp32 inputs of a split-precision call.
 
     ``inputs`` holds (tensor, name, view shape, view strides) for the
     elements the kernel reads.  One reduction per input and one
     synchronisation for all of them, on ``stream`` (the launch stream), so
-    data written there before the call is what is checked.  Skipped for raw
-    addresses, for host tensors (rejected at launch) and while the stream is
-    being captured into a graph."""
+    data written there before the call is what is measured.  Returns
+    {name: k} for each input whose largest |x| lies outside _SPLIT_RANGE: k
+    puts it in [2^13, 2^14), where the hi + lo split is exact to ~2^-22 of
+    the largest element, instead of underflowing (tiny inputs) or
+    overflowing (|x| >= 65504) in fp16.  Raises NesoArgumentError for
+    infinite inputs; NaN inputs pass (they give NaN rows, as an fp32
+    computation does).  Returns {} for raw addresses, host tensors
+    (rejected at launch) and while the stream is being captured into a
+    graph, where no synchronisation is possible."""
     views = [(t.as_strided(shape, strides), name) for t, name, shape, strides in inputs
              if isinstance(t, torch.Tensor) and t.device.type == "cuda"]
     if not views or torch.cuda.is_current_stream_capturing():
-        return
+        return {}
     dev = views[0][0].device
     with _on_stream(stream, dev):
         if torch.cuda.is_current_stream_capturing():
-            return
+            return {}
         maxima = torch.stack([v.abs().amax() for v, _ in views]).cpu()
+    out = {}
     for (_, name), m in zip(views, maxima.tolist()):
-        if m >= 65504.0:
+        if math.isinf(m):
             raise _lib.NesoArgumentError(
-                _lib.NESO_EINVAL, f"{name}: |x| reaches {m:g}; fp32 inputs must lie within the "
-                                  f"fp16 range (|x| < 65504)")
+                _lib.NESO_EINVAL, f"{name}: infinite element; fp32 inputs must be finite")
+        if m != m or m == 0.0 or _SPLIT_RANGE[0] <= m < _SPLIT_RANGE[1]:
+            continue
+        out[name] = _SPLIT_TOP - math.frexp(m)[1]  # m in [2^(e-1), 2^e)
+    return out
+
+
+def _pow2_scaled(t: torch.Tensor, k: int, name: str, stream: int) -> torch.Tensor:
+    """t * 2^k (exact: a power-of-two factor only moves exponents), same
+    shape and layout as t, formed on the launch stream."""
+    if not t.is_contiguous():
+        raise _lib.NesoArgumentError(
+            _lib.NESO_EINVAL, f"{name}: a non-contiguous fp32 input whose magnitude lies outside "
+                              f"[2^-2, 2^15) cannot be rescaled for the fp16 hi + lo split")
+    with _on_stream(stream, t.device):
+        return t * (2.0 ** k)
+
+
+def _rescale_split_inputs(Q, K, V, O, scale: float, inputs, stream: int, o_view):
+    """Apply _split_exponents: Q, K, V replaced by power-of-two rescaled
+    copies where needed, the Q and K factors folded into ``scale``.  Returns
+    (Q, K, V, scale, post) where ``post()`` undoes V's factor on O's view
+    after the launch (None when V is not rescaled; V is left alone when O
+    is not a tensor, and then must lie below 65504)."""
+    exps = _split_exponents(inputs, stream)
+    if not exps:
+        return Q, K, V, scale, None
+    kq = max(-_QK_EXP_CAP, min(_QK_EXP_CAP, exps.get("Q", 0)))
+    kk = max(-_QK_EXP_CAP, min(_QK_EXP_CAP, exps.get("K", 0)))
+    kv = exps.get("V", 0)
+    if kq:
+        Q = _pow2_scaled(Q, kq, "Q", stream)
+    if kk:
+        K = _pow2_scaled(K, kk, "K", stream)
+    post = None
+    if kv and isinstance(O, torch.Tensor):
+        V = _pow2_scaled(V, kv, "V", stream)
+
+        def post():
+            with _on_stream(stream, O.device):
+                o_view().mul_(2.0 ** -kv)
+    elif kv < 0:
+        raise _lib.NesoArgumentError(
+            _lib.NESO_EINVAL, "V: |x| reaches the fp16 limit (65504) of the hi + lo split and O "
+                              "is a raw address, so the result cannot be rescaled")
+    return Q, K, V, scale * 2.0 ** -(kq + kk), post
 
 
 def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scale: float, *,
@@ -143,9 +200,13 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
     ``batch_heads`` with ``stride_bh_qo`` / ``stride_bh_kv`` for B*H slices
     in one launch, and ``causal``.  ``qkv_dtype`` is 'f16' or 'f32' as in
     the reference's generator (:79-89); for tensors it follows Q's dtype.
-    fp32 tensors must hold |x| < 65504 (the kernel splits them into fp16
-    hi + lo); ``check_range`` verifies that before the launch (one device
-    reduction and a synchronisation per input, skipped under graph capture).
+    The fp32 kernel splits each element into fp16 hi + lo; with
+    ``check_range`` (default) the largest |x| of each fp32 tensor is
+    measured first (one device reduction per input and one synchronisation)
+    and a tensor outside [2^-2, 2^15) is replaced by an exact power-of-two
+    rescaled copy, its factor folded into ``scale`` (Q, K) or undone on O
+    (V), so any finite magnitude keeps fp32-class accuracy.  Without it, or
+    under graph capture, fp32 elements must lie below 65504 in magnitude.
     """
     if head_dim is None:
         if not isinstance(Q, torch.Tensor):
@@ -161,14 +222,17 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
         for t, nm, sp in ((Q, "Q", span_q), (K, "K", span_kv), (V, "V", span_kv),
                           (O, "O", span_q)):
             _extent(t, nm, sp)
-        if qkv_dtype == "f32" and check_range:
-            _check_f16_range(
-                [(t, nm, (batch_heads, N, head_dim), (sb, sr, 1))
-                 for t, nm, sr, sb in ((Q, "Q", stride_qo, stride_bh_qo),
-                                       (K, "K", stride_kv, stride_bh_kv),
-                                       (V, "V", stride_kv, stride_bh_kv))
-                 if isinstance(t, torch.Tensor) and t.dtype == torch.float32],
-                _stream(stream, Q, O))
+    post = None
+    if qkv_dtype == "f32" and check_range and N > 0 and batch_heads > 0:
+        st = _stream(stream, Q, O)
+        Q, K, V, scale, post = _rescale_split_inputs(
+            Q, K, V, O, scale,
+            [(t, nm, (batch_heads, N, head_dim), (sb, sr, 1))
+             for t, nm, sr, sb in ((Q, "Q", stride_qo, stride_bh_qo),
+                                   (K, "K", stride_kv, stride_bh_kv),
+                                   (V, "V", stride_kv, stride_bh_kv))
+             if isinstance(t, torch.Tensor) and t.dtype == torch.float32], st,
+            lambda: O.as_strided((batch_heads, N, head_dim), (stride_bh_qo, stride_qo, 1)))
     lib = _lib.load()
     dt = torch.float32 if qkv_dtype == "f32" else torch.float16
     fn = lib.neso_flash_attention_f32_fwd if qkv_dtype == "f32" else lib.neso_flash_attention_fwd
@@ -178,6 +242,8 @@ def flash_attention_fwd(Q, K, V, O, N: int, stride_qo: int, stride_kv: int, scal
         int(head_dim), int(batch_heads), int(stride_bh_qo), int(stride_bh_kv), int(bool(causal)),
         _stream(stream, Q, O))
     _lib.check(st)
+    if post:
+        post()
 
 
 def flash_attention_io_fwd(Q, K, V, O, N: int, d_head: int, scale: float, *,
@@ -190,10 +256,9 @@ def flash_attention_io_fwd(Q, K, V, O, N: int, d_head: int, scale: float, *,
     one type (``io_type`` half or float there), N, d_head, scale.  Keyword
     extensions: ``batch_heads`` contiguous [batch_heads, N, d_head] slices in
     one launch; ``io_dtype`` 'f16' or 'f32' (inferred from Q for tensors).
-    fp32 tensors must hold |x| < 65504 (the kernel splits them into fp16
-    hi + lo); ``check_range`` verifies that before the launch (one device
-    reduction per input and one synchronisation, skipped under graph
-    capture).
+    fp32 tensors are rescaled by powers of two where their magnitude needs
+    it, as in :func:`flash_attention_fwd` (``check_range``; without it, or
+    under graph capture, fp32 elements must lie below 65504 in magnitude).
     """
     if io_dtype is None:
         if not isinstance(Q, torch.Tensor):
@@ -204,11 +269,14 @@ def flash_attention_io_fwd(Q, K, V, O, N: int, d_head: int, scale: float, *,
     if N > 0 and batch_heads > 0:
         for t, nm in ((Q, "Q"), (K, "K"), (V, "V"), (O, "O")):
             _extent(t, nm, batch_heads * N * d_head)
-        if io_dtype == "f32" and check_range:
-            _check_f16_range(
-                [(t, nm, (batch_heads * N * d_head,), (1,)) for t, nm in ((Q, "Q"), (K, "K"), (V, "V"))
-                 if isinstance(t, torch.Tensor) and t.dtype == torch.float32],
-                _stream(stream, Q, O))
+    post = None
+    if io_dtype == "f32" and check_range and N > 0 and batch_heads > 0:
+        n_el = batch_heads * N * d_head
+        Q, K, V, scale, post = _rescale_split_inputs(
+            Q, K, V, O, scale,
+            [(t, nm, (n_el,), (1,)) for t, nm in ((Q, "Q"), (K, "K"), (V, "V"))
+             if isinstance(t, torch.Tensor) and t.dtype == torch.float32],
+            _stream(stream, Q, O), lambda: O.view(-1)[:n_el])
     dt = torch.float32 if io_dtype == "f32" else torch.float16
     lib = _lib.load()
     st = lib.neso_flash_attention_io_fwd(
@@ -216,6 +284,8 @@ def flash_attention_io_fwd(Q, K, V, O, N: int, d_head: int, scale: float, *,
         int(d_head), float(scale), _lib.NESO_IO_F32 if io_dtype == "f32" else _lib.NESO_IO_F16,
         int(batch_heads), _stream(stream, Q, O))
     _lib.check(st)
+    if post:
+        post()
 
 
 def flash_attention_window_fwd(Q, K, V, O, seq_len: int, stride_h: int, stride_m: int,

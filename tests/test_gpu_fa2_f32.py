@@ -114,24 +114,30 @@ def test_padded_strides_and_slices(gpu):
     assert (o.cpu()[..., d:] == 7.0).all()  # padding untouched
 
 
-def test_fp16_range_checked(gpu):
-    """fp32 inputs reaching the fp16 limit are rejected before the launch
-    (their fp16 hi part would be inf); row padding the kernel does not read
-    is not checked; NaN inputs are not rejected; under graph capture the
-    check is skipped."""
+def test_fp16_range_rescaled(gpu):
+    """fp32 inputs at or past the fp16 limit of the hi + lo split are
+    rescaled by a power of two before the launch and give the fp64
+    oracle's result; infinite inputs are rejected; row padding the kernel
+    does not read is not measured; NaN inputs pass (NaN rows); under graph
+    capture nothing is measured (no synchronisation) and the call still
+    captures."""
     q, k, v = (x.to(DEV) for x in _inputs(1, 2, 64, 64, seed=3))
-    for bad in (7e4, -float("inf")):
-        k[0, 1, 5, 7] = bad
-        with pytest.raises(neso_amd.NesoArgumentError, match="K: "):
-            neso_amd.attention(q, k, v)
-    k[0, 1, 5, 7] = 0.5
-    v[0, 0, 3, 2] = 65503.0  # largest fp16 below the limit: accepted
-    neso_amd.attention(q, k, v)
+    k[0, 1, 5, 7] = -float("inf")
+    with pytest.raises(neso_amd.NesoArgumentError, match="K: "):
+        neso_amd.attention(q, k, v)
+    k[0, 1, 5, 7] = 7e4
+    v[0, 0, 3, 2] = 3e5
+    out = neso_amd.attention(q, k, v)
+    torch.cuda.synchronize()
+    ref = A.attention(q.cpu(), k.cpu(), v.cpu(), 0.125, dtype=torch.float64)
+    assert ((out.cpu().double() - ref).abs().max() / ref.abs().max()).item() <= TOL32 / 4
     n, d, stride = 64, 64, 68
     buf = torch.randn(n, stride, device=DEV)
     buf[:, d:] = 1e9
     o = torch.zeros(n, stride, device=DEV)
     neso_amd.flash_attention_fwd(buf, buf, buf, o, n, stride, stride, 0.125, head_dim=d)
+    k[0, 1, 5, 7] = 0.5
+    v[0, 0, 3, 2] = 1.0
     q[0, 0, 0, 0] = float("nan")
     out = neso_amd.attention(q, k, v)
     torch.cuda.synchronize()
@@ -145,6 +151,24 @@ def test_fp16_range_checked(gpu):
     with torch.cuda.graph(g, stream=s):
         neso_amd.attention(q, k, v, out=out)  # no synchronisation inside capture
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("amps", [(1e-5, 1e-5, 1e-5), (1e-4, 1e-4, 1e-4), (1.0, 1.0, 1e-5),
+                                  (3e-3, 2e-2, 1e-3), (2e4, 1e-4, 1e5), (1.0, 1.0, 1e6)])
+def test_magnitudes_keep_fp32_accuracy(gpu, amps):
+    """Inputs far from unit scale keep the split kernel's fp32-class
+    accuracy relative to their size: below 2^-2 the fp16 lo parts (and the
+    hi parts below 6e-5) would be subnormal, above 65504 the hi parts
+    infinite; the power-of-two rescale avoids both.  The bar is the unit
+    bar scaled by V's amplitude, against the fp64 oracle on the same fp32
+    inputs (an unscaled split misses it by two orders at 1e-5)."""
+    b, h, n, d = 1, 2, 256, 64
+    g = torch.Generator().manual_seed(11)
+    q, k, v = (torch.randn((b, h, n, d), generator=g) * a for a in amps)
+    out = _run(q, k, v)
+    ref = A.attention(q, k, v, 0.125, dtype=torch.float64)
+    err = (out.double() - ref).abs().max().item()
+    assert err <= TOL32 * amps[2], (err, amps)
 
 
 def test_f32_errors(gpu):
