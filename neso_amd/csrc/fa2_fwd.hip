@@ -255,6 +255,35 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   const int krow = kRowPerm(ql);
   const half2v ones = {(half_t)1.f, (half_t)1.f};
 
+  // Dense f16 bias (the reference's rel-pos mode) with every row 16-byte
+  // aligned (kBiasDenseF16Row16: N, the head stride and the base multiples
+  // of 8 halves): lane (ql, g) needs B[q][kb0 + 32 t + 16 h + 8 g + 0..7]
+  // for tile t and half h of a block, eight consecutive halves, one 16-byte
+  // load.  They are issued one step ahead into a two-block register ring
+  // (block i in slot i % 2), so their latency (the bias is read once, from
+  // HBM) overlaps the previous block's work.  Block indices are clamped
+  // like the K/V loads, so every step issues the same loads.  Rows and keys
+  // past N read zeros or the next row's values; every such key is masked.
+  // Unaligned rows (kBiasDenseF16) are read element by element when the
+  // scores are formed.
+  constexpr bool kDense = BIAS == kBiasDenseF16Row16;
+  half8v bb[kDense ? 2 : 1][kDense ? 2 * NT : 1];
+  const rsrc_t rsB = make_rsrc(
+      kDense ? static_cast<const half_t*>(p.bias) + (int64_t)bh * p.bias_stride_h : nullptr,
+      kDense ? (uint32_t)((int64_t)N * N * 2) : 0u);
+  auto bias_load = [&](int i, int slot) {
+    if constexpr (kDense) {
+      const int kb0 = (blk0 + max(0, min(kgu + KSPLIT * i, nblk - 1))) * kKB;
+#pragma unroll
+      for (int t = 0; t < NT; ++t)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          bb[slot][2 * t + h] =
+              buf_load_half8(rsB, (uint32_t)(q * N + kb0 + 32 * t + 16 * h + 8 * g) * 2u);
+        }
+    }
+  };
+
   auto compute = [&](int i, int buf) {
     const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
     // A wave whose 32 queries all miss this key block has nothing to do.
@@ -290,8 +319,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int kr = 32 * t + 16 * (r >> 3) + 8 * g + (r & 7);  // key - kb0
-          if (BIAS == kBiasDenseF16) {
-            // Reference semantics: (QK^T + B) * scale, B dense [T, T] f16.
+          if constexpr (kDense) {
+            // Reference semantics: (QK^T + B) * scale, B dense [T, T] f16
+            // (prefetched by bias_load; keys past N are masked below).
+            const float b = (float)(buf ? bb[1][2 * t + (r >> 3)][r & 7] : bb[0][2 * t + (r >> 3)][r & 7]);
+            s[t][r] = (s[t][r] + (neg ? -b : b)) * c;
+          } else if constexpr (BIAS == kBiasDenseF16) {
             const int key = kb0 + kr;
             const half_t* bp = static_cast<const half_t*>(p.bias) +
                                (int64_t)bh * p.bias_stride_h;
@@ -412,11 +445,13 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fwd_kernel(Fa2Args p) {
   St stA, stB;
   gload(stA, 0);
   gload(stB, 1);
+  bias_load(0, 0);
   sstore(stA, 0);
   lds_barrier();
 
   auto step = [&](int i, int buf, St& cur, St& nxt) {
     gload(cur, i + 2);  // cur's block i is already in LDS
+    bias_load(i + 1, buf ^ 1);
     if (i < my_n) compute(i, buf);
     sstore(nxt, buf ^ 1);
     lds_barrier();
@@ -662,6 +697,12 @@ hipError_t launch_fa2(Fa2Args a, int head_dim, bool causal, int bias_kind, bool 
     return out_f16 ? launch_fa2_d<kBiasTableF32, true>(a, head_dim, causal, ksplit, stream)
                    : launch_fa2_d<kBiasTableF32, false>(a, head_dim, causal, ksplit, stream);
   }
+  // Dense bias rows that all start 16-byte aligned take 16-byte loads (the
+  // kernel forms 32-bit offsets into one head's N x N bias: N <= 32768).
+  if (a.N % 8 == 0 && a.N <= 32768 && a.bias_stride_h % 8 == 0 &&
+      (reinterpret_cast<uintptr_t>(a.bias) & 15) == 0)
+    return out_f16 ? launch_fa2_d<kBiasDenseF16Row16, true>(a, head_dim, causal, ksplit, stream)
+                   : launch_fa2_d<kBiasDenseF16Row16, false>(a, head_dim, causal, ksplit, stream);
   return out_f16 ? launch_fa2_d<kBiasDenseF16, true>(a, head_dim, causal, ksplit, stream)
                  : launch_fa2_d<kBiasDenseF16, false>(a, head_dim, causal, ksplit, stream);
 }

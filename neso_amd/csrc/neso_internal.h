@@ -10,7 +10,9 @@
 
 namespace neso {
 
-enum BiasKind { kBiasNone = 0, kBiasTableF32 = 1, kBiasDenseF16 = 2 };
+// kBiasDenseF16Row16 is internal to the generic FA2 kernel: the dense f16
+// bias with every row 16-byte aligned (16-byte bias loads).
+enum BiasKind { kBiasNone = 0, kBiasTableF32 = 1, kBiasDenseF16 = 2, kBiasDenseF16Row16 = 3 };
 
 struct Fa2Args {
   const void* Q;        // f16, or f32 for the f32-input kernels

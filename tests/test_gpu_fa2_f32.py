@@ -161,7 +161,7 @@ def test_magnitudes_keep_fp32_accuracy(gpu, amps):
     hi parts below 6e-5) would be subnormal, above 65504 the hi parts
     infinite; the power-of-two rescale avoids both.  The bar is the unit
     bar scaled by V's amplitude, against the fp64 oracle on the same fp32
-    inputs (an unscaled split misses it by two orders at 1e-5)."""
+    inputs (an unscaled split misses it by 6-20x at amplitude 1e-5)."""
     b, h, n, d = 1, 2, 256, 64
     g = torch.Generator().manual_seed(11)
     q, k, v = (torch.randn((b, h, n, d), generator=g) * a for a in amps)
