@@ -823,8 +823,9 @@ __global__ __launch_bounds__(kThreads) void w4a16_mfma_kernel(W4Args a) {
 // W8A16 GEMM: C[M][N] f32 = A[M][K] f16 * f16(B[K][N] int8) [* scale[n]].
 //
 // Workgroup tile 128 x 128, four waves of 64 x 64 (2 x 2
-// v_mfma_f32_32x32x16_f16 tiles), K-steps of kW8BK.  A goes through LDS with
-// rows padded by 8 halves (conflict-free ds_read_b128).  B is N-contiguous
+// v_mfma_f32_32x32x16_f16 tiles), K-steps of kW8BK.  A goes through LDS in
+// unpadded rows with a piece swizzle (w8_a_at: conflict-free 16-byte stores
+// and ds_read_b128 fragment reads).  B is N-contiguous
 // in memory and stays so in LDS: thread (row, column group) loads 32
 // contiguous bytes of one k-row, converts them to f16 exactly (int8 -> f16
 // via the exponent trick: 0x6400 | (b ^ 0x80) is 1024 + b + 128) and stores
@@ -836,17 +837,34 @@ __global__ __launch_bounds__(kThreads) void w4a16_mfma_kernel(W4Args a) {
 // Double-buffered LDS, global loads one step ahead.
 // K-step 64: 16 MFMAs per wave between barriers (measured at 4096^3 on one
 // box: 179.0 us against 181.9 us with K-steps of 32).
-constexpr int kW8BK = 64, kW8LD = kW8BK + 8;
+constexpr int kW8BK = 64;
 constexpr int kW8AP = kW8BK / 32;  // 16-byte A pieces per thread and row half
 
-// B tile in LDS: [k][n] f16 in 128-column halves, rows of 128 halves (16
-// chunks of 16 bytes, one row spans every bank); in half hb, chunk c of row
-// r sits at c ^ 5 (r % 4) ^ 2 hb.  A store pass (16 lanes: 4 rows x chunks
-// 4 j + s of 4 column groups j, or with two halves 2 rows x 2 x 4 groups)
-// covers 16 positions 4 (j ^ i) + (s ^ i [^ 2]), and so does a transposed-
-// read pass (4 rows i x chunks 4 u .. 4 u + 3): every bank once.
+// LDS banks as the counters show them on gfx950: a 16-byte read
+// (ds_read_b128, and the transposing ds_read_b64_tr_b16 by 32 lanes) is
+// served 256 bytes at a time over 64 banks, a 16-byte write 128 bytes (8
+// lanes) at a time over 32 banks.  The layouts below keep both passes on
+// distinct banks (SQ_LDS_BANK_CONFLICT = 0).
+//
+// A tile: [m][k] f16 rows of kW8BK = 64 halves without padding (8 pieces of
+// 16 bytes, 32 banks), piece p of row r at p ^ fa(r), fa(r) = 4 (r & 1) ^
+// ((r >> 1) & 7).  A write pass (rows 2i, 2i + 1, pieces 4 j + 0..3) puts
+// the two rows on complementary piece halves; a read pass (16 consecutive
+// rows, one piece; even rows on banks 0..31, odd rows on 32..63) maps the 8
+// rows of each bank half to 8 distinct pieces.
+__device__ __forceinline__ int w8_a_at(int r, int p) {
+  return r * kW8BK + 8 * (p ^ (4 * (r & 1)) ^ ((r >> 1) & 7));
+}
+
+// B tile: [k][n] f16 in 128-column halves, rows of 128 halves (16 chunks of
+// 16 bytes, 64 banks); in half hb, chunk c of row r sits at c ^ 2 (c >> 3)
+// ^ 5 (r % 4) ^ hb.  A write pass (one row, chunks 4 j + s of column groups
+// j = 0..3 in each half) lands on 8 distinct positions mod 8 (bit 3 of c
+// folded into bit 1, the second half one position over); a transposed-read
+// pass (4 rows r % 4 = 0..3 x chunks 4 u .. 4 u + 3) covers the four
+// aligned groups of four positions once each.
 __device__ __forceinline__ int w8_b_at(int hb, int r, int c) {
-  return (hb * kW8BK + r) * 128 + 8 * (c ^ (5 * (r & 3)) ^ (2 * hb));
+  return (hb * kW8BK + r) * 128 + 8 * (c ^ (2 * (c >> 3)) ^ (5 * (r & 3)) ^ hb);
 }
 // This lane's offset for the B fragment of column tile u of half hb
 // (v_frag_tr's addressing: row 8 (l / 32) + (l % 16) / 4, columns 32 u + 16
@@ -864,7 +882,7 @@ __global__ __launch_bounds__(2 * T) void w8a16_gemm_kernel(W8Args a) {
   constexpr int NT = 2 * T;          // threads
   constexpr int NI = T / 64;         // 32-column MFMA tiles per wave
   constexpr int NH = T / 128;        // 128-column B halves
-  __shared__ half8v as[2][T * kW8LD / 8];
+  __shared__ half8v as[2][T * kW8BK / 8];
   __shared__ __attribute__((aligned(16))) half_t bs[2][NH * kW8BK * 128];  // [half][k][n]
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -927,7 +945,7 @@ __global__ __launch_bounds__(2 * T) void w8a16_gemm_kernel(W8Args a) {
     for (int p = 0; p < kW8AP; ++p)
 #pragma unroll
       for (int j = 0; j < 2; ++j)
-        as[buf][((ar + (T / 2) * j) * kW8LD + 8 * (ap + 4 * p)) / 8] = g.av[j][p];
+        as[buf][w8_a_at(ar + (T / 2) * j, ap + 4 * p) / 8] = g.av[j][p];
     // Row br as f16 in [k][n] order: bytes (n, n+1) of a word -> one f16
     // pair; chunk c of the row at w8_b_at.
 #pragma unroll
@@ -971,7 +989,7 @@ __global__ __launch_bounds__(2 * T) void w8a16_gemm_kernel(W8Args a) {
         bf[ni] = v_frag_tr<128>(bs[buf], w8_b_tr_offset(lane, hb, NH == 2 ? ni : 2 * wn + ni), ks);
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi) {
-        const half8v af = as[buf][((64 * wm + 32 * mi + li) * kW8LD + 16 * ks + 8 * lh) / 8];
+        const half8v af = as[buf][w8_a_at(64 * wm + 32 * mi + li, 2 * ks + lh) / 8];
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) acc[mi][ni] = mfma32x32x16(af, bf[ni], acc[mi][ni]);
       }
