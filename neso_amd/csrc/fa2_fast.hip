@@ -141,12 +141,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // K and V slots of the live layout, scores kept for the slow path (see
   // fast_live).
   constexpr bool kLive = fast_live<D, QW, BIAS, HALVES, PAIR, KSPLIT>();
-  // Ring layout at head_dim 64 without a bias or halves: Q arrives by LDS-DMA
-  // into ring slot 3 of key group 0 (free until step 1 loads block 3), so
-  // that no load the compiler tracks is in flight and the prologue can wait
-  // for Q and the first K tiles alone (counted vmcnt) while the later tiles
-  // land under block 0's softmax.
-  constexpr bool kQLds = !kLive && !HALVES && !BIAS && D == 64;
+  // Ring layout at head_dim 64 without a bias: Q arrives by LDS-DMA into
+  // ring slot 3 of key group 0 (free until step 1 loads block 3), so that no
+  // load the compiler tracks is in flight and the prologue can wait for Q
+  // and the first K tiles alone (counted vmcnt) while the later tiles land
+  // under block 0's softmax.
+  constexpr bool kQLds = !kLive && !BIAS && D == 64;
   constexpr int BSLOT = fast_band_slot<D, QW, BIAS, HALVES, PAIR, KSPLIT>();
   static_assert(!BIAS || 32 + kKB - 1 <= 2 * 64, "two band entries per lane");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
@@ -668,20 +668,35 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   float16v sa[NT], sb[NT];
   half8v pa[2 * NT], pb2[2 * NT];
   if constexpr (kQLds) {
-    // Q rows qb .. qb + kBMq - 1 (rows past N read as zeros) into ring slot 3
-    // of key group 0, row-major with the K chunk swizzle: 1 KiB instruction
-    // x holds rows RPI x .., QLC instructions per wave of the workgroup.
+    // The workgroup's 128 query rows (rows past N read as zeros) into ring
+    // slot 3 of key group 0, row-major with the K chunk swizzle, staging
+    // row 32 sl + ql holding slice sl's row ql: rows q0 .. q0 + 127, or with
+    // HALVES the short block's 64 rows then the long block's.  1 KiB
+    // instruction x holds staging rows RPI x .., QLC instructions per wave
+    // of the workgroup.
     constexpr int QLC = kBMq * D * 2 / 1024 / (QW * KSPLIT);
     static_assert(QLC >= 1 && QLC * QW * KSPLIT * 1024 == kBMq * D * 2 &&
-                  kBMq * D <= KSLOT + VSLOT, "Q staging");
+                  kBMq * D <= KSLOT + VSLOT && (!HALVES || 64 % RPI == 0), "Q staging");
     const int wwg = kg * QW + wave;  // wave of the workgroup (scalar)
     const uint32_t qslot_lds = lds_addr(smem) + (uint32_t)(3 * (KSLOT + VSLOT) * 2);
 #pragma unroll
     for (int j = 0; j < QLC; ++j) {
       const int x = wwg * QLC + j;
-      const int row = RPI * x + lane / CPR, pos = lane % CPR;
-      lds_dma16(rsQ, qslot_lds + (uint32_t)(x * 1024),
-                (uint32_t)((row * p.stride_q + 8 * (pos ^ kswz<D>(row))) * 2));
+      const int row = RPI * x + lane / CPR, pos = lane % CPR;  // staging row
+      rsrc_t rq = rsQ;
+      int rr = row;  // row within rq
+      if constexpr (HALVES) {
+        // Scalar per instruction: the short block (hs = qblk) or the long
+        // one (hl = n64 - 1 - qblk, none when it is the short block).
+        const bool lng = RPI * x >= 64;
+        const int r0 = __builtin_amdgcn_readfirstlane(64 * (lng ? n64 - 1 - qblk : qblk));
+        const int nr = __builtin_amdgcn_readfirstlane(
+            (lng && n64 - 1 - qblk == qblk) ? 0 : max(0, min(64, N - r0)));
+        rq = make_rsrc(Qh + (int64_t)r0 * p.stride_q, (uint32_t)nr * p.stride_q * 2);
+        rr = row - (lng ? 64 : 0);
+      }
+      lds_dma16(rq, qslot_lds + (uint32_t)(x * 1024),
+                (uint32_t)((rr * p.stride_q + 8 * (pos ^ kswz<D>(row))) * 2));
     }
     // K of blocks 0 and 1 first, then their V and block 2: the first wait
     // covers Q, K0 and K1 only.
@@ -713,7 +728,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     lds_barrier();
     {
       const half_t* qs = smem + 3 * (KSLOT + VSLOT);
-      const int row = wave * 32 + ql;
+      const int row = sl * 32 + ql;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         const half8v t = load_half8(qs + row * D + 8 * ((2 * ks + g) ^ kswz<D>(row)));
@@ -723,7 +738,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     // ---- step 0: scores of blocks 0 and 1, block 0's exact softmax ----
     qk(sa, kslot(0), 0);
     qk(sb, kslot(1), 1);
-    if (my_n > 0) {
+    if (HALVES ? my_nw > 0 : my_n > 0) {
       const int kb0 = (blk0 + kg) * kKB;
       const bool masked =
           (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
