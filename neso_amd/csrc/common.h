@@ -83,6 +83,15 @@ __device__ __forceinline__ half8v buf_load_half8(rsrc_t r, uint32_t byte_off) {
 __device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t byte_off) {
   return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, byte_off, 0, 0));
 }
+// The same as asm, which the compiler's wait-count bookkeeping does not
+// see: the caller issues the s_waitcnt that covers it before any use of the
+// result, and ties the result to that wait (an empty asm with the value as
+// "+v" operand after it).
+__device__ __forceinline__ float buf_load_f32_untracked(rsrc_t r, uint32_t byte_off) {
+  float v;
+  asm volatile("buffer_load_dword %0, %1, %2, 0 offen" : "=v"(v) : "v"(byte_off), "s"(r) : "memory");
+  return v;
+}
 __device__ __forceinline__ void buf_store_f32x4(float4v v, rsrc_t r, uint32_t byte_off) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(int4v, v), r, byte_off, 0, 0);
 }

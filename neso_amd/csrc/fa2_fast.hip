@@ -147,6 +147,13 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // and the first K tiles alone (counted vmcnt) while the later tiles land
   // under block 0's softmax.
   constexpr bool kQLds = !kLive && !BIAS && D == 64;
+  // The same for the live layout with two query waves and 64-key blocks: Q
+  // (64 rows) in V slot 1 of key group 0, free until step 1 loads V of
+  // block 1.  The bias
+  // band's prologue loads are issued untracked (band_load_untracked) for
+  // the same reason.
+  constexpr bool kQLive = kLive && QW == 2 && !HALVES && 32 * QW <= kKB;
+  constexpr bool kQStage = kQLds || kQLive;
   constexpr int BSLOT = fast_band_slot<D, QW, BIAS, HALVES, PAIR, KSPLIT>();
   static_assert(!BIAS || 32 + kKB - 1 <= 2 * 64, "two band entries per lane");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
@@ -211,7 +218,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   const int qrows = HALVES ? max(0, min(N - qw0, 32)) : min(N - q0, kBMq);
   const rsrc_t rsQ = make_rsrc(Qh + (int64_t)qb * p.stride_q, (uint32_t)qrows * p.stride_q * 2);
   half8v qf[KS];
-  if constexpr (!kQLds) {
+  if constexpr (!kQStage) {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       const half8v t = buf_load_half8(rsQ, ((q - qb) * p.stride_q + 16 * ks + 8 * g) * 2);
@@ -357,6 +364,26 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     }
     return r;
   };
+  // band_load through asm buffer loads the compiler does not track (their
+  // waits are explicit, band_ready after them).
+  auto band_load_untracked = [&](int i) {
+    BandRegs r{};
+    if constexpr (BIAS) {
+      const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
+      const int j0 = qw0 - kb0 - (kKB - 1) + N - 1 + lane;
+      r.t[0] = buf_load_f32_untracked(rsT, elem_offset(j0, 2 * N - 1, 4));
+      if constexpr (BENT > 64) r.t[1] = buf_load_f32_untracked(rsT, elem_offset(j0 + 64, 2 * N - 1, 4));
+    }
+    return r;
+  };
+  // After the explicit wait that covers them: ties the registers to it.
+  auto band_ready = [&](BandRegs& r) {
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int e = 0; e < (BENT > 64 ? 2 : 1); ++e) asm volatile("" : "+v"(r.t[e]));
+    }
+  };
+  constexpr int kBandLoads = BIAS ? (BENT > 64 ? 2 : 1) : 0;  // per block and lane
   // Band slots by block parity: block i uses slot i % 2 (par).
   auto band_store = [&](int par, const BandRegs& r) {
     if constexpr (BIAS) {
@@ -746,6 +773,71 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     }
     serial_lds_point();
     wait_vmem();
+    lds_barrier();
+  } else if constexpr (kQLive) {
+    // Issue order: bands of blocks 0, 1 (untracked), Q, K0, K1, and V0
+    // without a bias.  The first wait covers bands, Q and K0; the second K1.
+    if (my_n > 0) bpro[0] = band_load_untracked(0);
+    if (my_n > 1) bpro[1] = band_load_untracked(1);
+    constexpr int QLC = kBMq * D * 2 / 1024 / (QW * KSPLIT);
+    static_assert(QLC >= 1 && QLC * QW * KSPLIT * 1024 == kBMq * D * 2 && kBMq * D <= VSLOT,
+                  "Q staging");
+    const int wwg = kg * QW + wave;
+    const uint32_t qslot_lds = lds_addr(smem) + (uint32_t)((2 * KSLOT + VSLOT) * 2);
+#pragma unroll
+    for (int j = 0; j < QLC; ++j) {
+      const int x = wwg * QLC + j;
+      const int row = RPI * x + lane / CPR, pos = lane % CPR;
+      lds_dma16(rsQ, qslot_lds + (uint32_t)(x * 1024),
+                (uint32_t)((row * p.stride_q + 8 * (pos ^ kswz<D>(row))) * 2));
+    }
+    if (my_n > 0) tile_load(0, false, 0);
+    if (my_n > 1) tile_load(1, false, 1);
+    if (!BIAS && my_n > 0) tile_load(0, true, 0);
+    serial_lds_point();
+    if (my_n > 1)
+      wait_vmem_n<LCH + (BIAS ? 0 : LCH)>();  // K1 (and V0) still in flight
+    else
+      wait_vmem();
+    band_ready(bpro[0]);
+    band_ready(bpro[1]);
+    band_store(0, bpro[0]);
+    band_store(1, bpro[1]);
+    lds_barrier();
+    {
+      const half_t* qs = smem + 2 * KSLOT + VSLOT;
+      const int row = wave * 32 + ql;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const half8v t = load_half8(qs + row * D + 8 * ((2 * ks + g) ^ kswz<D>(row)));
+        qf[ks] = neg ? -t : t;
+      }
+    }
+    // Scores of block 0; then K1 landed and a barrier (every wave done with
+    // K slot 0); K of block 2 into that slot while the scores of block 1 are
+    // formed.
+    qk(sa, kslot(0), 0);
+    if (my_n > 1) {
+      if constexpr (BIAS) wait_vmem(); else wait_vmem_n<LCH>();  // V0 may stay in flight
+    }
+    lds_barrier();
+    if (my_n > 2) {
+      tile_load(2, false, 0);
+      bpro[2] = band_load_untracked(2);
+    }
+    qk(sb, kslot(1), 1);
+    // ---- step 0: block 0's exact softmax (with the bias, V of block 0) ----
+    if (BIAS && my_n > 0) tile_load(0, true, 0);
+    serial_lds_point();
+    if (my_n > 0) {
+      const int kb0 = (blk0 + kg) * kKB;
+      const bool masked =
+          (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
+      l_run += slow_scores(sa, kb0, masked, pb2);
+    }
+    wait_vmem();
+    band_ready(bpro[2]);
+    if (BIAS && my_n > 2) band_store(0, bpro[2]);
     lds_barrier();
   } else {
   if (my_n > 0) {
