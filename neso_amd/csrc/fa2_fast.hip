@@ -342,10 +342,11 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // wave's 32 queries against the block's keys (indices past the table read
   // as zero; they meet only keys or queries past N).  Lane l loads entries
   // l and l + 64 into registers with the block's K (step i - 2) and stores
-  // them after that step's wait.  The block's scores (step i - 1) read
-  // their 16 NT entries per lane from the slot, and so does its slow path
-  // (step i) with four query waves; the slot is rewritten for block i + 2
-  // at the end of step i.
+  // them after that step's barrier (the slot is the wave's own, and its
+  // reads follow the store in program order).  The block's scores (step
+  // i - 1) read their 16 NT entries per lane from the slot, and so does its
+  // slow path (step i) with four query waves; the slot is rewritten for
+  // block i + 2 after the barrier of step i.
   constexpr int BENT = 32 + kKB - 1;  // band entries per block
   const float* Th = BIAS ? static_cast<const float*>(p.bias) + (int64_t)bh * p.bias_stride_h : nullptr;
   const rsrc_t rsT = make_rsrc(Th, BIAS ? (uint32_t)(2 * N - 1) * 4u : 0u);
@@ -686,8 +687,10 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     // stays in place.
     serial_lds_point();
     wait_vmem();
-    if (BIAS && i + 2 < my_n) band_store(P0, bload);
     lds_barrier();
+    // The band slot is this wave's own: its store needs no barrier, and
+    // after the barrier its latency overlaps the next step's loads.
+    if (BIAS && i + 2 < my_n) band_store(P0, bload);
   };
 
   // ---- prologue: blocks 0 and 1 into LDS in one round trip ----
@@ -837,8 +840,8 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     }
     wait_vmem();
     band_ready(bpro[2]);
-    if (BIAS && my_n > 2) band_store(0, bpro[2]);
     lds_barrier();
+    if (BIAS && my_n > 2) band_store(0, bpro[2]);
   } else {
   if (my_n > 0) {
     if constexpr (kLive) {
@@ -897,8 +900,8 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     l_run += slow_scores(sa, kb0, masked, pb2);
   }
   wait_vmem();
-  if (BIAS && my_n > 2) band_store(0, bpro[2]);
   lds_barrier();
+  if (BIAS && my_n > 2) band_store(0, bpro[2]);
   }  // kQLds
 
   // Steps 1, 2, ...: unrolled by four, so that the score and P arrays swap
