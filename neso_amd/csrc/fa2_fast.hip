@@ -88,12 +88,17 @@ constexpr int fast_band_slot() {
   return fast_kb<D, QW, BIAS, HALVES, PAIR, K>() == 64 ? 128 : 64;
 }
 
+// Floats past the band slots that reads of masked keys (past N) may touch
+// when the slots hold the workgroup's whole table range.
+constexpr int kFastTabPad = 64;
+
 // Bytes of LDS of one workgroup: the key groups' tiles, and with a bias two
-// band slots per wave.
+// band slots per wave (or the table range, in the same space).
 template <int D, int QW, bool BIAS, bool HALVES, bool PAIR, int K>
 constexpr int fast_lds_bytes() {
   return K * (fast_group_lds_halves<D, QW, BIAS, HALVES, PAIR, K>() * 2 +
-              (BIAS ? QW * 2 * fast_band_slot<D, QW, BIAS, HALVES, PAIR, K>() * 4 : 0));
+              (BIAS ? QW * 2 * fast_band_slot<D, QW, BIAS, HALVES, PAIR, K>() * 4 : 0)) +
+         (BIAS ? kFastTabPad * 4 : 0);
 }
 
 // Debug build (NESO_FA2_SERIAL_LDS): every LDS phase ends in a full wait and
@@ -119,12 +124,13 @@ __device__ __forceinline__ void serial_lds_point() {
 // (t / |scale|), so that c * s is the biased logit in log2 units and the
 // softmax is the unbiased one.
 template <int D, bool CAUSAL, bool OUT_F16, int KSPLIT, bool PAIR = false, bool HALVES = false,
-          int QW = 4, bool BIAS = false>
+          int QW = 4, bool BIAS = false, bool TAB = false>
 __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   static_assert(!PAIR || CAUSAL, "paired query blocks are for causal grids");
   static_assert(!HALVES || (CAUSAL && !PAIR), "64-row halves are for full causal grids");
   static_assert(QW == 4 || (QW == 2 && !HALVES), "query waves");
   static_assert(!BIAS || !CAUSAL, "the biased entry point is never masked");
+  static_assert(!TAB || BIAS, "the table range is a bias layout");
   constexpr int kBMq = 32 * QW;      // queries per workgroup
   constexpr int kGroup = 64 * QW;    // threads per key group
   constexpr int kKB = fast_kb<D, QW, BIAS, HALVES, PAIR, KSPLIT>();  // keys per block
@@ -157,8 +163,11 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   constexpr int BSLOT = fast_band_slot<D, QW, BIAS, HALVES, PAIR, KSPLIT>();
   static_assert(!BIAS || 32 + kKB - 1 <= 2 * 64, "two band entries per lane");
   __shared__ __attribute__((aligned(16))) half_t smem[KSPLIT * GLDS];
-  // Bias band: two slots per wave (its own, no barrier).
-  __shared__ float sband[BIAS ? KSPLIT * QW * 2 * BSLOT : 1];
+  // Bias band: two slots per wave (its own, no barrier); or the whole
+  // table range of the workgroup's rows, in the same space (see use_tab).
+  constexpr int kTabCap = KSPLIT * QW * 2 * BSLOT;
+  __shared__ float sband[BIAS ? kTabCap + kFastTabPad : 1];
+  float* const stab = sband;
 
   const int tid = threadIdx.x;
   const int kg = __builtin_amdgcn_readfirstlane(tid / kGroup);  // key group
@@ -336,6 +345,13 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) koff[ks] = krow * D + 8 * ((2 * ks + g) ^ kswz<D>(krow));
 
+  // Bias entries enter the score MFMAs as their initial accumulator, in
+  // score units (t / |scale|), from one of two LDS layouts.
+  // * Table range (use_tab): the entries q0 .. q0 + kBMq + N - 2, all that
+  //   the workgroup's rows meet, loaded once in the prologue when they fit
+  //   in the band slots' space (kBMq + N - 1 <= kTabCap), entry q0 + x at
+  //   position kTabCap - 1 - x.
+  // * Otherwise per-block bands.
   // Bias band of block i (BIAS): entry j < 32 + KB - 1, at position
   // BSLOT - 1 - j of the wave's band slot i % 2, is table[h][qw0 - kb0 -
   // (KB - 1) + N - 1 + j] in score units (t / |scale|), the entries of this
@@ -352,12 +368,37 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   const rsrc_t rsT = make_rsrc(Th, BIAS ? (uint32_t)(2 * N - 1) * 4u : 0u);
   const float tscale = kLog2e / c;  // c (s + t tscale) = c s + t log2(e)
   float* const band = &sband[BIAS ? (kg * QW + wave) * 2 * BSLOT : 0];
+  constexpr int kThreads = 64 * QW * KSPLIT;
+  constexpr int kTL = BIAS ? kTabCap / kThreads : 1;  // table loads per thread (BSLOT / 32)
+  static_assert(!BIAS || kTL * kThreads == kTabCap, "table range");
+  const int ntab = kBMq + N - 1;  // <= kTabCap (the launcher's choice of TAB)
+  constexpr bool use_tab = TAB;
+  // The table range's loads, first of all (untracked; tab_store after the
+  // prologue's first wait stores them).
+  float tabv[kTL];
+  if constexpr (use_tab) {
+#pragma unroll
+    for (int m = 0; m < kTL; ++m) {
+      const int x = tid + kThreads * m;
+      if (x < ntab) tabv[m] = buf_load_f32_untracked(rsT, elem_offset(q0 + x, 2 * N - 1, 4));
+    }
+  }
+  auto tab_store = [&]() {
+    if constexpr (use_tab) {
+#pragma unroll
+      for (int m = 0; m < kTL; ++m) {
+        asm volatile("" : "+v"(tabv[m]));
+        const int x = tid + kThreads * m;
+        if (x < ntab && x < kTabCap) stab[kTabCap - 1 - x] = tabv[m] * tscale;
+      }
+    }
+  };
   struct BandRegs {
     float t[BENT > 64 ? 2 : 1];
   };
   auto band_load = [&](int i) {
     BandRegs r{};
-    if constexpr (BIAS) {
+    if constexpr (BIAS && !use_tab) {
       const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
       const int j0 = qw0 - kb0 - (kKB - 1) + N - 1 + lane;
       r.t[0] = buf_load_f32(rsT, elem_offset(j0, 2 * N - 1, 4));
@@ -369,7 +410,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // waits are explicit, band_ready after them).
   auto band_load_untracked = [&](int i) {
     BandRegs r{};
-    if constexpr (BIAS) {
+    if constexpr (BIAS && !use_tab) {
       const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
       const int j0 = qw0 - kb0 - (kKB - 1) + N - 1 + lane;
       r.t[0] = buf_load_f32_untracked(rsT, elem_offset(j0, 2 * N - 1, 4));
@@ -387,21 +428,27 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   constexpr int kBandLoads = BIAS ? (BENT > 64 ? 2 : 1) : 0;  // per block and lane
   // Band slots by block parity: block i uses slot i % 2 (par).
   auto band_store = [&](int par, const BandRegs& r) {
-    if constexpr (BIAS) {
+    if constexpr (BIAS && !use_tab) {
       float* const slot = band + BSLOT * par + BSLOT - 1;
       slot[-lane] = r.t[0] * tscale;
       if constexpr (BENT > 64) slot[-(lane + 64)] = r.t[1] * tscale;  // within the slot
     }
   };
-  // Initial score accumulator of 32-key tile t of block i: register r of
-  // lane (ql, g) is key 32 t + 16 (r / 8) + 8 g + r % 8 of the block, band
-  // entry ql - key + KB - 1 at position BSLOT - KB - ql + key: consecutive
-  // registers read consecutive positions (pairs of them per ds_read2_b32,
-  // straight into the accumulator registers).
-  auto band_acc = [&](int par, int t) {
+  // Initial score accumulator of 32-key tile t of the block at key kbb
+  // (band slot par): register r of lane (ql, g) is key 32 t + 16 (r / 8) +
+  // 8 g + r % 8 of the block, band entry ql - key + KB - 1 at position
+  // BSLOT - KB - ql + key, or table entry q - (kbb + key) + N - 1 at
+  // position kTabCap - 1 - (q - q0) + kbb + key - (N - 1): either way
+  // consecutive registers read consecutive positions (pairs of them per
+  // ds_read2_b32, straight into the accumulator registers).
+  auto band_acc = [&](int par, int kbb, int t) {
     float16v a;
     if constexpr (BIAS) {
-      const float* b = band + BSLOT * par + BSLOT - kKB - ql + 8 * g + 32 * t;
+      const float* b;
+      if constexpr (use_tab)
+        b = stab + (kTabCap - 1) - (qw0 - q0) - (N - 1) - ql + 8 * g + kbb + 32 * t;
+      else
+        b = band + BSLOT * par + BSLOT - kKB - ql + 8 * g + 32 * t;
 #pragma unroll
       for (int r = 0; r < 16; ++r) a[r] = b[16 * (r >> 3) + (r & 7)];
     } else {
@@ -410,13 +457,13 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     return a;
   };
 
-  // Scores of a block (K tile in k_l), with its bias band (slot par) as
-  // initial accumulator.
-  auto qk = [&](float16v(&s)[NT], const half_t* k_l, int par) {
+  // Scores of a block (K tile in k_l, first key kbb), with its bias (band
+  // slot par) as initial accumulator.
+  auto qk = [&](float16v(&s)[NT], const half_t* k_l, int par, int kbb) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
       s[t] = mfma32x32x16(load_half8(k_l + koff[0] + 32 * t * D), qf[0],
-                          BIAS ? band_acc(par, t) : float16v{});
+                          BIAS ? band_acc(par, kbb, t) : float16v{});
 #pragma unroll
       for (int ks = 1; ks < KS; ++ks)
         s[t] = mfma32x32x16(load_half8(k_l + koff[ks] + 32 * t * D), qf[ks], s[t]);
@@ -465,7 +512,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // sum of fp16 pcur.
   auto fused = [&](const float16v(&s)[NT], float16v(&sn)[NT], const half_t* k_l,
                    const half_t* v_l, const half8v(&pprev)[2 * NT], half8v(&pcur)[2 * NT],
-                   int npar) {
+                   int npar, int kbn) {
     constexpr int NQ = KS * NT;       // score MFMAs
     constexpr int NP = DT * 2 * NT;   // P V MFMAs
     constexpr int NJ = NQ + NP;       // slots
@@ -486,7 +533,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     float16v binit[NT];  // bias band of the next block (slot npar), read ahead of the K fragments
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-      if constexpr (BIAS) binit[t] = band_acc(npar, t);
+      if constexpr (BIAS) binit[t] = band_acc(npar, kbn, t);
     half8v fr[NJ];
 #pragma unroll
     for (int j = 0; j < AHEAD; ++j) fr[j] = frag(j);
@@ -585,7 +632,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   // not keep them live.
   auto slow = [&](int ks, int par, int kb0, bool masked, half8v(&pb)[2 * NT]) {
     float16v s[NT];
-    qk(s, kslot(ks), par);
+    qk(s, kslot(ks), par, kb0);
     return slow_scores(s, kb0, masked, pb);
   };
 
@@ -638,7 +685,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
         const int kb0 = (blk0 + kg + KSPLIT * i) * kKB;
         const bool masked =
             (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
-        float ls = fused(s, sn, kslot(P1), vslot(P1), pprev, pcur, P1);
+        float ls = fused(s, sn, kslot(P1), vslot(P1), pprev, pcur, P1, kb0 + KSPLIT * kKB);
         if (__any(masked || !(ls <= thr))) ls = slow_scores(s, kb0, masked, pcur);
         l_run += ls;
       }
@@ -676,7 +723,8 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
           (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
       // After the group's last block the next scores come from a stale
       // slot and are never used.
-      float ls = fused(s, sn, kslot((R + 1) & 3), vslot((R + 3) & 3), pprev, pcur, P1);
+      float ls = fused(s, sn, kslot((R + 1) & 3), vslot((R + 3) & 3), pprev, pcur, P1,
+                       kb0 + KSPLIT * kKB);
       // ls enters the condition so that the softmax cannot sink below it.
       if (__any(masked || !(ls <= thr))) ls = slow(R, P0, kb0, masked, pcur);
       l_run += ls;
@@ -766,8 +814,8 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       }
     }
     // ---- step 0: scores of blocks 0 and 1, block 0's exact softmax ----
-    qk(sa, kslot(0), 0);
-    qk(sb, kslot(1), 1);
+    qk(sa, kslot(0), 0, (blk0 + kg) * kKB);
+    qk(sb, kslot(1), 1, (blk0 + kg + KSPLIT) * kKB);
     if (HALVES ? my_nw > 0 : my_n > 0) {
       const int kb0 = (blk0 + kg) * kKB;
       const bool masked =
@@ -806,6 +854,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     band_ready(bpro[1]);
     band_store(0, bpro[0]);
     band_store(1, bpro[1]);
+    tab_store();
     lds_barrier();
     {
       const half_t* qs = smem + 2 * KSLOT + VSLOT;
@@ -819,7 +868,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
     // Scores of block 0; then K1 landed and a barrier (every wave done with
     // K slot 0); K of block 2 into that slot while the scores of block 1 are
     // formed.
-    qk(sa, kslot(0), 0);
+    qk(sa, kslot(0), 0, (blk0 + kg) * kKB);
     if (my_n > 1) {
       if constexpr (BIAS) wait_vmem(); else wait_vmem_n<LCH>();  // V0 may stay in flight
     }
@@ -828,7 +877,7 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       tile_load(2, false, 0);
       bpro[2] = band_load_untracked(2);
     }
-    qk(sb, kslot(1), 1);
+    qk(sb, kslot(1), 1, (blk0 + kg + KSPLIT) * kKB);
     // ---- step 0: block 0's exact softmax (with the bias, V of block 0) ----
     if (BIAS && my_n > 0) tile_load(0, true, 0);
     serial_lds_point();
@@ -867,17 +916,18 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   wait_vmem();
   band_store(0, bpro[0]);
   band_store(1, bpro[1]);
+  tab_store();
   lds_barrier();
   if constexpr (kLive) {
     // Scores of block 0, a barrier (every wave done with K slot 0), then K
     // of block 2 into that slot while the scores of block 1 are formed.
-    qk(sa, kslot(0), 0);
+    qk(sa, kslot(0), 0, (blk0 + kg) * kKB);
     lds_barrier();
     if (my_n > 2) {
       tile_load(2, false, 0);
       bpro[2] = band_load(2);
     }
-    qk(sb, kslot(1), 1);
+    qk(sb, kslot(1), 1, (blk0 + kg + KSPLIT) * kKB);
   }
 
   // ---- step 0, peeled: block 0 is every row's first visible block, so its
@@ -891,12 +941,12 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
   }
   if (kLive && BIAS && my_n > 0) tile_load(0, true, 0);
   serial_lds_point();
-  if constexpr (!kLive) qk(sa, kslot(0), 0);
+  if constexpr (!kLive) qk(sa, kslot(0), 0, (blk0 + kg) * kKB);
   if (HALVES ? my_nw > 0 : my_n > 0) {
     const int kb0 = (blk0 + kg) * kKB;
     const bool masked =
         (kb0 + kKB > N) || (CAUSAL && (kb0 + kKB - 1 > qw0 + wr || kb0 < qw0 + 31 - wl));
-    if constexpr (!kLive) qk(sb, kslot(1), 1);
+    if constexpr (!kLive) qk(sb, kslot(1), 1, (blk0 + kg + KSPLIT) * kKB);
     l_run += slow_scores(sa, kb0, masked, pb2);
   }
   wait_vmem();
@@ -1093,6 +1143,17 @@ bool launch_fast_k(const Fa2Args& a, hipStream_t stream, hipError_t& err) {
     }
   }
   if constexpr (fast_lds_bytes<D, QW, BIAS, false, false, K>() <= 160 * 1024) {
+    if constexpr (BIAS) {
+      // The bias table range of a workgroup's rows in the band slots' space
+      // when it fits (the plan records BIAS = 2 for it).
+      constexpr int cap = K * QW * 2 * fast_band_slot<D, QW, BIAS, false, false, K>();
+      if ((int64_t)32 * QW + a.N - 1 <= cap) {
+        err = launch<&fa2_fast_kernel<D, CAUSAL, OUT_F16, K, false, false, QW, true, true>>(
+            ktag("fa2_fast_kernel", D, CAUSAL, OUT_F16, K, false, false, QW, 2),
+            dim3(a.num_qblocks * a.batch_heads), dim3(K * 64 * QW), stream, a);
+        return true;
+      }
+    }
     err = launch<&fa2_fast_kernel<D, CAUSAL, OUT_F16, K, false, false, QW, BIAS>>(
         ktag("fa2_fast_kernel", D, CAUSAL, OUT_F16, K, false, false, QW, BIAS),
         dim3(a.num_qblocks * a.batch_heads), dim3(K * 64 * QW), stream, a);

@@ -133,7 +133,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table whenever |scale| >= 1e-20 (BIAS 2: the table entries of a workgroup's rows, 32 * QW + N - 1, loaded once into the band slots' LDS when they fit, KSPLIT * QW * 2 * 128 or 64 floats; BIAS 1: per-block bands otherwise); KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -145,7 +145,7 @@ constexpr char kManifest[] = R"JSON({
       "block_m": "32 * QW",
       "block_n": "(64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32)",
       "lds_layout": "2 K + 2 V slots (scores kept for the slow path) if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else a 4-slot ring of K + V",
-      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0))"
+      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0)) + (256 if BIAS else 0)"
      }
     },
     {
@@ -410,7 +410,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table whenever |scale| >= 1e-20 (BIAS 2: the table entries of a workgroup's rows, 32 * QW + N - 1, loaded once into the band slots' LDS when they fit, KSPLIT * QW * 2 * 128 or 64 floats; BIAS 1: per-block bands otherwise); KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -422,7 +422,7 @@ constexpr char kManifest[] = R"JSON({
       "block_m": "32 * QW",
       "block_n": "(64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32)",
       "lds_layout": "2 K + 2 V slots (scores kept for the slow path) if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else a 4-slot ring of K + V",
-      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0))"
+      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0)) + (256 if BIAS else 0)"
      }
     },
     {
@@ -576,7 +576,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table whenever |scale| >= 1e-20 (BIAS 2: the table entries of a workgroup's rows, 32 * QW + N - 1, loaded once into the band slots' LDS when they fit, KSPLIT * QW * 2 * 128 or 64 floats; BIAS 1: per-block bands otherwise); KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -588,7 +588,7 @@ constexpr char kManifest[] = R"JSON({
       "block_m": "32 * QW",
       "block_n": "(64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32)",
       "lds_layout": "2 K + 2 V slots (scores kept for the slow path) if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else a 4-slot ring of K + V",
-      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0))"
+      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0)) + (256 if BIAS else 0)"
      }
     },
     {
@@ -752,7 +752,7 @@ constexpr char kManifest[] = R"JSON({
       "QW",
       "BIAS"
      ],
-     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table (BIAS) whenever |scale| >= 1e-20; KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
+     "when": "fp16 Q/K/V at head_dim 64 or 128: without a bias where measured faster than fa2_fwd_kernel (fa2_fast_preferred), and with the f32 bias table whenever |scale| >= 1e-20 (BIAS 2: the table entries of a workgroup's rows, 32 * QW + N - 1, loaded once into the band slots' LDS when they fit, KSPLIT * QW * 2 * 128 or 64 floats; BIAS 1: per-block bands otherwise); KSPLIT key groups of QW query waves (QW = 2 on grids whose 128-query workgroups fill at most half the CUs, from N = 512 without a bias, with KSPLIT = 4 while cdiv(N, 64) * batch_heads <= cus and N >= 1024, else 2); PAIR (causal grids of >= 2 workgroups per CU with QW = 4; head_dim 128 causal without a window from N = 2048 when cdiv(cdiv(N, 64), 2) * batch_heads <= cus with QW = 2, KSPLIT = 4): each workgroup takes query blocks x and nqb-1-x; HALVES (causal without a window, fewer than 2 workgroups per CU, QW = 4): each workgroup takes the 64-row blocks x and cdiv(N, 64)-1-x",
      "threadgroup_size": "64 * QW * KSPLIT",
      "num_warps": "QW * KSPLIT",
      "grid": [
@@ -764,7 +764,7 @@ constexpr char kManifest[] = R"JSON({
       "block_m": "32 * QW",
       "block_n": "(64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32)",
       "lds_layout": "2 K + 2 V slots (scores kept for the slow path) if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else a 4-slot ring of K + V",
-      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0))"
+      "lds_bytes": "KSPLIT * ((4 if (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1))) else 8) * (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) * D * 2 + (QW * 2 * (128 if (64 if (D == 64 and not (BIAS and QW == 4)) or (D == 128 and QW == 4 and (QW == 2 or (D == 128 and not BIAS and not HALVES and not (PAIR and KSPLIT == 1)))) else 32) == 64 else 64) * 4 if BIAS else 0)) + (256 if BIAS else 0)"
      }
     },
     {

@@ -180,7 +180,7 @@ CHOICE_CASES = [
     # 96 workgroups of 128 queries fill under half of 256
     # CUs, so the biased fast kernel runs 64-query workgroups, 4 key groups.
     ("neso_rel_pos_fa2_fwd", [_P] * 5 + [1500, 64, 0.125, 1500 * 64, 2999, 8, 64, 1, 1],
-     "fa2_fast_kernel", dict(D=64, QW=2, KSPLIT=4, BIAS=1)),
+     "fa2_fast_kernel", dict(D=64, QW=2, KSPLIT=4, BIAS=2)),
     # A larger biased grid: 128-query workgroups.
     ("neso_rel_pos_fa2_fwd", [_P] * 5 + [8192, 64, 0.125, 8192 * 64, 16383, 16, 64, 1, 1],
      "fa2_fast_kernel", dict(QW=4, KSPLIT=1, BIAS=1)),
