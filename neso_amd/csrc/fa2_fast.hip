@@ -425,7 +425,6 @@ __global__ __launch_bounds__(64 * QW * KSPLIT) void fa2_fast_kernel(Fa2Args p) {
       for (int e = 0; e < (BENT > 64 ? 2 : 1); ++e) asm volatile("" : "+v"(r.t[e]));
     }
   };
-  constexpr int kBandLoads = BIAS ? (BENT > 64 ? 2 : 1) : 0;  // per block and lane
   // Band slots by block parity: block i uses slot i % 2 (par).
   auto band_store = [&](int par, const BandRegs& r) {
     if constexpr (BIAS && !use_tab) {

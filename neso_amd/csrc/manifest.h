@@ -1051,7 +1051,7 @@ constexpr char kManifest[] = R"JSON({
       "WV",
       "G32"
      ],
-     "when": "M <= 64 outside the cases above",
+     "when": "M <= 32 (NESO_AMD_W4_SKINNY_MAX_M overrides, at most 64) outside the cases above",
      "threadgroup_size": "64 * WV",
      "num_warps": "WV",
      "grid": [
@@ -1070,7 +1070,7 @@ constexpr char kManifest[] = R"JSON({
      "template_params": [
       "KG"
      ],
-     "when": "M >= 192: dequantise-once 128 x 128 tiles, KG K-groups per workgroup (2 while the tiles fit on the CUs)",
+     "when": "M >= 129 (NESO_AMD_W4_TILE_MIN_M overrides): 128 x 128 tiles, each wave a 128 x 32 column strip with its weights dequantised once into MFMA registers and X through LDS; KG K-groups per workgroup (2 while the tiles fit on the CUs)",
      "threadgroup_size": "256 * KG",
      "num_warps": "4 * KG",
      "grid": [
@@ -1092,7 +1092,7 @@ constexpr char kManifest[] = R"JSON({
       "WN",
       "BN"
      ],
-     "when": "64 < M < 192",
+     "when": "32 < M <= 128",
      "threadgroup_size": "64 * WM * WN",
      "num_warps": "WM * WN",
      "grid": [

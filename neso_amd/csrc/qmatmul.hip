@@ -556,37 +556,42 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// Large-M regime, dequantise-once tile GEMM (M >= 128).
+// Large-M regime, tile GEMM (M >= 192).
 //
-// A workgroup computes a 128 (m) x 128 (n) tile of Y.  Its 8 waves form two
-// K-groups of 4 waves (64 x 64 each, 2 x 2 v_mfma_f32_32x32x16_f16 tiles):
-// group g takes the K-steps s = g, g + 2, ... in its own LDS buffers, so a
-// SIMD holds two waves whose loads, dequantisation and LDS traffic overlap
-// each other's MFMAs; the two partial tiles are summed through LDS at the
-// end.  Per K-step of 64 codes and group:
-//   * X tile 128 x 64 fp16 -> LDS, each 8-element group stored in the order
-//     {0,4,1,5,2,6,3,7} of unpack_word, rows padded to 72 halves;
-//   * W tile 128 rows x 64 codes: thread t loads word quad t&1 (32 codes,
-//     16 bytes) of row t>>1 and its scale, dequantises (c - z) * s once for
-//     the group (one fp16 rounding) and stores the 32 halves to an LDS B
-//     tile [n][k] in the same nibble order, rows padded to 72 halves;
-//   * each wave reads its A and B fragments (ds_read_b128) and issues 16
-//     MFMAs; a fragment feeds two MFMAs (4 KiB of LDS reads per 4 MFMAs).
-// LDS is double-buffered per group (2 x 72 KiB); global loads run two of
-// the group's steps ahead in registers; the next step's dequantisation and
-// LDS stores are issued among the current step's MFMAs.  One barrier per
-// step.
+// A workgroup computes a 128 (m) x 128 (n) tile of Y with KG K-groups of 4
+// waves; group g takes the contiguous range of K-steps [g T, (g + 1) T) (64
+// codes per step) in its own LDS buffers, and the groups' partial tiles are
+// summed through LDS at the end.  Wave w of a group owns columns
+// 32 w .. 32 w + 31 of the tile for all 128 rows (4 x 1
+// v_mfma_f32_32x32x16_f16 tiles), so no two waves of a group need the same
+// weights and each code is dequantised once per workgroup:
+//   * W: lane (n = l%32, h = l/32) loads word quad h (32 codes, 16 bytes,
+//     one scale group) of its row's step and its scale, and dequantises
+//     (c - z) * s (one fp16 rounding) straight into MFMA B operands: MFMA
+//     ks of the step takes word ks, i.e. codes 32 h + 8 ks + {0,4,1,5,2,6,
+//     3,7}, the order of unpack_word_x16;
+//   * X: the tile (128 x 64 fp16 per step) goes through LDS, each
+//     8-element group stored in that nibble order, rows padded to 72 halves
+//     (no bank conflicts); thread t loads 16-byte piece t%8 of rows
+//     t/8 + 32 j.  A wave's A fragment for MFMA (mi, ks) is row 32 mi + l%32
+//     at codes 32 h + 8 ks of the step, one ds_read_b128.
+// Per step and wave: 16 MFMAs, 16 fragment reads, 4 dequantised words and
+// 4 X stores.  Only X is stored to LDS; that store stream (LDS writes run at
+// about a third of the read rate on gfx950) was the cost of the earlier
+// form, which dequantised W into LDS too.  LDS is double-buffered per
+// group; X loads run two steps ahead of their store, W loads two steps
+// ahead of their use; the next step's X stores are issued among the current
+// step's MFMAs.  One barrier per step.
 constexpr int kTT = 128, kTK = 64, kTLD = kTK + 8;
 
-template <int kTKG>  // K-groups per workgroup (1 or 2)
+template <int kTKG>  // K-groups per workgroup
 __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   constexpr uint32_t kOut = 0x80000000u;  // buffer offset past any extent: loads return 0
   constexpr int kBuf = kTT * kTLD / 8;    // half8v per LDS tile
-  __shared__ half8v lds[kTKG][2][2][kBuf];  // [group][buffer][X, W]
+  __shared__ half8v lds[kTKG][2][kBuf];   // [group][buffer] X tile
   const int tid = threadIdx.x % 256, lane = tid & 63;
   const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x / 256);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
   const int li = lane & 31, lh = lane >> 5;
   const int mtiles = (a.M + kTT - 1) / kTT;
   const int ntiles = (a.N + kTT - 1) / kTT;
@@ -603,25 +608,30 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   const uint32_t gm = (uint32_t)a.group >> 5;  // 32-code chunks per scale group
   const bool gpow2 = (gm & (gm - 1)) == 0;
   const uint32_t gshift = __builtin_ctz(gm);
+  // Steps per group (every group runs the same count: the barrier is
+  // shared); steps past K read zeros.
+  const int T = ((a.K + kTK - 1) / kTK + kTKG - 1) / kTKG;
 
-  // X: row tid/8 + 32j, 16-byte piece tid%8 of the step.  W: row tid/2,
-  // word quad tid&1.
+  // X: row tid/8 + 32j, 16-byte piece tid%8 of the step.  W: row 32 wave + li
+  // of the tile, word quad lh of the step.
   const int xr0 = tid >> 3, xp = tid & 7;
-  const int wrow = tid >> 1, wq = tid & 1;
-  struct Stage {
+  const int wrow = 32 * wave + li;
+  struct XStage {
     half8v x[4];
+  };
+  struct WStage {
     uint4v w;
     half_t s;
   };
-  // Loads of the group's step t (global step kTKG t + kg).  Steps past K
-  // read zeros.
-  auto gload = [&](Stage& g, int t) {
-    const int k0 = (kTKG * t + kg) * kTK;
-    const uint32_t xoob = k0 + 8 * xp < a.K ? 0u : kOut;
+  auto xload = [&](XStage& g, int t) {
+    const int k = (kg * T + t) * kTK + 8 * xp;
+    const uint32_t xoob = k < a.K ? 0u : kOut;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-      g.x[j] = buf_load_half8(rx, (((uint32_t)(xr0 + 32 * j) * a.ldx + k0 + 8 * xp) * 2u) | xoob);
-    const uint32_t chunk = (uint32_t)(k0 >> 5) + wq;
+      g.x[j] = buf_load_half8(rx, (((uint32_t)(xr0 + 32 * j) * a.ldx + k) * 2u) | xoob);
+  };
+  auto wload = [&](WStage& g, int t) {
+    const uint32_t chunk = (uint32_t)((kg * T + t) * (kTK / 32)) + lh;
     const uint32_t woob = (int)(32 * chunk) < a.K ? 0u : kOut;
     const uint32_t sidx = gpow2 ? chunk >> gshift : chunk / gm;
     g.w = __builtin_bit_cast(uint4v, __builtin_amdgcn_raw_buffer_load_b128(
@@ -629,126 +639,111 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
     g.s = __builtin_bit_cast(half_t, (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
                                          rs, (((uint32_t)wrow * SG + sidx) * 2u) | woob, 0, 0));
   };
-  // Piece 0..3: X row piece j; 4..7: dequantised W word i = piece - 4.
-  auto sstore_piece = [&](const Stage& g, int buf, int piece) {
-    if (piece < 4) {
-      const half8v x = g.x[piece];
-      lds[kg][buf][0][((xr0 + 32 * piece) * kTLD + 8 * xp) / 8] =
-          half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
-    } else {
-      const int i = piece - 4;
-      const half2v s1 = {g.s, g.s};
-      const half_t s16v = g.s * (half_t)0.0625f;
-      const half2v s16 = {s16v, s16v};
-      half2v r[4];
-      unpack_word_x16(g.w[i], nib, zp, r);
-      const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
-      lds[kg][buf][1][(wrow * kTLD + 32 * wq + 8 * i) / 8] =
-          half8v{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
-    }
+  auto xstore = [&](const XStage& g, int buf, int j) {
+    const half8v x = g.x[j];
+    lds[kg][buf][((xr0 + 32 * j) * kTLD + 8 * xp) / 8] = half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
   };
 
-  float16v acc[2][2];
+  float16v acc[4];
 #pragma unroll
-  for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-    for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = float16v{};
+  for (int mi = 0; mi < 4; ++mi) acc[mi] = float16v{};
 
-  // One K-step on LDS buffer buf, with the next step's LDS stores (from
-  // stage g into buffer buf ^ 1) spread over its MFMAs.  After the last
+  // One step: X from LDS buffer buf, W from registers ws; X stage xn (the
+  // next step) stored into buffer buf ^ 1 among the MFMAs.  After the last
   // step the stage holds the zeros loaded past K; storing them into the
   // idle buffer is harmless and keeps the step one basic block.
-  auto step = [&](int buf, const Stage& g) {
-    const half8v* xb = lds[kg][buf][0];
-    const half8v* wb = lds[kg][buf][1];
-    auto afrag = [&](int mi, int ks) { return xb[((64 * wm + 32 * mi + li) * kTLD + 16 * ks + 8 * lh) / 8]; };
-    auto bfrag = [&](int nj, int ks) { return wb[((64 * wn + 32 * nj + li) * kTLD + 16 * ks + 8 * lh) / 8]; };
-    half8v af[2][2], bf[2][2];
+  auto step = [&](int buf, const WStage& ws, const XStage& xn) {
+    const half8v* xb = lds[kg][buf];
+    auto afrag = [&](int mi, int ks) { return xb[((32 * mi + li) * kTLD + 32 * lh + 8 * ks) / 8]; };
+    const half2v s1 = {ws.s, ws.s};
+    const half_t s16v = ws.s * (half_t)0.0625f;
+    const half2v s16 = {s16v, s16v};
+    half8v af[2][4];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) { af[0][t] = afrag(t, 0); bf[0][t] = bfrag(t, 0); }
+    for (int mi = 0; mi < 4; ++mi) af[0][mi] = afrag(mi, 0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int c = ks & 1;
       if (ks + 1 < 4) {
 #pragma unroll
-        for (int t = 0; t < 2; ++t) { af[c ^ 1][t] = afrag(t, ks + 1); bf[c ^ 1][t] = bfrag(t, ks + 1); }
+        for (int mi = 0; mi < 4; ++mi) af[c ^ 1][mi] = afrag(mi, ks + 1);
       }
+      half2v r[4];
+      unpack_word_x16(ws.w[ks], nib, zp, r);
+      const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
+      const half8v bop = half8v{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-        for (int nj = 0; nj < 2; ++nj) acc[mi][nj] = mfma32x32x16(af[c][mi], bf[c][nj], acc[mi][nj]);
-      sstore_piece(g, buf ^ 1, 2 * ks);
-      sstore_piece(g, buf ^ 1, 2 * ks + 1);
+      for (int mi = 0; mi < 4; ++mi) acc[mi] = mfma32x32x16(af[c][mi], bop, acc[mi]);
+      xstore(xn, buf ^ 1, ks);
     }
   };
 
-  // Group steps: both groups run the same count (the barrier is shared);
-  // a group's steps past K compute on zeros.
-  const int nsteps = (a.K + kTK - 1) / kTK;
-  const int T = (nsteps + kTKG - 1) / kTKG;
-  Stage g0, g1;
-  gload(g0, 0);
-  gload(g1, 1);
+  XStage x0, x1;
+  WStage w0, w1;
+  xload(x0, 0);
+  wload(w0, 0);
+  xload(x1, 1);
+  wload(w1, 1);
 #pragma unroll
-  for (int piece = 0; piece < 8; ++piece) sstore_piece(g0, 0, piece);
-  gload(g0, 2);
+  for (int j = 0; j < 4; ++j) xstore(x0, 0, j);
+  xload(x0, 2);
   lds_barrier();
-  // Step t computes buffer t&1 and stores step t+1 (stage (t+1)&1, loaded
-  // two steps ahead) into buffer (t+1)&1, then reloads that stage for step
-  // t+3.  Unrolled by two so the stages swap roles without copies.
+  // Step t: W stage t&1, X buffer t&1; X stage (t+1)&1 stored into buffer
+  // (t+1)&1 and reloaded with step t+3; W stage t&1 reloaded with step t+2.
+  // Unrolled by two so the stages swap roles without copies.
   for (int t0 = 0; t0 < T; t0 += 2) {
-    step(0, g1);
-    gload(g1, t0 + 3);
+    step(0, w0, x1);
+    wload(w0, t0 + 2);
+    xload(x1, t0 + 3);
     lds_barrier();
     if (t0 + 1 < T) {
-      step(1, g0);
-      gload(g0, t0 + 4);
+      step(1, w1, x0);
+      wload(w1, t0 + 3);
+      xload(x0, t0 + 4);
       lds_barrier();
     }
   }
 
-  // Sum the groups' partial tiles: group 1 publishes, group 0 adds and
-  // stores.  The loop's last barrier ordered every LDS read before this.
-  if constexpr (kTKG == 2) {
+  // Sum the groups' partial tiles into group 0, one group at a time in group
+  // order.  The loop's last barrier ordered every LDS read before this.
+  if constexpr (kTKG > 1) {
     static_assert(sizeof(lds) >= (size_t)4 * 64 * 64 * sizeof(float), "reduction buffer");
     float* red = reinterpret_cast<float*>(lds) + (size_t)wave * 64 * 64 + lane;
-    if (kg == 1) {
 #pragma unroll
-      for (int mi = 0; mi < 2; ++mi)
+    for (int g = 1; g < kTKG; ++g) {
+      if (g > 1) lds_barrier();
+      if (kg == g) {
 #pragma unroll
-        for (int nj = 0; nj < 2; ++nj)
+        for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) red[((2 * mi + nj) * 16 + r) * 64] = acc[mi][nj][r];
+          for (int r = 0; r < 16; ++r) red[(mi * 16 + r) * 64] = acc[mi][r];
+      }
+      lds_barrier();
+      if (kg == 0) {
+#pragma unroll
+        for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[mi][r] += red[(mi * 16 + r) * 64];
+      }
     }
-    lds_barrier();
-    if (kg == 1) return;
-#pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-      for (int nj = 0; nj < 2; ++nj)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[mi][nj][r] += red[((2 * mi + nj) * 16 + r) * 64];
+    if (kg != 0) return;
   }
 
-  // acc[mi][nj] register r: row 64 wm + 32 mi + 8(r/4) + 4 lh + r%4,
-  // column 64 wn + 32 nj + li of the tile at (m0, n0).  Rows past M fall
-  // outside the buffer resource (ldy >= N >= n0 + nrows); columns past N
-  // get an out-of-range offset.
+  // acc[mi] register r: row 32 mi + 8(r/4) + 4 lh + r%4, column
+  // 32 wave + li of the tile at (m0, n0).  Rows past M fall outside the
+  // buffer resource (ldy >= N >= n0 + nrows); columns past N get an
+  // out-of-range offset.
   const rsrc_t ry = make_rsrc(a.Y + (int64_t)m0 * a.ldy + n0, (uint32_t)(((int64_t)(mrows - 1) * a.ldy + nrows) * 2));
+  const int nl = 32 * wave + li;
+  const uint32_t noob = nl < nrows ? 0u : kOut;
 #pragma unroll
-  for (int nj = 0; nj < 2; ++nj) {
-    const int nl = 64 * wn + 32 * nj + li;
-    const uint32_t noob = nl < nrows ? 0u : kOut;
+  for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int mi = 0; mi < 2; ++mi)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int ml = 64 * wm + 32 * mi + 8 * (r >> 2) + 4 * lh + (r & 3);
-        const uint32_t off = (((uint32_t)ml * a.ldy + (uint32_t)nl) * 2u) | noob;
-        __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (half_t)acc[mi][nj][r]),
-                                              ry, off, 0, 0);
-      }
-  }
+    for (int r = 0; r < 16; ++r) {
+      const int ml = 32 * mi + 8 * (r >> 2) + 4 * lh + (r & 3);
+      const uint32_t off = (((uint32_t)ml * a.ldy + (uint32_t)nl) * 2u) | noob;
+      __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(uint16_t, (half_t)acc[mi][r]), ry, off, 0, 0);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1142,7 +1137,13 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
     // (qmatmul_skinny.hip).
     return launch_w4a16_skinny_lds(a, s);
   }
-  if (a.M <= 64 && skinny_fits) {
+  // The split-K skinny kernel up to M = 32; from M = 40 the 128 x 64 kernel
+  // below is faster (K = 4096, N = 11008, skinny / 128 x 64: M = 32 28.5 /
+  // 33.0 us, M = 40 36.4 / 33.3, M = 64 40.5 / 33.9).
+  // NESO_AMD_W4_SKINNY_MAX_M (at most 64) overrides.
+  const char* skinny_env = getenv("NESO_AMD_W4_SKINNY_MAX_M");
+  const int skinny_max_m = skinny_env ? atoi(skinny_env) : 32;
+  if (a.M <= skinny_max_m && a.M <= 64 && skinny_fits) {
     // One 8-byte load fetches the scales of a chunk quad when every chunk
     // has its own scale and rows hold whole quads (8-byte aligned).
     const bool g32 = a.group == 32 && a.K % 128 == 0;
@@ -1166,20 +1167,24 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
 #ifndef NESO_GEMM_BN
 #define NESO_GEMM_BN 64
 #endif
-  // Dequantise-once tile GEMM: 128 x 128 tiles; its buffer offsets (one
-  // tile's X rows, W rows and scales) must stay below 2^31 bytes.
+  // Tile GEMM: 128 x 128 tiles; its buffer offsets (one tile's X rows, W
+  // rows and scales) must stay below 2^31 bytes.
   const bool tile_fits = (int64_t)kTT * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
                          (int64_t)kTT * a.K / 2 < ((int64_t)1 << 31);
   const char* tile_env = getenv("NESO_AMD_W4_TILE_GEMM");
   const int tile_mode = tile_env ? atoi(tile_env) : -1;
-  // Measured at K = 4096, N = 11008: the tile GEMM wins from M = 256 up (two
+  // Measured at K = 4096, N = 11008: the tile GEMM wins above M = 128 (two
   // K-groups while the tiles fit on the CUs, one workgroup each; one K-group,
-  // two workgroups per CU, beyond); at M = 128 its 86 tiles leave most CUs
-  // idle and the 128 x 64 kernel below is faster.
-  // NESO_AMD_W4_TILE_GEMM = 0 / 1 / 2 forces off / one / two K-groups.
+  // two workgroups per CU, beyond: M = 144 39.2 against 54.6 us); up to
+  // M = 128 its 86 tiles leave most CUs idle and the 128 x 64 kernel below
+  // is faster (M = 128 34.7 against 37.1 us).
+  // NESO_AMD_W4_TILE_GEMM = 0 / 1 / 2 forces off / one / two K-groups, and
+  // NESO_AMD_W4_TILE_MIN_M moves the threshold.
   const int tiles = ((a.M + kTT - 1) / kTT) * ((a.N + kTT - 1) / kTT);
+  const char* tile_min_env = getenv("NESO_AMD_W4_TILE_MIN_M");
+  const int tile_min_m = tile_min_env ? atoi(tile_min_env) : 129;
   const int kgroups = tile_mode >= 0 ? tile_mode
-                      : a.M < 192    ? 0
+                      : a.M < tile_min_m ? 0
                                      : (tiles <= device_cu_count() ? 2 : 1);
   if (kgroups && tile_fits) {
     return kgroups == 2 ? launch<&w4a16_tile_gemm_kernel<2>>(

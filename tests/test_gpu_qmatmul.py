@@ -118,6 +118,34 @@ def test_small_m_both_regimes(gpu, monkeypatch, gemv_max_m, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
+@pytest.mark.parametrize("env,m,kernel", [
+    ({}, 32, "w4a16_skinny_kernel"),
+    ({}, 33, "w4a16_gemm_kernel"),
+    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 48, "w4a16_skinny_kernel"),
+    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 64, "w4a16_skinny_kernel"),
+    ({}, 64, "w4a16_gemm_kernel"),
+    ({}, 128, "w4a16_gemm_kernel"),
+    ({}, 129, "w4a16_tile_gemm_kernel"),
+    ({"NESO_AMD_W4_TILE_MIN_M": "192"}, 160, "w4a16_gemm_kernel"),
+    ({}, 160, "w4a16_tile_gemm_kernel"),
+])
+@pytest.mark.parametrize("n,k", [(300, 4096), (1000, 2080)])
+def test_route_thresholds(gpu, monkeypatch, env, m, kernel, n, k):
+    """Both kernels on each side of the skinny / 128 x 64 / tile GEMM
+    thresholds (M = 32 | 33 and 128 | 129 by default, moved by the
+    NESO_AMD_W4_SKINNY_MAX_M and NESO_AMD_W4_TILE_MIN_M overrides)."""
+    for key, val in env.items():
+        monkeypatch.setenv(key, val)
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n + k)
+    words = Q.pack_int4(codes.numpy())
+    xd, wd, sd = x.to(DEV), torch.as_tensor(words).to(DEV), scales.to(DEV)
+    plan = neso_amd.launch_plan("w4a16_matmul", xd, wd, sd, xd, m, n, k, k, n, 32, 8)
+    assert [p["device_kernel"] for p in plan] == [kernel], plan
+    y = gpu_w4(x, words, scales)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
+    assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
+
+
 @pytest.mark.parametrize("group,zero", [(64, 8), (128, 7), (32, 0), (4096, 15)])
 @pytest.mark.parametrize("m", [1, 16])
 def test_group_and_zero_point(gpu, group, zero, m):
