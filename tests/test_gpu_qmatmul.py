@@ -208,8 +208,14 @@ def test_outlier_activations(gpu, amp, at_zero, m):
     assert (np.abs(y - ref) <= half_ulp + fold).all(), np.abs(y - ref).max()
 
 
-def test_strided_output(gpu):
-    m, n, k = 3, 200, 512
+@pytest.mark.parametrize("m,tile", [(3, None), (48, None), (200, None), (300, "1"), (300, "2")])
+def test_strided_output(gpu, monkeypatch, m, tile):
+    """Row strides of X and Y wider than K and N on every regime (GEMV or
+    skinny, 128 x 64, tile GEMM with one and two K-groups): the padding
+    columns of Y keep their contents."""
+    if tile:
+        monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", tile)
+    n, k = 200, 512
     x, codes, scales = I.qmatmul_inputs(m, k, n, seed=9)
     words = torch.from_numpy(Q.pack_int4(codes.numpy())).to(DEV)
     xp = torch.zeros(m, k + 64, dtype=torch.float16, device=DEV)
