@@ -1068,19 +1068,20 @@ constexpr char kManifest[] = R"JSON({
      "device_kernel": "w4a16_tile_gemm_kernel",
      "source": "neso_amd/csrc/qmatmul.hip",
      "template_params": [
-      "KG"
+      "KG",
+      "WN"
      ],
-     "when": "M >= 129 (NESO_AMD_W4_TILE_MIN_M overrides): 128 x 128 tiles, each wave a 128 x 32 column strip with its weights dequantised once into MFMA registers and X through LDS; KG K-groups per workgroup (2 while the tiles fit on the CUs)",
-     "threadgroup_size": "256 * KG",
-     "num_warps": "4 * KG",
+     "when": "M > 32: 128 x 32 WN tiles, each wave a 128 x 32 column strip with its weights dequantised once into MFMA registers and X through LDS, KG K-groups of WN waves per workgroup; M >= 129 (NESO_AMD_W4_WIDE_TILE_MIN_M overrides): WN = 4, KG = 2 while the tiles fit on the CUs, else 1; M <= 128: WN = 2, KG = 4 while the tiles fit on the CUs, else 2",
+     "threadgroup_size": "64 * WN * KG",
+     "num_warps": "WN * KG",
      "grid": [
-      "cdiv(M, 128) * cdiv(N, 128)",
+      "cdiv(M, 128) * cdiv(N, 32 * WN)",
       "1",
       "1"
      ],
      "constants": {
       "block_m": "128",
-      "block_n": "128",
+      "block_n": "32 * WN",
       "block_k": "64"
      }
     },
@@ -1092,7 +1093,7 @@ constexpr char kManifest[] = R"JSON({
       "WN",
       "BN"
      ],
-     "when": "32 < M <= 128",
+     "when": "32 < M: only when the tile GEMM's buffer offsets would pass 2^31 bytes, or NESO_AMD_W4_TILE_GEMM = 0",
      "threadgroup_size": "64 * WM * WN",
      "num_warps": "WM * WN",
      "grid": [

@@ -584,22 +584,26 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
 // step's MFMAs.  One barrier per step.
 constexpr int kTT = 128, kTK = 64, kTLD = kTK + 8;
 
-template <int kTKG>  // K-groups per workgroup
-__global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
+template <int kTKG, int WN = 4>  // K-groups per workgroup, waves (32-column strips) per group
+__global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
+  static_assert(WN == 1 || WN == 2 || WN == 4, "waves per group");
   constexpr uint32_t kOut = 0x80000000u;  // buffer offset past any extent: loads return 0
   constexpr int kBuf = kTT * kTLD / 8;    // half8v per LDS tile
+  constexpr int GT = 64 * WN;             // threads per group
+  constexpr int TN = 32 * WN;             // tile columns
+  constexpr int XP = 16 / WN;             // X pieces per thread and step
   __shared__ half8v lds[kTKG][2][kBuf];   // [group][buffer] X tile
-  const int tid = threadIdx.x % 256, lane = tid & 63;
-  const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x / 256);
+  const int tid = threadIdx.x % GT, lane = tid & 63;
+  const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x / GT);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 31, lh = lane >> 5;
   const int mtiles = (a.M + kTT - 1) / kTT;
-  const int ntiles = (a.N + kTT - 1) / kTT;
+  const int ntiles = (a.N + TN - 1) / TN;
   const int id = (int)xcd_swizzle(blockIdx.x, (uint32_t)(mtiles * ntiles));
-  const int m0 = (id % mtiles) * kTT, n0 = (id / mtiles) * kTT;
+  const int m0 = (id % mtiles) * kTT, n0 = (id / mtiles) * TN;
   const int KW = a.K >> 3, SG = a.K / a.group;
   const int mrows = __builtin_amdgcn_readfirstlane(min(kTT, a.M - m0));
-  const int nrows = __builtin_amdgcn_readfirstlane(min(kTT, a.N - n0));
+  const int nrows = __builtin_amdgcn_readfirstlane(min(TN, a.N - n0));
   const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)(((int64_t)(mrows - 1) * a.ldx + a.K) * 2));
   const rsrc_t rw = make_rsrc(a.W + (int64_t)n0 * KW, (uint32_t)nrows * KW * 4u);
   const rsrc_t rs = make_rsrc(a.S + (int64_t)n0 * SG, (uint32_t)nrows * SG * 2u);
@@ -612,12 +616,12 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   // shared); steps past K read zeros.
   const int T = ((a.K + kTK - 1) / kTK + kTKG - 1) / kTKG;
 
-  // X: row tid/8 + 32j, 16-byte piece tid%8 of the step.  W: row 32 wave + li
-  // of the tile, word quad lh of the step.
+  // X: row tid/8 + 8 WN j, 16-byte piece tid%8 of the step.  W: row
+  // 32 wave + li of the tile, word quad lh of the step.
   const int xr0 = tid >> 3, xp = tid & 7;
   const int wrow = 32 * wave + li;
   struct XStage {
-    half8v x[4];
+    half8v x[XP];
   };
   struct WStage {
     uint4v w;
@@ -627,8 +631,8 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
     const int k = (kg * T + t) * kTK + 8 * xp;
     const uint32_t xoob = k < a.K ? 0u : kOut;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      g.x[j] = buf_load_half8(rx, (((uint32_t)(xr0 + 32 * j) * a.ldx + k) * 2u) | xoob);
+    for (int j = 0; j < XP; ++j)
+      g.x[j] = buf_load_half8(rx, (((uint32_t)(xr0 + 8 * WN * j) * a.ldx + k) * 2u) | xoob);
   };
   auto wload = [&](WStage& g, int t) {
     const uint32_t chunk = (uint32_t)((kg * T + t) * (kTK / 32)) + lh;
@@ -641,7 +645,7 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   };
   auto xstore = [&](const XStage& g, int buf, int j) {
     const half8v x = g.x[j];
-    lds[kg][buf][((xr0 + 32 * j) * kTLD + 8 * xp) / 8] = half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
+    lds[kg][buf][((xr0 + 8 * WN * j) * kTLD + 8 * xp) / 8] = half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
   };
 
   float16v acc[4];
@@ -674,7 +678,8 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
       const half8v bop = half8v{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) acc[mi] = mfma32x32x16(af[c][mi], bop, acc[mi]);
-      xstore(xn, buf ^ 1, ks);
+#pragma unroll
+      for (int j = 0; j < XP / 4; ++j) xstore(xn, buf ^ 1, (XP / 4) * ks + j);
     }
   };
 
@@ -685,7 +690,7 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   xload(x1, 1);
   wload(w1, 1);
 #pragma unroll
-  for (int j = 0; j < 4; ++j) xstore(x0, 0, j);
+  for (int j = 0; j < XP; ++j) xstore(x0, 0, j);
   xload(x0, 2);
   lds_barrier();
   // Step t: W stage t&1, X buffer t&1; X stage (t+1)&1 stored into buffer
@@ -707,7 +712,7 @@ __global__ __launch_bounds__(256 * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   // Sum the groups' partial tiles into group 0, one group at a time in group
   // order.  The loop's last barrier ordered every LDS read before this.
   if constexpr (kTKG > 1) {
-    static_assert(sizeof(lds) >= (size_t)4 * 64 * 64 * sizeof(float), "reduction buffer");
+    static_assert(sizeof(lds) >= (size_t)WN * 64 * 64 * sizeof(float), "reduction buffer");
     float* red = reinterpret_cast<float*>(lds) + (size_t)wave * 64 * 64 + lane;
 #pragma unroll
     for (int g = 1; g < kTKG; ++g) {
@@ -1137,10 +1142,10 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
     // (qmatmul_skinny.hip).
     return launch_w4a16_skinny_lds(a, s);
   }
-  // The split-K skinny kernel up to M = 32; from M = 40 the 128 x 64 kernel
-  // below is faster (K = 4096, N = 11008, skinny / 128 x 64: M = 32 28.5 /
-  // 33.0 us, M = 40 36.4 / 33.3, M = 64 40.5 / 33.9).
-  // NESO_AMD_W4_SKINNY_MAX_M (at most 64) overrides.
+  // The split-K skinny kernel up to M = 32; above it the tile GEMM below is
+  // faster (K = 4096, N = 11008, skinny / tile GEMM with 128 x 64 tiles:
+  // M = 24 25.7 / 28.0 us, M = 32 28.4 / 28.2, M = 40 33.9 / 28.7, M = 64
+  // 40.5 / 29.5).  NESO_AMD_W4_SKINNY_MAX_M (at most 64) overrides.
   const char* skinny_env = getenv("NESO_AMD_W4_SKINNY_MAX_M");
   const int skinny_max_m = skinny_env ? atoi(skinny_env) : 32;
   if (a.M <= skinny_max_m && a.M <= 64 && skinny_fits) {
@@ -1167,30 +1172,46 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
 #ifndef NESO_GEMM_BN
 #define NESO_GEMM_BN 64
 #endif
-  // Tile GEMM: 128 x 128 tiles; its buffer offsets (one tile's X rows, W
-  // rows and scales) must stay below 2^31 bytes.
+  // Tile GEMM: 128-row tiles; its buffer offsets (one tile's X rows, W rows
+  // and scales) must stay below 2^31 bytes.
   const bool tile_fits = (int64_t)kTT * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
                          (int64_t)kTT * a.K / 2 < ((int64_t)1 << 31);
+  // Measured at K = 4096, N = 11008 (and K = 11008, N = 4096):
+  // * M >= 129: 128 x 128 tiles (WN = 4 waves per K-group), two K-groups
+  //   while the tiles fit on the CUs (one workgroup each), one K-group and
+  //   two workgroups per CU beyond (M = 144 39.2 us against 54.6 for the
+  //   128 x 64 kernel).
+  // * M <= 128: 128 x 64 tiles (WN = 2), four K-groups while the tiles fit
+  //   on the CUs, two K-groups (two workgroups per CU) beyond; against the
+  //   128 x 64 kernel: M = 40 28.7 / 33.9 us, M = 64 29.5 / 34.2, M = 128
+  //   32.7 / 35.3, K = 11008 N = 4096 M = 64 68.6 / 80.1, N = 32768 M = 64
+  //   (two K-groups) 59.9 / 66.8.
+  // NESO_AMD_W4_TILE_GEMM = 0 turns the tile GEMM off (128 x 64 kernel),
+  // 1 / 2 forces 128 x 128 tiles with one / two K-groups, 3 / 4 forces
+  // 128 x 64 tiles with two / four K-groups; NESO_AMD_W4_WIDE_TILE_MIN_M
+  // moves the 128 / 129 boundary.
   const char* tile_env = getenv("NESO_AMD_W4_TILE_GEMM");
   const int tile_mode = tile_env ? atoi(tile_env) : -1;
-  // Measured at K = 4096, N = 11008: the tile GEMM wins above M = 128 (two
-  // K-groups while the tiles fit on the CUs, one workgroup each; one K-group,
-  // two workgroups per CU, beyond: M = 144 39.2 against 54.6 us); up to
-  // M = 128 its 86 tiles leave most CUs idle and the 128 x 64 kernel below
-  // is faster (M = 128 34.7 against 37.1 us).
-  // NESO_AMD_W4_TILE_GEMM = 0 / 1 / 2 forces off / one / two K-groups, and
-  // NESO_AMD_W4_TILE_MIN_M moves the threshold.
-  const int tiles = ((a.M + kTT - 1) / kTT) * ((a.N + kTT - 1) / kTT);
-  const char* tile_min_env = getenv("NESO_AMD_W4_TILE_MIN_M");
-  const int tile_min_m = tile_min_env ? atoi(tile_min_env) : 129;
-  const int kgroups = tile_mode >= 0 ? tile_mode
-                      : a.M < tile_min_m ? 0
-                                     : (tiles <= device_cu_count() ? 2 : 1);
-  if (kgroups && tile_fits) {
-    return kgroups == 2 ? launch<&w4a16_tile_gemm_kernel<2>>(
-        ktag("w4a16_tile_gemm_kernel", 2), dim3(tiles), dim3(512), s, a)
-                        : launch<&w4a16_tile_gemm_kernel<1>>(
-                            ktag("w4a16_tile_gemm_kernel", 1), dim3(tiles), dim3(256), s, a);
+  const char* wide_env = getenv("NESO_AMD_W4_WIDE_TILE_MIN_M");
+  const int wide_min_m = wide_env ? atoi(wide_env) : 129;
+  const int mtiles = (a.M + kTT - 1) / kTT;
+  const int tiles128 = mtiles * ((a.N + 127) / 128), tiles64 = mtiles * ((a.N + 63) / 64);
+  const int cus = device_cu_count();
+  const int mode = tile_mode >= 0    ? tile_mode
+                   : a.M >= wide_min_m ? (tiles128 <= cus ? 2 : 1)
+                                       : (tiles64 <= cus ? 4 : 3);
+  if (tile_fits) {
+    switch (mode) {
+      case 1: return launch<&w4a16_tile_gemm_kernel<1, 4>>(ktag("w4a16_tile_gemm_kernel", 1, 4), dim3(tiles128),
+                                                            dim3(256), s, a);
+      case 2: return launch<&w4a16_tile_gemm_kernel<2, 4>>(ktag("w4a16_tile_gemm_kernel", 2, 4), dim3(tiles128),
+                                                            dim3(512), s, a);
+      case 3: return launch<&w4a16_tile_gemm_kernel<2, 2>>(ktag("w4a16_tile_gemm_kernel", 2, 2), dim3(tiles64),
+                                                            dim3(256), s, a);
+      case 4: return launch<&w4a16_tile_gemm_kernel<4, 2>>(ktag("w4a16_tile_gemm_kernel", 4, 2), dim3(tiles64),
+                                                            dim3(512), s, a);
+      default: break;
+    }
   }
   constexpr int WM = 2, WN = NESO_GEMM_WN, BN = NESO_GEMM_BN;
   if ((int64_t)kGBM * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&

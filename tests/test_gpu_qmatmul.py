@@ -118,22 +118,25 @@ def test_small_m_both_regimes(gpu, monkeypatch, gemv_max_m, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
-@pytest.mark.parametrize("env,m,kernel", [
-    ({}, 32, "w4a16_skinny_kernel"),
-    ({}, 33, "w4a16_gemm_kernel"),
-    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 48, "w4a16_skinny_kernel"),
-    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 64, "w4a16_skinny_kernel"),
-    ({}, 64, "w4a16_gemm_kernel"),
-    ({}, 128, "w4a16_gemm_kernel"),
-    ({}, 129, "w4a16_tile_gemm_kernel"),
-    ({"NESO_AMD_W4_TILE_MIN_M": "192"}, 160, "w4a16_gemm_kernel"),
-    ({}, 160, "w4a16_tile_gemm_kernel"),
+@pytest.mark.parametrize("env,m,kernel,targs", [
+    ({}, 32, "w4a16_skinny_kernel", None),
+    ({}, 33, "w4a16_tile_gemm_kernel", [4, 2]),
+    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 48, "w4a16_skinny_kernel", None),
+    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 64, "w4a16_skinny_kernel", None),
+    ({}, 64, "w4a16_tile_gemm_kernel", [4, 2]),
+    ({"NESO_AMD_W4_TILE_GEMM": "0"}, 64, "w4a16_gemm_kernel", None),
+    ({"NESO_AMD_W4_TILE_GEMM": "3"}, 64, "w4a16_tile_gemm_kernel", [2, 2]),
+    ({}, 128, "w4a16_tile_gemm_kernel", [4, 2]),
+    ({}, 129, "w4a16_tile_gemm_kernel", [2, 4]),
+    ({"NESO_AMD_W4_WIDE_TILE_MIN_M": "192"}, 160, "w4a16_tile_gemm_kernel", [4, 2]),
+    ({}, 160, "w4a16_tile_gemm_kernel", [2, 4]),
 ])
 @pytest.mark.parametrize("n,k", [(300, 4096), (1000, 2080)])
-def test_route_thresholds(gpu, monkeypatch, env, m, kernel, n, k):
-    """Both kernels on each side of the skinny / 128 x 64 / tile GEMM
-    thresholds (M = 32 | 33 and 128 | 129 by default, moved by the
-    NESO_AMD_W4_SKINNY_MAX_M and NESO_AMD_W4_TILE_MIN_M overrides)."""
+def test_route_thresholds(gpu, monkeypatch, env, m, kernel, targs, n, k):
+    """The kernels on each side of the skinny / tile GEMM threshold (M = 32 |
+    33) and of the tile GEMM's 64- / 128-column tiles (M = 128 | 129), moved
+    by the NESO_AMD_W4_SKINNY_MAX_M and NESO_AMD_W4_WIDE_TILE_MIN_M
+    overrides, and the 128 x 64 kernel with the tile GEMM turned off."""
     for key, val in env.items():
         monkeypatch.setenv(key, val)
     x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n + k)
@@ -141,6 +144,8 @@ def test_route_thresholds(gpu, monkeypatch, env, m, kernel, n, k):
     xd, wd, sd = x.to(DEV), torch.as_tensor(words).to(DEV), scales.to(DEV)
     plan = neso_amd.launch_plan("w4a16_matmul", xd, wd, sd, xd, m, n, k, k, n, 32, 8)
     assert [p["device_kernel"] for p in plan] == [kernel], plan
+    if targs is not None:
+        assert plan[0]["template_args"] == targs, plan
     y = gpu_w4(x, words, scales)
     ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
@@ -208,10 +213,11 @@ def test_outlier_activations(gpu, amp, at_zero, m):
     assert (np.abs(y - ref) <= half_ulp + fold).all(), np.abs(y - ref).max()
 
 
-@pytest.mark.parametrize("m,tile", [(3, None), (48, None), (200, None), (300, "1"), (300, "2")])
+@pytest.mark.parametrize("m,tile", [(3, None), (48, None), (48, "0"), (200, None), (300, "1"), (300, "2"),
+                                    (300, "3"), (300, "4")])
 def test_strided_output(gpu, monkeypatch, m, tile):
-    """Row strides of X and Y wider than K and N on every regime (GEMV or
-    skinny, 128 x 64, tile GEMM with one and two K-groups): the padding
+    """Row strides of X and Y wider than K and N on every regime (GEMV, the
+    128 x 64 kernel, the tile GEMM in each of its forms): the padding
     columns of Y keep their contents."""
     if tile:
         monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", tile)
@@ -323,13 +329,14 @@ def test_w8a16_large_tiles(gpu, scaled, m, n, k):
     assert Q.rel_err(c.cpu().numpy(), ref) < 1e-4
 
 
-@pytest.mark.parametrize("kgroups", ["1", "2"])
+@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4"])
 @pytest.mark.parametrize("m,n,k", [(128, 11008, 4096), (200, 300, 4096), (256, 1000, 4128),
                                    (300, 129, 96), (640, 256, 1024)])
 def test_tile_gemm(gpu, monkeypatch, kgroups, m, n, k):
-    """The dequantise-once tile GEMM with one and two K-groups: ragged M and N
-    tiles, K not a multiple of its 64-code step, and a K shorter than one
-    step per group."""
+    """The tile GEMM in its four forms (128-column tiles with one or two
+    K-groups, 64-column tiles with two or four): ragged M and N tiles, K not
+    a multiple of its 64-code step, and a K shorter than one step per
+    group."""
     monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
     x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n + k)
     words = Q.pack_int4(codes.numpy())
@@ -338,7 +345,7 @@ def test_tile_gemm(gpu, monkeypatch, kgroups, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
-@pytest.mark.parametrize("kgroups", ["1", "2"])
+@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4"])
 @pytest.mark.parametrize("group,zero", [(64, 8), (128, 7), (32, 0), (4096, 15)])
 def test_tile_gemm_groups(gpu, monkeypatch, kgroups, group, zero):
     monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
