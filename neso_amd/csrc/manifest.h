@@ -1051,7 +1051,7 @@ constexpr char kManifest[] = R"JSON({
       "WV",
       "G32"
      ],
-     "when": "M <= 32 (NESO_AMD_W4_SKINNY_MAX_M overrides, at most 64) outside the cases above",
+     "when": "M <= 16 outside the case above, and 17 <= M <= 32 where the tile GEMM's 32 x 64 grid would fill less than half the CUs (NESO_AMD_W4_SKINNY_MAX_M forces it up to that M, at most 64)",
      "threadgroup_size": "64 * WV",
      "num_warps": "WV",
      "grid": [
@@ -1069,18 +1069,19 @@ constexpr char kManifest[] = R"JSON({
      "source": "neso_amd/csrc/qmatmul.hip",
      "template_params": [
       "KG",
-      "WN"
+      "WN",
+      "MI"
      ],
-     "when": "M > 32: 128 x 32 WN tiles, each wave a 128 x 32 column strip with its weights dequantised once into MFMA registers and X through LDS, KG K-groups of WN waves per workgroup; M >= 129 (NESO_AMD_W4_WIDE_TILE_MIN_M overrides): WN = 4, KG = 2 while the tiles fit on the CUs, else 1; M <= 128: WN = 2, KG = 4 while the tiles fit on the CUs, else 2",
+     "when": "M > 16: 32 MI x 32 WN tiles, each wave a 32 MI x 32 column strip with its weights dequantised once into MFMA registers and X through LDS, KG K-groups of WN waves per workgroup; M >= 129 (NESO_AMD_W4_WIDE_TILE_MIN_M overrides): WN = 4, MI = 4, KG = 2 while the tiles fit on the CUs, else 1; 65 <= M <= 128: WN = 2, MI = 4, KG = 4 while the tiles fit on the CUs, else 2; 33 <= M <= 64: WN = 2, MI = 2, KG = 4; 17 <= M <= 32: WN = 2, MI = 1, KG = 4 when 2 * cdiv(M, 32) * cdiv(N, 64) >= cus",
      "threadgroup_size": "64 * WN * KG",
      "num_warps": "WN * KG",
      "grid": [
-      "cdiv(M, 128) * cdiv(N, 32 * WN)",
+      "cdiv(M, 32 * MI) * cdiv(N, 32 * WN)",
       "1",
       "1"
      ],
      "constants": {
-      "block_m": "128",
+      "block_m": "32 * MI",
       "block_n": "32 * WN",
       "block_k": "64"
      }

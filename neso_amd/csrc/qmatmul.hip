@@ -584,25 +584,31 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
 // step's MFMAs.  One barrier per step.
 constexpr int kTT = 128, kTK = 64, kTLD = kTK + 8;
 
-template <int kTKG, int WN = 4>  // K-groups per workgroup, waves (32-column strips) per group
+// K-groups per workgroup, waves (32-column strips) per group, 32-row MFMA
+// tiles per wave (tile rows 32 MI).
+template <int kTKG, int WN = 4, int MI = 4>
 __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args a) {
   static_assert(WN == 1 || WN == 2 || WN == 4, "waves per group");
+  static_assert(MI == 1 || MI == 2 || MI == 4, "32-row tiles per wave");
   constexpr uint32_t kOut = 0x80000000u;  // buffer offset past any extent: loads return 0
-  constexpr int kBuf = kTT * kTLD / 8;    // half8v per LDS tile
+  constexpr int TM = 32 * MI;             // tile rows
+  constexpr int kBuf = TM * kTLD / 8;     // half8v per LDS tile
   constexpr int GT = 64 * WN;             // threads per group
   constexpr int TN = 32 * WN;             // tile columns
-  constexpr int XP = 16 / WN;             // X pieces per thread and step
+  constexpr int XP = 4 * MI / WN;         // X pieces per thread and step
+  constexpr int XPK = (XP + 3) / 4;       // X pieces stored per k-slice of a step
+  static_assert(XP >= 1 && XP * GT == TM * 8, "X pieces");
   __shared__ half8v lds[kTKG][2][kBuf];   // [group][buffer] X tile
   const int tid = threadIdx.x % GT, lane = tid & 63;
   const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x / GT);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 31, lh = lane >> 5;
-  const int mtiles = (a.M + kTT - 1) / kTT;
+  const int mtiles = (a.M + TM - 1) / TM;
   const int ntiles = (a.N + TN - 1) / TN;
   const int id = (int)xcd_swizzle(blockIdx.x, (uint32_t)(mtiles * ntiles));
-  const int m0 = (id % mtiles) * kTT, n0 = (id / mtiles) * TN;
+  const int m0 = (id % mtiles) * TM, n0 = (id / mtiles) * TN;
   const int KW = a.K >> 3, SG = a.K / a.group;
-  const int mrows = __builtin_amdgcn_readfirstlane(min(kTT, a.M - m0));
+  const int mrows = __builtin_amdgcn_readfirstlane(min(TM, a.M - m0));
   const int nrows = __builtin_amdgcn_readfirstlane(min(TN, a.N - n0));
   const rsrc_t rx = make_rsrc(a.X + (int64_t)m0 * a.ldx, (uint32_t)(((int64_t)(mrows - 1) * a.ldx + a.K) * 2));
   const rsrc_t rw = make_rsrc(a.W + (int64_t)n0 * KW, (uint32_t)nrows * KW * 4u);
@@ -648,9 +654,9 @@ __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args 
     lds[kg][buf][((xr0 + 8 * WN * j) * kTLD + 8 * xp) / 8] = half8v{x[0], x[4], x[1], x[5], x[2], x[6], x[3], x[7]};
   };
 
-  float16v acc[4];
+  float16v acc[MI];
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi) acc[mi] = float16v{};
+  for (int mi = 0; mi < MI; ++mi) acc[mi] = float16v{};
 
   // One step: X from LDS buffer buf, W from registers ws; X stage xn (the
   // next step) stored into buffer buf ^ 1 among the MFMAs.  After the last
@@ -662,24 +668,25 @@ __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args 
     const half2v s1 = {ws.s, ws.s};
     const half_t s16v = ws.s * (half_t)0.0625f;
     const half2v s16 = {s16v, s16v};
-    half8v af[2][4];
+    half8v af[2][MI];
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) af[0][mi] = afrag(mi, 0);
+    for (int mi = 0; mi < MI; ++mi) af[0][mi] = afrag(mi, 0);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int c = ks & 1;
       if (ks + 1 < 4) {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi) af[c ^ 1][mi] = afrag(mi, ks + 1);
+        for (int mi = 0; mi < MI; ++mi) af[c ^ 1][mi] = afrag(mi, ks + 1);
       }
       half2v r[4];
       unpack_word_x16(ws.w[ks], nib, zp, r);
       const half2v d0 = r[0] * s1, d1 = r[1] * s16, d2 = r[2] * s1, d3 = r[3] * s16;
       const half8v bop = half8v{d0[0], d0[1], d1[0], d1[1], d2[0], d2[1], d3[0], d3[1]};
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) acc[mi] = mfma32x32x16(af[c][mi], bop, acc[mi]);
+      for (int mi = 0; mi < MI; ++mi) acc[mi] = mfma32x32x16(af[c][mi], bop, acc[mi]);
 #pragma unroll
-      for (int j = 0; j < XP / 4; ++j) xstore(xn, buf ^ 1, (XP / 4) * ks + j);
+      for (int j = 0; j < XPK; ++j)
+        if (XPK * ks + j < XP) xstore(xn, buf ^ 1, XPK * ks + j);
     }
   };
 
@@ -712,21 +719,21 @@ __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args 
   // Sum the groups' partial tiles into group 0, one group at a time in group
   // order.  The loop's last barrier ordered every LDS read before this.
   if constexpr (kTKG > 1) {
-    static_assert(sizeof(lds) >= (size_t)WN * 64 * 64 * sizeof(float), "reduction buffer");
-    float* red = reinterpret_cast<float*>(lds) + (size_t)wave * 64 * 64 + lane;
+    static_assert(sizeof(lds) >= (size_t)WN * MI * 16 * 64 * sizeof(float), "reduction buffer");
+    float* red = reinterpret_cast<float*>(lds) + (size_t)wave * MI * 16 * 64 + lane;
 #pragma unroll
     for (int g = 1; g < kTKG; ++g) {
       if (g > 1) lds_barrier();
       if (kg == g) {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
+        for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
           for (int r = 0; r < 16; ++r) red[(mi * 16 + r) * 64] = acc[mi][r];
       }
       lds_barrier();
       if (kg == 0) {
 #pragma unroll
-        for (int mi = 0; mi < 4; ++mi)
+        for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[mi][r] += red[(mi * 16 + r) * 64];
       }
@@ -742,7 +749,7 @@ __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args 
   const int nl = 32 * wave + li;
   const uint32_t noob = nl < nrows ? 0u : kOut;
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int ml = 32 * mi + 8 * (r >> 2) + 4 * lh + (r & 3);
@@ -1137,18 +1144,58 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
   // stay below 2^31 bytes (the out-of-range marker).
   const bool skinny_fits = (int64_t)32 * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
                            (int64_t)32 * a.K / 2 < ((int64_t)1 << 31);
-  if (a.M <= 16 && a.group == 32 && a.K % 128 == 0 && a.K <= w4a16_skinny_lds_max_k()) {
+  // Tile GEMM: its buffer offsets (one tile's X rows, W rows and scales)
+  // must stay below 2^31 bytes.
+  const bool tile_fits = (int64_t)kTT * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
+                         (int64_t)kTT * a.K / 2 < ((int64_t)1 << 31);
+  // Its form (K = 4096, N = 11008 unless stated; against the kernels it
+  // replaced):
+  // * M >= 129: 128 x 128 tiles (WN = 4 waves per K-group), two K-groups
+  //   while the tiles fit on the CUs (one workgroup each), one K-group and
+  //   two workgroups per CU beyond (M = 144 39.2 us against 54.6 for the
+  //   128 x 64 kernel).
+  // * 65 <= M <= 128: 128 x 64 tiles (WN = 2), four K-groups while the tiles
+  //   fit on the CUs, two beyond (M = 96 30.9 us, 128 31.9, against 34.2
+  //   and 35.3 for the 128 x 64 kernel; N = 32768 M = 64 59.9 against 66.8
+  //   with two K-groups).
+  // * 33 <= M <= 64: 64 x 64 tiles (MI = 2), four K-groups (M = 40 20.7,
+  //   M = 64 22.1 us against 33.9 and 34.2; K = 11008 N = 4096 M = 64 53.0
+  //   against 76.7).
+  // * 17 <= M <= 32: 32 x 64 tiles (MI = 1), four K-groups, when the grid
+  //   fills at least half the CUs (M = 17 16.8, M = 32 17.3 us against 22.8
+  //   and 28.1 for the split-K skinny kernel); on smaller grids the skinny
+  //   kernel stays (K = 11008 N = 4096 M = 32: 39.1 against 42.3).
+  // NESO_AMD_W4_TILE_GEMM = 0 turns the tile GEMM off; 1 / 2: 128 x 128
+  // tiles with one / two K-groups; 3 / 4: 128 x 64 with two / four; 5:
+  // 64 x 64 with four; 6: 32 x 64 with four.  NESO_AMD_W4_WIDE_TILE_MIN_M
+  // moves the 128 / 129 boundary.
+  const char* tile_env = getenv("NESO_AMD_W4_TILE_GEMM");
+  const int tile_mode = tile_env ? atoi(tile_env) : -1;
+  const char* wide_env = getenv("NESO_AMD_W4_WIDE_TILE_MIN_M");
+  const int wide_min_m = wide_env ? atoi(wide_env) : 129;
+  const int cus = device_cu_count();
+  auto tiles_of = [&](int tm, int tn) { return ((a.M + tm - 1) / tm) * ((a.N + tn - 1) / tn); };
+  const int mode = tile_mode >= 0      ? tile_mode
+                   : a.M >= wide_min_m ? (tiles_of(128, 128) <= cus ? 2 : 1)
+                   : a.M > 64          ? (tiles_of(128, 64) <= cus ? 4 : 3)
+                   : a.M > 32          ? 5
+                                       : 6;
+
+  // The skinny kernels: X in LDS up to M = 16 (group 32, K <= 4096), the
+  // split-K skinny kernel otherwise up to M = 16, and up to M = 32 where
+  // the tile GEMM's grid would fill less than half the CUs.
+  // NESO_AMD_W4_SKINNY_MAX_M (at most 64) forces them up to that M.
+  const char* skinny_env = getenv("NESO_AMD_W4_SKINNY_MAX_M");
+  const int skinny_max_m = skinny_env ? atoi(skinny_env) : 32;
+  const bool skinny_default =
+      a.M <= 16 || !(tile_fits && (tile_mode < 0 || tile_mode == 6) && 2 * tiles_of(32, 64) >= cus);
+  if (a.M <= 16 && a.M <= skinny_max_m && a.group == 32 && a.K % 128 == 0 &&
+      a.K <= w4a16_skinny_lds_max_k()) {
     // X in LDS, one persistent workgroup per CU, 8 waves splitting K
     // (qmatmul_skinny.hip).
     return launch_w4a16_skinny_lds(a, s);
   }
-  // The split-K skinny kernel up to M = 32; above it the tile GEMM below is
-  // faster (K = 4096, N = 11008, skinny / tile GEMM with 128 x 64 tiles:
-  // M = 24 25.7 / 28.0 us, M = 32 28.4 / 28.2, M = 40 33.9 / 28.7, M = 64
-  // 40.5 / 29.5).  NESO_AMD_W4_SKINNY_MAX_M (at most 64) overrides.
-  const char* skinny_env = getenv("NESO_AMD_W4_SKINNY_MAX_M");
-  const int skinny_max_m = skinny_env ? atoi(skinny_env) : 32;
-  if (a.M <= skinny_max_m && a.M <= 64 && skinny_fits) {
+  if (a.M <= skinny_max_m && a.M <= 64 && skinny_fits && (skinny_env || skinny_default)) {
     // One 8-byte load fetches the scales of a chunk quad when every chunk
     // has its own scale and rows hold whole quads (8-byte aligned).
     const bool g32 = a.group == 32 && a.K % 128 == 0;
@@ -1172,44 +1219,20 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
 #ifndef NESO_GEMM_BN
 #define NESO_GEMM_BN 64
 #endif
-  // Tile GEMM: 128-row tiles; its buffer offsets (one tile's X rows, W rows
-  // and scales) must stay below 2^31 bytes.
-  const bool tile_fits = (int64_t)kTT * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
-                         (int64_t)kTT * a.K / 2 < ((int64_t)1 << 31);
-  // Measured at K = 4096, N = 11008 (and K = 11008, N = 4096):
-  // * M >= 129: 128 x 128 tiles (WN = 4 waves per K-group), two K-groups
-  //   while the tiles fit on the CUs (one workgroup each), one K-group and
-  //   two workgroups per CU beyond (M = 144 39.2 us against 54.6 for the
-  //   128 x 64 kernel).
-  // * M <= 128: 128 x 64 tiles (WN = 2), four K-groups while the tiles fit
-  //   on the CUs, two K-groups (two workgroups per CU) beyond; against the
-  //   128 x 64 kernel: M = 40 28.7 / 33.9 us, M = 64 29.5 / 34.2, M = 128
-  //   32.7 / 35.3, K = 11008 N = 4096 M = 64 68.6 / 80.1, N = 32768 M = 64
-  //   (two K-groups) 59.9 / 66.8.
-  // NESO_AMD_W4_TILE_GEMM = 0 turns the tile GEMM off (128 x 64 kernel),
-  // 1 / 2 forces 128 x 128 tiles with one / two K-groups, 3 / 4 forces
-  // 128 x 64 tiles with two / four K-groups; NESO_AMD_W4_WIDE_TILE_MIN_M
-  // moves the 128 / 129 boundary.
-  const char* tile_env = getenv("NESO_AMD_W4_TILE_GEMM");
-  const int tile_mode = tile_env ? atoi(tile_env) : -1;
-  const char* wide_env = getenv("NESO_AMD_W4_WIDE_TILE_MIN_M");
-  const int wide_min_m = wide_env ? atoi(wide_env) : 129;
-  const int mtiles = (a.M + kTT - 1) / kTT;
-  const int tiles128 = mtiles * ((a.N + 127) / 128), tiles64 = mtiles * ((a.N + 63) / 64);
-  const int cus = device_cu_count();
-  const int mode = tile_mode >= 0    ? tile_mode
-                   : a.M >= wide_min_m ? (tiles128 <= cus ? 2 : 1)
-                                       : (tiles64 <= cus ? 4 : 3);
   if (tile_fits) {
     switch (mode) {
-      case 1: return launch<&w4a16_tile_gemm_kernel<1, 4>>(ktag("w4a16_tile_gemm_kernel", 1, 4), dim3(tiles128),
-                                                            dim3(256), s, a);
-      case 2: return launch<&w4a16_tile_gemm_kernel<2, 4>>(ktag("w4a16_tile_gemm_kernel", 2, 4), dim3(tiles128),
-                                                            dim3(512), s, a);
-      case 3: return launch<&w4a16_tile_gemm_kernel<2, 2>>(ktag("w4a16_tile_gemm_kernel", 2, 2), dim3(tiles64),
-                                                            dim3(256), s, a);
-      case 4: return launch<&w4a16_tile_gemm_kernel<4, 2>>(ktag("w4a16_tile_gemm_kernel", 4, 2), dim3(tiles64),
-                                                            dim3(512), s, a);
+      case 1: return launch<&w4a16_tile_gemm_kernel<1, 4, 4>>(ktag("w4a16_tile_gemm_kernel", 1, 4, 4),
+                                                               dim3(tiles_of(128, 128)), dim3(256), s, a);
+      case 2: return launch<&w4a16_tile_gemm_kernel<2, 4, 4>>(ktag("w4a16_tile_gemm_kernel", 2, 4, 4),
+                                                               dim3(tiles_of(128, 128)), dim3(512), s, a);
+      case 3: return launch<&w4a16_tile_gemm_kernel<2, 2, 4>>(ktag("w4a16_tile_gemm_kernel", 2, 2, 4),
+                                                               dim3(tiles_of(128, 64)), dim3(256), s, a);
+      case 4: return launch<&w4a16_tile_gemm_kernel<4, 2, 4>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 4),
+                                                               dim3(tiles_of(128, 64)), dim3(512), s, a);
+      case 5: return launch<&w4a16_tile_gemm_kernel<4, 2, 2>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 2),
+                                                               dim3(tiles_of(64, 64)), dim3(512), s, a);
+      case 6: return launch<&w4a16_tile_gemm_kernel<4, 2, 1>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 1),
+                                                               dim3(tiles_of(32, 64)), dim3(512), s, a);
       default: break;
     }
   }

@@ -120,23 +120,29 @@ def test_small_m_both_regimes(gpu, monkeypatch, gemv_max_m, m, n, k):
 
 @pytest.mark.parametrize("env,m,kernel,targs", [
     ({}, 32, "w4a16_skinny_kernel", None),
-    ({}, 33, "w4a16_tile_gemm_kernel", [4, 2]),
+    ({}, 33, "w4a16_tile_gemm_kernel", [4, 2, 2]),
     ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 48, "w4a16_skinny_kernel", None),
     ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 64, "w4a16_skinny_kernel", None),
-    ({}, 64, "w4a16_tile_gemm_kernel", [4, 2]),
+    ({}, 64, "w4a16_tile_gemm_kernel", [4, 2, 2]),
+    ({"NESO_AMD_W4_TILE_GEMM": "6"}, 24, "w4a16_skinny_kernel", None),
     ({"NESO_AMD_W4_TILE_GEMM": "0"}, 64, "w4a16_gemm_kernel", None),
-    ({"NESO_AMD_W4_TILE_GEMM": "3"}, 64, "w4a16_tile_gemm_kernel", [2, 2]),
-    ({}, 128, "w4a16_tile_gemm_kernel", [4, 2]),
-    ({}, 129, "w4a16_tile_gemm_kernel", [2, 4]),
-    ({"NESO_AMD_W4_WIDE_TILE_MIN_M": "192"}, 160, "w4a16_tile_gemm_kernel", [4, 2]),
-    ({}, 160, "w4a16_tile_gemm_kernel", [2, 4]),
+    ({"NESO_AMD_W4_TILE_GEMM": "3"}, 64, "w4a16_tile_gemm_kernel", [2, 2, 4]),
+    ({"NESO_AMD_W4_SKINNY_MAX_M": "16", "NESO_AMD_W4_TILE_GEMM": "6"}, 24, "w4a16_tile_gemm_kernel", [4, 2, 1]),
+    ({}, 96, "w4a16_tile_gemm_kernel", [4, 2, 4]),
+    ({}, 128, "w4a16_tile_gemm_kernel", [4, 2, 4]),
+    ({}, 129, "w4a16_tile_gemm_kernel", [2, 4, 4]),
+    ({"NESO_AMD_W4_WIDE_TILE_MIN_M": "192"}, 160, "w4a16_tile_gemm_kernel", [4, 2, 4]),
+    ({}, 160, "w4a16_tile_gemm_kernel", [2, 4, 4]),
 ])
 @pytest.mark.parametrize("n,k", [(300, 4096), (1000, 2080)])
 def test_route_thresholds(gpu, monkeypatch, env, m, kernel, targs, n, k):
-    """The kernels on each side of the skinny / tile GEMM threshold (M = 32 |
-    33) and of the tile GEMM's 64- / 128-column tiles (M = 128 | 129), moved
-    by the NESO_AMD_W4_SKINNY_MAX_M and NESO_AMD_W4_WIDE_TILE_MIN_M
-    overrides, and the 128 x 64 kernel with the tile GEMM turned off."""
+    """The kernels on each side of the skinny / tile GEMM threshold and of the
+    tile GEMM's tile shapes (32 x 64 up to M = 32 on grids that fill half
+    the CUs, 64 x 64 up to 64, 128 x 64 up to 128, 128 x 128 beyond), moved
+    by the NESO_AMD_W4_SKINNY_MAX_M, NESO_AMD_W4_TILE_GEMM and
+    NESO_AMD_W4_WIDE_TILE_MIN_M overrides, and the 128 x 64 kernel with the
+    tile GEMM turned off.  These N give small grids, so M = 24 stays on the
+    skinny kernel by default (test_small_tile_route covers the other side)."""
     for key, val in env.items():
         monkeypatch.setenv(key, val)
     x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n + k)
@@ -146,6 +152,24 @@ def test_route_thresholds(gpu, monkeypatch, env, m, kernel, targs, n, k):
     assert [p["device_kernel"] for p in plan] == [kernel], plan
     if targs is not None:
         assert plan[0]["template_args"] == targs, plan
+    y = gpu_w4(x, words, scales)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
+    assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("m,targs", [(17, [4, 2, 1]), (32, [4, 2, 1]), (33, [4, 2, 2]), (64, [4, 2, 2]),
+                                    (65, [4, 2, 4])])
+def test_small_tile_route(gpu, m, targs):
+    """N = 11008 gives the 32 x 64 tiles a grid that fills more than half
+    the CUs, so M = 17..32 takes the tile GEMM; 33..64 takes 64 x 64 tiles
+    and 65 up 128 x 64 ones."""
+    n, k = 11008, 256
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m)
+    words = Q.pack_int4(codes.numpy())
+    xd, wd, sd = x.to(DEV), torch.as_tensor(words).to(DEV), scales.to(DEV)
+    yd = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    plan = neso_amd.launch_plan("w4a16_matmul", xd, wd, sd, yd, m, n, k, k, n, 32, 8, cu_count=256)
+    assert [(p["device_kernel"], p["template_args"]) for p in plan] == [("w4a16_tile_gemm_kernel", targs)], plan
     y = gpu_w4(x, words, scales)
     ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
@@ -213,14 +237,15 @@ def test_outlier_activations(gpu, amp, at_zero, m):
     assert (np.abs(y - ref) <= half_ulp + fold).all(), np.abs(y - ref).max()
 
 
-@pytest.mark.parametrize("m,tile", [(3, None), (48, None), (48, "0"), (200, None), (300, "1"), (300, "2"),
-                                    (300, "3"), (300, "4")])
+@pytest.mark.parametrize("m,tile", [(3, None), (24, "6"), (48, None), (48, "0"), (200, None), (300, "1"),
+                                    (300, "2"), (300, "3"), (300, "4"), (300, "5"), (300, "6")])
 def test_strided_output(gpu, monkeypatch, m, tile):
     """Row strides of X and Y wider than K and N on every regime (GEMV, the
     128 x 64 kernel, the tile GEMM in each of its forms): the padding
     columns of Y keep their contents."""
     if tile:
         monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", tile)
+        monkeypatch.setenv("NESO_AMD_W4_SKINNY_MAX_M", "0")
     n, k = 200, 512
     x, codes, scales = I.qmatmul_inputs(m, k, n, seed=9)
     words = torch.from_numpy(Q.pack_int4(codes.numpy())).to(DEV)
@@ -329,14 +354,14 @@ def test_w8a16_large_tiles(gpu, scaled, m, n, k):
     assert Q.rel_err(c.cpu().numpy(), ref) < 1e-4
 
 
-@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4"])
+@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4", "5", "6"])
 @pytest.mark.parametrize("m,n,k", [(128, 11008, 4096), (200, 300, 4096), (256, 1000, 4128),
                                    (300, 129, 96), (640, 256, 1024)])
 def test_tile_gemm(gpu, monkeypatch, kgroups, m, n, k):
-    """The tile GEMM in its four forms (128-column tiles with one or two
-    K-groups, 64-column tiles with two or four): ragged M and N tiles, K not
-    a multiple of its 64-code step, and a K shorter than one step per
-    group."""
+    """The tile GEMM in its six forms (128 x 128 tiles with one or two
+    K-groups, 128 x 64 with two or four, 64 x 64 and 32 x 64 with four):
+    ragged M and N tiles, K not a multiple of its 64-code step, and a K
+    shorter than one step per group."""
     monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
     x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n + k)
     words = Q.pack_int4(codes.numpy())
@@ -345,7 +370,7 @@ def test_tile_gemm(gpu, monkeypatch, kgroups, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
-@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4"])
+@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4", "5", "6"])
 @pytest.mark.parametrize("group,zero", [(64, 8), (128, 7), (32, 0), (4096, 15)])
 def test_tile_gemm_groups(gpu, monkeypatch, kgroups, group, zero):
     monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
