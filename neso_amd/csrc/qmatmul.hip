@@ -556,13 +556,13 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// Large-M regime, tile GEMM (M >= 192).
+// Tile GEMM (M > 16; the launcher picks the tile shape by M).
 //
-// A workgroup computes a 128 (m) x 128 (n) tile of Y with KG K-groups of 4
-// waves; group g takes the contiguous range of K-steps [g T, (g + 1) T) (64
-// codes per step) in its own LDS buffers, and the groups' partial tiles are
-// summed through LDS at the end.  Wave w of a group owns columns
-// 32 w .. 32 w + 31 of the tile for all 128 rows (4 x 1
+// A workgroup computes a 32 MI (m) x 32 WN (n) tile of Y with KG K-groups of
+// WN waves; group g takes the contiguous range of K-steps [g T, (g + 1) T)
+// (64 codes per step) in its own LDS buffers, and the groups' partial tiles
+// are summed through LDS at the end.  Wave w of a group owns columns
+// 32 w .. 32 w + 31 of the tile for all its rows (MI x 1
 // v_mfma_f32_32x32x16_f16 tiles), so no two waves of a group need the same
 // weights and each code is dequantised once per workgroup:
 //   * W: lane (n = l%32, h = l/32) loads word quad h (32 codes, 16 bytes,
@@ -570,18 +570,18 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
 //     (c - z) * s (one fp16 rounding) straight into MFMA B operands: MFMA
 //     ks of the step takes word ks, i.e. codes 32 h + 8 ks + {0,4,1,5,2,6,
 //     3,7}, the order of unpack_word_x16;
-//   * X: the tile (128 x 64 fp16 per step) goes through LDS, each
+//   * X: the tile (32 MI x 64 fp16 per step) goes through LDS, each
 //     8-element group stored in that nibble order, rows padded to 72 halves
 //     (no bank conflicts); thread t loads 16-byte piece t%8 of rows
-//     t/8 + 32 j.  A wave's A fragment for MFMA (mi, ks) is row 32 mi + l%32
-//     at codes 32 h + 8 ks of the step, one ds_read_b128.
-// Per step and wave: 16 MFMAs, 16 fragment reads, 4 dequantised words and
-// 4 X stores.  Only X is stored to LDS; that store stream (LDS writes run at
-// about a third of the read rate on gfx950) was the cost of the earlier
-// form, which dequantised W into LDS too.  LDS is double-buffered per
-// group; X loads run two steps ahead of their store, W loads two steps
-// ahead of their use; the next step's X stores are issued among the current
-// step's MFMAs.  One barrier per step.
+//     t/8 + 8 WN j.  A wave's A fragment for MFMA (mi, ks) is row
+//     32 mi + l%32 at codes 32 h + 8 ks of the step, one ds_read_b128.
+// Per step and wave: 4 MI MFMAs, 4 MI fragment reads, 4 dequantised words
+// and 4 MI / WN X stores.  Only X is stored to LDS; that store stream (LDS
+// writes run at about a third of the read rate on gfx950) was the cost of
+// the earlier form, which dequantised W into LDS too.  LDS is
+// double-buffered per group; X loads run two steps ahead of their store, W
+// loads two steps ahead of their use; the next step's X stores are issued
+// among the current step's MFMAs.  One barrier per step.
 constexpr int kTT = 128, kTK = 64, kTLD = kTK + 8;
 
 // K-groups per workgroup, waves (32-column strips) per group, 32-row MFMA
