@@ -108,6 +108,9 @@ struct W4Args {
   int32_t ldx, ldy;
   int32_t group;
   int32_t zero;
+  // Tile GEMM only, set by launch_w4a16: nonzero syncs each K-group's
+  // waves through an LDS arrival counter instead of the workgroup barrier.
+  int32_t group_sync;
 };
 
 hipError_t launch_w4a16(const W4Args& a, hipStream_t stream);

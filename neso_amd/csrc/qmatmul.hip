@@ -599,6 +599,7 @@ __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args 
   constexpr int XPK = (XP + 3) / 4;       // X pieces stored per k-slice of a step
   static_assert(XP >= 1 && XP * GT == TM * 8, "X pieces");
   __shared__ half8v lds[kTKG][2][kBuf];   // [group][buffer] X tile
+  __shared__ uint32_t arrivals[kTKG];      // per-group arrival counters
   const int tid = threadIdx.x % GT, lane = tid & 63;
   const int kg = __builtin_amdgcn_readfirstlane(threadIdx.x / GT);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -618,8 +619,8 @@ __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args 
   const uint32_t gm = (uint32_t)a.group >> 5;  // 32-code chunks per scale group
   const bool gpow2 = (gm & (gm - 1)) == 0;
   const uint32_t gshift = __builtin_ctz(gm);
-  // Steps per group (every group runs the same count: the barrier is
-  // shared); steps past K read zeros.
+  // Steps per group (every group runs the same count, as the workgroup
+  // barriers require); steps past K read zeros.
   const int T = ((a.K + kTK - 1) / kTK + kTKG - 1) / kTKG;
 
   // X: row tid/8 + 8 WN j, 16-byte piece tid%8 of the step.  W: row
@@ -690,6 +691,32 @@ __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args 
     }
   };
 
+  // The end of a step: every wave of the group has stored its share of the
+  // next X tile and read its last fragment of this one.  Only the group's
+  // waves share those buffers, so with a.group_sync each wave counts
+  // itself in the group's LDS arrival counter and waits for the group's
+  // count (WN per sync), letting the groups drift apart; the two waves
+  // that share a SIMD then overlap one's MFMAs with the other's loads and
+  // stores.  The wait is bounded: it ends after 2^16 polls whatever it
+  // reads (a group's waves are resident together and each adds itself
+  // before it waits, so a real wait ends long before).
+  uint32_t syncs = 0;
+  auto step_sync = [&]() {
+    if (kTKG == 1 || !a.group_sync) {
+      lds_barrier();
+      return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    if (lane == 0) __hip_atomic_fetch_add(&arrivals[kg], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const uint32_t target = (uint32_t)WN * ++syncs;
+    for (int i = 0; i < (1 << 16); ++i) {
+      const uint32_t seen = __builtin_amdgcn_readfirstlane(
+          __hip_atomic_load(&arrivals[kg], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP));
+      if (seen >= target) break;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  };
+
   XStage x0, x1;
   WStage w0, w1;
   xload(x0, 0);
@@ -699,6 +726,7 @@ __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args 
 #pragma unroll
   for (int j = 0; j < XP; ++j) xstore(x0, 0, j);
   xload(x0, 2);
+  if (threadIdx.x < kTKG) arrivals[threadIdx.x] = 0;
   lds_barrier();
   // Step t: W stage t&1, X buffer t&1; X stage (t+1)&1 stored into buffer
   // (t+1)&1 and reloaded with step t+3; W stage t&1 reloaded with step t+2.
@@ -707,18 +735,20 @@ __global__ __launch_bounds__(64 * WN * kTKG) void w4a16_tile_gemm_kernel(W4Args 
     step(0, w0, x1);
     wload(w0, t0 + 2);
     xload(x1, t0 + 3);
-    lds_barrier();
+    step_sync();
     if (t0 + 1 < T) {
       step(1, w1, x0);
       wload(w1, t0 + 3);
       xload(x0, t0 + 4);
-      lds_barrier();
+      step_sync();
     }
   }
 
   // Sum the groups' partial tiles into group 0, one group at a time in group
-  // order.  The loop's last barrier ordered every LDS read before this.
+  // order.  The partials overwrite every group's X buffers: the first
+  // barrier waits for the last group to finish its loop.
   if constexpr (kTKG > 1) {
+    lds_barrier();
     static_assert(sizeof(lds) >= (size_t)WN * MI * 16 * 64 * sizeof(float), "reduction buffer");
     float* red = reinterpret_cast<float*>(lds) + (size_t)wave * MI * 16 * 64 + lane;
 #pragma unroll
@@ -1219,21 +1249,33 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
 #ifndef NESO_GEMM_BN
 #define NESO_GEMM_BN 64
 #endif
-  if (tile_fits) {
+  if (tile_fits && mode >= 1 && mode <= 6) {
+    // Per-group arrival counters instead of workgroup barriers (the
+    // kernel's step_sync) pay on long K-loops and on 128-row tiles, where
+    // each K-group's step is long (K = 4096, N = 11008: M = 96 29.2 ->
+    // 26.4, M = 128 30.2 -> 27.8 us; K = 11008, N = 4096: M = 64 45.7 ->
+    // 41.7, M = 128 73.0 -> 58.8, M = 256 94.4 -> 86.6).  Short loops of
+    // 32- and 64-row tiles lose 2-4% to the counter round trip.
+    // NESO_AMD_W4_TILE_SYNC = 0 / 1 forces barriers / counters.
+    static constexpr int kGroups[7] = {0, 1, 2, 2, 4, 4, 4}, kRowTiles[7] = {0, 4, 4, 4, 4, 2, 1};
+    const int kgroups = kGroups[mode], steps = ((a.K + kTK - 1) / kTK + kgroups - 1) / kgroups;
+    const char* sync_env = getenv("NESO_AMD_W4_TILE_SYNC");
+    W4Args t = a;
+    t.group_sync = kgroups > 1 && (sync_env ? atoi(sync_env) != 0
+                                            : steps >= (kRowTiles[mode] == 4 ? 16 : 32));
     switch (mode) {
       case 1: return launch<&w4a16_tile_gemm_kernel<1, 4, 4>>(ktag("w4a16_tile_gemm_kernel", 1, 4, 4),
-                                                               dim3(tiles_of(128, 128)), dim3(256), s, a);
+                                                               dim3(tiles_of(128, 128)), dim3(256), s, t);
       case 2: return launch<&w4a16_tile_gemm_kernel<2, 4, 4>>(ktag("w4a16_tile_gemm_kernel", 2, 4, 4),
-                                                               dim3(tiles_of(128, 128)), dim3(512), s, a);
+                                                               dim3(tiles_of(128, 128)), dim3(512), s, t);
       case 3: return launch<&w4a16_tile_gemm_kernel<2, 2, 4>>(ktag("w4a16_tile_gemm_kernel", 2, 2, 4),
-                                                               dim3(tiles_of(128, 64)), dim3(256), s, a);
+                                                               dim3(tiles_of(128, 64)), dim3(256), s, t);
       case 4: return launch<&w4a16_tile_gemm_kernel<4, 2, 4>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 4),
-                                                               dim3(tiles_of(128, 64)), dim3(512), s, a);
+                                                               dim3(tiles_of(128, 64)), dim3(512), s, t);
       case 5: return launch<&w4a16_tile_gemm_kernel<4, 2, 2>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 2),
-                                                               dim3(tiles_of(64, 64)), dim3(512), s, a);
-      case 6: return launch<&w4a16_tile_gemm_kernel<4, 2, 1>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 1),
-                                                               dim3(tiles_of(32, 64)), dim3(512), s, a);
-      default: break;
+                                                               dim3(tiles_of(64, 64)), dim3(512), s, t);
+      default: return launch<&w4a16_tile_gemm_kernel<4, 2, 1>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 1),
+                                                                dim3(tiles_of(32, 64)), dim3(512), s, t);
     }
   }
   constexpr int WM = 2, WN = NESO_GEMM_WN, BN = NESO_GEMM_BN;

@@ -354,15 +354,18 @@ def test_w8a16_large_tiles(gpu, scaled, m, n, k):
     assert Q.rel_err(c.cpu().numpy(), ref) < 1e-4
 
 
+@pytest.mark.parametrize("sync", ["0", "1"])
 @pytest.mark.parametrize("kgroups", ["1", "2", "3", "4", "5", "6"])
 @pytest.mark.parametrize("m,n,k", [(128, 11008, 4096), (200, 300, 4096), (256, 1000, 4128),
-                                   (300, 129, 96), (640, 256, 1024)])
-def test_tile_gemm(gpu, monkeypatch, kgroups, m, n, k):
+                                   (300, 129, 96), (640, 256, 1024), (96, 200, 11008)])
+def test_tile_gemm(gpu, monkeypatch, kgroups, sync, m, n, k):
     """The tile GEMM in its six forms (128 x 128 tiles with one or two
-    K-groups, 128 x 64 with two or four, 64 x 64 and 32 x 64 with four):
-    ragged M and N tiles, K not a multiple of its 64-code step, and a K
-    shorter than one step per group."""
+    K-groups, 128 x 64 with two or four, 64 x 64 and 32 x 64 with four),
+    each with workgroup barriers and with per-group arrival counters:
+    ragged M and N tiles, K not a multiple of its 64-code step, a K
+    shorter than one step per group, and a long K loop."""
     monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
+    monkeypatch.setenv("NESO_AMD_W4_TILE_SYNC", sync)
     x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n + k)
     words = Q.pack_int4(codes.numpy())
     y = gpu_w4(x, words, scales)
@@ -370,10 +373,28 @@ def test_tile_gemm(gpu, monkeypatch, kgroups, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
+@pytest.mark.parametrize("kgroups", ["2", "3", "4", "5", "6"])
+def test_tile_sync_identical(gpu, monkeypatch, kgroups):
+    """Per-group arrival counters and workgroup barriers order the same
+    LDS traffic, so the two syncs give bit-identical results."""
+    monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
+    x, codes, scales = I.qmatmul_inputs(200, 11008, 300, seed=int(kgroups))
+    words = Q.pack_int4(codes.numpy())
+    ys = []
+    for sync in ("0", "1"):
+        monkeypatch.setenv("NESO_AMD_W4_TILE_SYNC", sync)
+        ys.append(gpu_w4(x, words, scales))
+    assert torch.equal(ys[0], ys[1])
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
+    assert Q.rel_err(ys[1].float().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("sync", ["0", "1"])
 @pytest.mark.parametrize("kgroups", ["1", "2", "3", "4", "5", "6"])
 @pytest.mark.parametrize("group,zero", [(64, 8), (128, 7), (32, 0), (4096, 15)])
-def test_tile_gemm_groups(gpu, monkeypatch, kgroups, group, zero):
+def test_tile_gemm_groups(gpu, monkeypatch, kgroups, sync, group, zero):
     monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
+    monkeypatch.setenv("NESO_AMD_W4_TILE_SYNC", sync)
     x, codes, scales = I.qmatmul_inputs(256, 4096, 300, group=group, seed=group + zero)
     words = Q.pack_int4(codes.numpy())
     y = gpu_w4(x, words, scales, group, zero)
