@@ -1178,36 +1178,46 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
   // must stay below 2^31 bytes.
   const bool tile_fits = (int64_t)kTT * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
                          (int64_t)kTT * a.K / 2 < ((int64_t)1 << 31);
-  // Its form (K = 4096, N = 11008 unless stated; against the kernels it
-  // replaced):
+  // Its form: the finest of 32 x 64, 64 x 64 and 128 x 64 tiles (four
+  // K-groups) whose grid fits on the CUs in one round.  Finer tiles put
+  // more CUs to work; their extra W and X re-reads mostly hit L2 (K = 4096
+  // unless stated: N = 4096 M = 64 15.1 against 18.6 us for 64 x 64, M =
+  // 128 15.3 against 25.5 for 128 x 64, M = 256 20.2 against 25.8 and 35.5
+  // for 128 x 128; K = 11008 N = 4096 M = 128 36.9 against 58.6, M = 256
+  // 49.1 against 87.4).  At N = 11008 this gives 32 x 64 tiles for M <= 32,
+  // 64 x 64 for M <= 64 and 128 x 64 for M <= 128 (M = 32 17.3, M = 64
+  // 22.1, M = 128 31.9 us against 28.1, 34.2 and 35.3 for the kernels they
+  // replaced).  When none fits:
   // * M >= 129: 128 x 128 tiles (WN = 4 waves per K-group), two K-groups
   //   while the tiles fit on the CUs (one workgroup each), one K-group and
   //   two workgroups per CU beyond (M = 144 39.2 us against 54.6 for the
-  //   128 x 64 kernel).
-  // * 65 <= M <= 128: 128 x 64 tiles (WN = 2), four K-groups while the tiles
-  //   fit on the CUs, two beyond (M = 96 30.9 us, 128 31.9, against 34.2
-  //   and 35.3 for the 128 x 64 kernel; N = 32768 M = 64 59.9 against 66.8
-  //   with two K-groups).
-  // * 33 <= M <= 64: 64 x 64 tiles (MI = 2), four K-groups (M = 40 20.7,
-  //   M = 64 22.1 us against 33.9 and 34.2; K = 11008 N = 4096 M = 64 53.0
-  //   against 76.7).
-  // * 17 <= M <= 32: 32 x 64 tiles (MI = 1), four K-groups, when the grid
-  //   fills at least half the CUs (M = 17 16.8, M = 32 17.3 us against 22.8
-  //   and 28.1 for the split-K skinny kernel); on smaller grids the skinny
-  //   kernel stays (K = 11008 N = 4096 M = 32: 39.1 against 42.3).
+  //   128 x 64 kernel; M = 160 36.5 against 49.3 for 128 x 64 tiles in two
+  //   rounds);
+  // * 65 <= M <= 128: 128 x 64 tiles with two K-groups (N = 32768 M = 64
+  //   59.9 against 66.8 with four);
+  // * 33 <= M <= 64: 64 x 64 tiles (N = 32768 M = 64 42.8 against 55.6);
+  // * 17 <= M <= 32: 32 x 64 tiles (N = 32768 M = 32 34.4 against 53.6).
+  // Up to M = 32 the split-K skinny kernel takes grids on which 32 x 64
+  // tiles would fill less than half the CUs (K = 11008 N = 4096 M = 32:
+  // 39.1 against 42.3 us).
   // NESO_AMD_W4_TILE_GEMM = 0 turns the tile GEMM off; 1 / 2: 128 x 128
   // tiles with one / two K-groups; 3 / 4: 128 x 64 with two / four; 5:
   // 64 x 64 with four; 6: 32 x 64 with four.  NESO_AMD_W4_WIDE_TILE_MIN_M
-  // moves the 128 / 129 boundary.
+  // moves the 128 / 129 boundary of the forms taken when no fine tile fits.
   const char* tile_env = getenv("NESO_AMD_W4_TILE_GEMM");
   const int tile_mode = tile_env ? atoi(tile_env) : -1;
   const char* wide_env = getenv("NESO_AMD_W4_WIDE_TILE_MIN_M");
   const int wide_min_m = wide_env ? atoi(wide_env) : 129;
   const int cus = device_cu_count();
   auto tiles_of = [&](int tm, int tn) { return ((a.M + tm - 1) / tm) * ((a.N + tn - 1) / tn); };
+  const int fine = tiles_of(32, 64) <= cus    ? 6
+                   : tiles_of(64, 64) <= cus  ? 5
+                   : tiles_of(128, 64) <= cus ? 4
+                                              : 0;
   const int mode = tile_mode >= 0      ? tile_mode
+                   : fine              ? fine
                    : a.M >= wide_min_m ? (tiles_of(128, 128) <= cus ? 2 : 1)
-                   : a.M > 64          ? (tiles_of(128, 64) <= cus ? 4 : 3)
+                   : a.M > 64          ? 3
                    : a.M > 32          ? 5
                                        : 6;
 

@@ -118,37 +118,48 @@ def test_small_m_both_regimes(gpu, monkeypatch, gemv_max_m, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
-@pytest.mark.parametrize("env,m,kernel,targs", [
-    ({}, 32, "w4a16_skinny_kernel", None),
-    ({}, 33, "w4a16_tile_gemm_kernel", [4, 2, 2]),
-    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 48, "w4a16_skinny_kernel", None),
-    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 64, "w4a16_skinny_kernel", None),
-    ({}, 64, "w4a16_tile_gemm_kernel", [4, 2, 2]),
-    ({"NESO_AMD_W4_TILE_GEMM": "6"}, 24, "w4a16_skinny_kernel", None),
-    ({"NESO_AMD_W4_TILE_GEMM": "0"}, 64, "w4a16_gemm_kernel", None),
-    ({"NESO_AMD_W4_TILE_GEMM": "3"}, 64, "w4a16_tile_gemm_kernel", [2, 2, 4]),
-    ({"NESO_AMD_W4_SKINNY_MAX_M": "16", "NESO_AMD_W4_TILE_GEMM": "6"}, 24, "w4a16_tile_gemm_kernel", [4, 2, 1]),
-    ({}, 96, "w4a16_tile_gemm_kernel", [4, 2, 4]),
-    ({}, 128, "w4a16_tile_gemm_kernel", [4, 2, 4]),
-    ({}, 129, "w4a16_tile_gemm_kernel", [2, 4, 4]),
-    ({"NESO_AMD_W4_WIDE_TILE_MIN_M": "192"}, 160, "w4a16_tile_gemm_kernel", [4, 2, 4]),
-    ({}, 160, "w4a16_tile_gemm_kernel", [2, 4, 4]),
+@pytest.mark.parametrize("env,m,n,kernel,targs", [
+    ({}, 32, 300, "w4a16_skinny_kernel", None),
+    ({}, 33, 11008, "w4a16_tile_gemm_kernel", [4, 2, 2]),
+    ({}, 33, 1000, "w4a16_tile_gemm_kernel", [4, 2, 1]),
+    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 48, 300, "w4a16_skinny_kernel", None),
+    ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 64, 300, "w4a16_skinny_kernel", None),
+    ({}, 64, 11008, "w4a16_tile_gemm_kernel", [4, 2, 2]),
+    ({}, 64, 4096, "w4a16_tile_gemm_kernel", [4, 2, 1]),
+    ({"NESO_AMD_W4_TILE_GEMM": "6"}, 24, 300, "w4a16_skinny_kernel", None),
+    ({"NESO_AMD_W4_TILE_GEMM": "0"}, 64, 300, "w4a16_gemm_kernel", None),
+    ({"NESO_AMD_W4_TILE_GEMM": "3"}, 64, 300, "w4a16_tile_gemm_kernel", [2, 2, 4]),
+    ({"NESO_AMD_W4_SKINNY_MAX_M": "16", "NESO_AMD_W4_TILE_GEMM": "6"}, 24, 300, "w4a16_tile_gemm_kernel", [4, 2, 1]),
+    ({}, 96, 11008, "w4a16_tile_gemm_kernel", [4, 2, 4]),
+    ({}, 128, 11008, "w4a16_tile_gemm_kernel", [4, 2, 4]),
+    ({}, 128, 4096, "w4a16_tile_gemm_kernel", [4, 2, 1]),
+    ({}, 129, 11008, "w4a16_tile_gemm_kernel", [2, 4, 4]),
+    ({}, 256, 4096, "w4a16_tile_gemm_kernel", [4, 2, 2]),
+    ({}, 256, 8192, "w4a16_tile_gemm_kernel", [4, 2, 4]),
+    ({"NESO_AMD_W4_WIDE_TILE_MIN_M": "192"}, 160, 11008, "w4a16_tile_gemm_kernel", [2, 2, 4]),
+    ({}, 160, 11008, "w4a16_tile_gemm_kernel", [2, 4, 4]),
+    ({}, 1024, 4096, "w4a16_tile_gemm_kernel", [2, 4, 4]),
+    ({}, 1200, 4096, "w4a16_tile_gemm_kernel", [1, 4, 4]),
 ])
-@pytest.mark.parametrize("n,k", [(300, 4096), (1000, 2080)])
-def test_route_thresholds(gpu, monkeypatch, env, m, kernel, targs, n, k):
+def test_route_thresholds(gpu, monkeypatch, env, m, n, kernel, targs):
     """The kernels on each side of the skinny / tile GEMM threshold and of the
-    tile GEMM's tile shapes (32 x 64 up to M = 32 on grids that fill half
-    the CUs, 64 x 64 up to 64, 128 x 64 up to 128, 128 x 128 beyond), moved
-    by the NESO_AMD_W4_SKINNY_MAX_M, NESO_AMD_W4_TILE_GEMM and
+    tile GEMM's tile shapes, for a 256-CU part: the finest of 32 x 64,
+    64 x 64 and 128 x 64 tiles whose grid fits on the CUs, else 128 x 128
+    from M = 129 (two K-groups while those tiles fit, one beyond), 128 x 64
+    with two K-groups from M = 65, 64 x 64 from M = 33; the
+    NESO_AMD_W4_SKINNY_MAX_M, NESO_AMD_W4_TILE_GEMM and
     NESO_AMD_W4_WIDE_TILE_MIN_M overrides, and the 128 x 64 kernel with the
-    tile GEMM turned off.  These N give small grids, so M = 24 stays on the
-    skinny kernel by default (test_small_tile_route covers the other side)."""
+    tile GEMM turned off.  N = 300 gives small grids, so M = 24 and 32 stay
+    on the skinny kernel by default (test_small_tile_route covers the other
+    side)."""
     for key, val in env.items():
         monkeypatch.setenv(key, val)
+    k = 4096 if n <= 1000 else 256
     x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n + k)
     words = Q.pack_int4(codes.numpy())
     xd, wd, sd = x.to(DEV), torch.as_tensor(words).to(DEV), scales.to(DEV)
-    plan = neso_amd.launch_plan("w4a16_matmul", xd, wd, sd, xd, m, n, k, k, n, 32, 8)
+    yd = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    plan = neso_amd.launch_plan("w4a16_matmul", xd, wd, sd, yd, m, n, k, k, n, 32, 8, cu_count=256)
     assert [p["device_kernel"] for p in plan] == [kernel], plan
     if targs is not None:
         assert plan[0]["template_args"] == targs, plan
