@@ -1178,13 +1178,14 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
   // must stay below 2^31 bytes.
   const bool tile_fits = (int64_t)kTT * a.ldx * 2 + (int64_t)a.K * 2 < ((int64_t)1 << 31) &&
                          (int64_t)kTT * a.K / 2 < ((int64_t)1 << 31);
-  // Its form: the finest of 32 x 64, 64 x 64 and 128 x 64 tiles (four
-  // K-groups) whose grid fits on the CUs in one round.  Finer tiles put
-  // more CUs to work; their extra W and X re-reads mostly hit L2 (K = 4096
-  // unless stated: N = 4096 M = 64 15.1 against 18.6 us for 64 x 64, M =
-  // 128 15.3 against 25.5 for 128 x 64, M = 256 20.2 against 25.8 and 35.5
-  // for 128 x 128; K = 11008 N = 4096 M = 128 36.9 against 58.6, M = 256
-  // 49.1 against 87.4).  At N = 11008 this gives 32 x 64 tiles for M <= 32,
+  // Its form: the finest of 32 x 32 (eight K-groups of one wave), 32 x 64,
+  // 64 x 64 and 128 x 64 tiles (four K-groups of two waves) whose grid fits
+  // on the CUs in one round.  Finer tiles put more CUs to work; their extra
+  // W and X re-reads mostly hit L2 (K = 4096 unless stated: N = 4096 M = 64
+  // 12.5 against 14.5 us for 32 x 64 and 18.6 for 64 x 64, M = 128 15.3
+  // against 25.5 for 128 x 64, M = 256 20.2 against 25.8 and 35.5 for
+  // 128 x 128; K = 11008 N = 4096 M = 64 26.6 against 33.3, M = 128 36.9
+  // against 58.6, M = 256 49.1 against 87.4).  At N = 11008 this gives 32 x 64 tiles for M <= 32,
   // 64 x 64 for M <= 64 and 128 x 64 for M <= 128 (M = 32 17.3, M = 64
   // 22.1, M = 128 31.9 us against 28.1, 34.2 and 35.3 for the kernels they
   // replaced).  When none fits:
@@ -1197,20 +1198,22 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
   //   59.9 against 66.8 with four);
   // * 33 <= M <= 64: 64 x 64 tiles (N = 32768 M = 64 42.8 against 55.6);
   // * 17 <= M <= 32: 32 x 64 tiles (N = 32768 M = 32 34.4 against 53.6).
-  // Up to M = 32 the split-K skinny kernel takes grids on which 32 x 64
-  // tiles would fill less than half the CUs (K = 11008 N = 4096 M = 32:
-  // 39.1 against 42.3 us).
+  // From M = 17 the tile GEMM is ahead of the split-K skinny kernel on
+  // every grid measured (M = 17 N = 1024 10.8 against 13.0 us, N = 4096
+  // 11.7 against 13.5; M = 32 K = 11008 N = 4096 25.4 against 39.5).
   // NESO_AMD_W4_TILE_GEMM = 0 turns the tile GEMM off; 1 / 2: 128 x 128
   // tiles with one / two K-groups; 3 / 4: 128 x 64 with two / four; 5:
-  // 64 x 64 with four; 6: 32 x 64 with four.  NESO_AMD_W4_WIDE_TILE_MIN_M
-  // moves the 128 / 129 boundary of the forms taken when no fine tile fits.
+  // 64 x 64 with four; 6: 32 x 64 with four; 7: 32 x 32 with eight.
+  // NESO_AMD_W4_WIDE_TILE_MIN_M moves the 128 / 129 boundary of the forms
+  // taken when no fine tile fits.
   const char* tile_env = getenv("NESO_AMD_W4_TILE_GEMM");
   const int tile_mode = tile_env ? atoi(tile_env) : -1;
   const char* wide_env = getenv("NESO_AMD_W4_WIDE_TILE_MIN_M");
   const int wide_min_m = wide_env ? atoi(wide_env) : 129;
   const int cus = device_cu_count();
   auto tiles_of = [&](int tm, int tn) { return ((a.M + tm - 1) / tm) * ((a.N + tn - 1) / tn); };
-  const int fine = tiles_of(32, 64) <= cus    ? 6
+  const int fine = tiles_of(32, 32) <= cus    ? 7
+                   : tiles_of(32, 64) <= cus  ? 6
                    : tiles_of(64, 64) <= cus  ? 5
                    : tiles_of(128, 64) <= cus ? 4
                                               : 0;
@@ -1222,13 +1225,13 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
                                        : 6;
 
   // The skinny kernels: X in LDS up to M = 16 (group 32, K <= 4096), the
-  // split-K skinny kernel otherwise up to M = 16, and up to M = 32 where
-  // the tile GEMM's grid would fill less than half the CUs.
+  // split-K skinny kernel otherwise up to M = 16, and up to M = 32 when the
+  // tile GEMM is off or its offsets would pass 2^31 bytes.
   // NESO_AMD_W4_SKINNY_MAX_M (at most 64) forces them up to that M.
   const char* skinny_env = getenv("NESO_AMD_W4_SKINNY_MAX_M");
   const int skinny_max_m = skinny_env ? atoi(skinny_env) : 32;
   const bool skinny_default =
-      a.M <= 16 || !(tile_fits && (tile_mode < 0 || tile_mode == 6) && 2 * tiles_of(32, 64) >= cus);
+      a.M <= 16 || !tile_fits || tile_mode == 0;
   if (a.M <= 16 && a.M <= skinny_max_m && a.group == 32 && a.K % 128 == 0 &&
       a.K <= w4a16_skinny_lds_max_k()) {
     // X in LDS, one persistent workgroup per CU, 8 waves splitting K
@@ -1259,7 +1262,7 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
 #ifndef NESO_GEMM_BN
 #define NESO_GEMM_BN 64
 #endif
-  if (tile_fits && mode >= 1 && mode <= 6) {
+  if (tile_fits && mode >= 1 && mode <= 7) {
     // Per-group arrival counters instead of workgroup barriers (the
     // kernel's step_sync) pay on long K-loops and on 128-row tiles, where
     // each K-group's step is long (K = 4096, N = 11008: M = 96 29.2 ->
@@ -1267,7 +1270,7 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
     // 41.7, M = 128 73.0 -> 58.8, M = 256 94.4 -> 86.6).  Short loops of
     // 32- and 64-row tiles lose 2-4% to the counter round trip.
     // NESO_AMD_W4_TILE_SYNC = 0 / 1 forces barriers / counters.
-    static constexpr int kGroups[7] = {0, 1, 2, 2, 4, 4, 4}, kRowTiles[7] = {0, 4, 4, 4, 4, 2, 1};
+    static constexpr int kGroups[8] = {0, 1, 2, 2, 4, 4, 4, 8}, kRowTiles[8] = {0, 4, 4, 4, 4, 2, 1, 1};
     const int kgroups = kGroups[mode], steps = ((a.K + kTK - 1) / kTK + kgroups - 1) / kgroups;
     const char* sync_env = getenv("NESO_AMD_W4_TILE_SYNC");
     W4Args t = a;
@@ -1284,8 +1287,10 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
                                                                dim3(tiles_of(128, 64)), dim3(512), s, t);
       case 5: return launch<&w4a16_tile_gemm_kernel<4, 2, 2>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 2),
                                                                dim3(tiles_of(64, 64)), dim3(512), s, t);
-      default: return launch<&w4a16_tile_gemm_kernel<4, 2, 1>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 1),
-                                                                dim3(tiles_of(32, 64)), dim3(512), s, t);
+      case 6: return launch<&w4a16_tile_gemm_kernel<4, 2, 1>>(ktag("w4a16_tile_gemm_kernel", 4, 2, 1),
+                                                               dim3(tiles_of(32, 64)), dim3(512), s, t);
+      default: return launch<&w4a16_tile_gemm_kernel<8, 1, 1>>(ktag("w4a16_tile_gemm_kernel", 8, 1, 1),
+                                                                dim3(tiles_of(32, 32)), dim3(512), s, t);
     }
   }
   constexpr int WM = 2, WN = NESO_GEMM_WN, BN = NESO_GEMM_BN;

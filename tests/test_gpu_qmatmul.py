@@ -119,14 +119,18 @@ def test_small_m_both_regimes(gpu, monkeypatch, gemv_max_m, m, n, k):
 
 
 @pytest.mark.parametrize("env,m,n,kernel,targs", [
-    ({}, 32, 300, "w4a16_skinny_kernel", None),
+    ({}, 32, 300, "w4a16_tile_gemm_kernel", [8, 1, 1]),
+    ({}, 16, 300, "w4a16_skinny_lds_kernel", None),
+    ({"NESO_AMD_W4_TILE_GEMM": "0"}, 24, 300, "w4a16_skinny_kernel", None),
+    ({}, 32, 8192, "w4a16_tile_gemm_kernel", [8, 1, 1]),
+    ({"NESO_AMD_W4_TILE_GEMM": "7"}, 64, 11008, "w4a16_tile_gemm_kernel", [8, 1, 1]),
     ({}, 33, 11008, "w4a16_tile_gemm_kernel", [4, 2, 2]),
-    ({}, 33, 1000, "w4a16_tile_gemm_kernel", [4, 2, 1]),
+    ({}, 33, 1000, "w4a16_tile_gemm_kernel", [8, 1, 1]),
     ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 48, 300, "w4a16_skinny_kernel", None),
     ({"NESO_AMD_W4_SKINNY_MAX_M": "64"}, 64, 300, "w4a16_skinny_kernel", None),
     ({}, 64, 11008, "w4a16_tile_gemm_kernel", [4, 2, 2]),
-    ({}, 64, 4096, "w4a16_tile_gemm_kernel", [4, 2, 1]),
-    ({"NESO_AMD_W4_TILE_GEMM": "6"}, 24, 300, "w4a16_skinny_kernel", None),
+    ({}, 64, 4096, "w4a16_tile_gemm_kernel", [8, 1, 1]),
+    ({"NESO_AMD_W4_TILE_GEMM": "6"}, 24, 300, "w4a16_tile_gemm_kernel", [4, 2, 1]),
     ({"NESO_AMD_W4_TILE_GEMM": "0"}, 64, 300, "w4a16_gemm_kernel", None),
     ({"NESO_AMD_W4_TILE_GEMM": "3"}, 64, 300, "w4a16_tile_gemm_kernel", [2, 2, 4]),
     ({"NESO_AMD_W4_SKINNY_MAX_M": "16", "NESO_AMD_W4_TILE_GEMM": "6"}, 24, 300, "w4a16_tile_gemm_kernel", [4, 2, 1]),
@@ -142,16 +146,14 @@ def test_small_m_both_regimes(gpu, monkeypatch, gemv_max_m, m, n, k):
     ({}, 1200, 4096, "w4a16_tile_gemm_kernel", [1, 4, 4]),
 ])
 def test_route_thresholds(gpu, monkeypatch, env, m, n, kernel, targs):
-    """The kernels on each side of the skinny / tile GEMM threshold and of the
-    tile GEMM's tile shapes, for a 256-CU part: the finest of 32 x 64,
-    64 x 64 and 128 x 64 tiles whose grid fits on the CUs, else 128 x 128
-    from M = 129 (two K-groups while those tiles fit, one beyond), 128 x 64
-    with two K-groups from M = 65, 64 x 64 from M = 33; the
-    NESO_AMD_W4_SKINNY_MAX_M, NESO_AMD_W4_TILE_GEMM and
-    NESO_AMD_W4_WIDE_TILE_MIN_M overrides, and the 128 x 64 kernel with the
-    tile GEMM turned off.  N = 300 gives small grids, so M = 24 and 32 stay
-    on the skinny kernel by default (test_small_tile_route covers the other
-    side)."""
+    """The kernels on each side of the skinny / tile GEMM threshold (M = 16
+    / 17) and of the tile GEMM's tile shapes, for a 256-CU part: the finest
+    of 32 x 32, 32 x 64, 64 x 64 and 128 x 64 tiles whose grid fits on the
+    CUs, else 128 x 128 from M = 129 (two K-groups while those tiles fit,
+    one beyond), 128 x 64 with two K-groups from M = 65, 64 x 64 from
+    M = 33; the NESO_AMD_W4_SKINNY_MAX_M, NESO_AMD_W4_TILE_GEMM and
+    NESO_AMD_W4_WIDE_TILE_MIN_M overrides, and the skinny and 128 x 64
+    kernels with the tile GEMM turned off."""
     for key, val in env.items():
         monkeypatch.setenv(key, val)
     k = 4096 if n <= 1000 else 256
@@ -249,7 +251,7 @@ def test_outlier_activations(gpu, amp, at_zero, m):
 
 
 @pytest.mark.parametrize("m,tile", [(3, None), (24, "6"), (48, None), (48, "0"), (200, None), (300, "1"),
-                                    (300, "2"), (300, "3"), (300, "4"), (300, "5"), (300, "6")])
+                                    (300, "2"), (300, "3"), (300, "4"), (300, "5"), (300, "6"), (300, "7")])
 def test_strided_output(gpu, monkeypatch, m, tile):
     """Row strides of X and Y wider than K and N on every regime (GEMV, the
     128 x 64 kernel, the tile GEMM in each of its forms): the padding
@@ -366,12 +368,13 @@ def test_w8a16_large_tiles(gpu, scaled, m, n, k):
 
 
 @pytest.mark.parametrize("sync", ["0", "1"])
-@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4", "5", "6"])
+@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4", "5", "6", "7"])
 @pytest.mark.parametrize("m,n,k", [(128, 11008, 4096), (200, 300, 4096), (256, 1000, 4128),
                                    (300, 129, 96), (640, 256, 1024), (96, 200, 11008)])
 def test_tile_gemm(gpu, monkeypatch, kgroups, sync, m, n, k):
-    """The tile GEMM in its six forms (128 x 128 tiles with one or two
-    K-groups, 128 x 64 with two or four, 64 x 64 and 32 x 64 with four),
+    """The tile GEMM in its seven forms (128 x 128 tiles with one or two
+    K-groups, 128 x 64 with two or four, 64 x 64 and 32 x 64 with four,
+    32 x 32 with eight),
     each with workgroup barriers and with per-group arrival counters:
     ragged M and N tiles, K not a multiple of its 64-code step, a K
     shorter than one step per group, and a long K loop."""
@@ -384,7 +387,7 @@ def test_tile_gemm(gpu, monkeypatch, kgroups, sync, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
-@pytest.mark.parametrize("kgroups", ["2", "3", "4", "5", "6"])
+@pytest.mark.parametrize("kgroups", ["2", "3", "4", "5", "6", "7"])
 def test_tile_sync_identical(gpu, monkeypatch, kgroups):
     """Per-group arrival counters and workgroup barriers order the same
     LDS traffic, so the two syncs give bit-identical results."""
@@ -401,7 +404,7 @@ def test_tile_sync_identical(gpu, monkeypatch, kgroups):
 
 
 @pytest.mark.parametrize("sync", ["0", "1"])
-@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4", "5", "6"])
+@pytest.mark.parametrize("kgroups", ["1", "2", "3", "4", "5", "6", "7"])
 @pytest.mark.parametrize("group,zero", [(64, 8), (128, 7), (32, 0), (4096, 15)])
 def test_tile_gemm_groups(gpu, monkeypatch, kgroups, sync, group, zero):
     monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", kgroups)
