@@ -387,7 +387,23 @@ def test_tile_gemm(gpu, monkeypatch, kgroups, sync, m, n, k):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
-@pytest.mark.parametrize("kgroups", ["2", "3", "4", "5", "6", "7"])
+def test_tile_one_wave_groups_repeat(gpu, monkeypatch):
+    """The 32 x 32 form's K-groups are one wave each and order their LDS
+    double buffer with a wave-level fence only: five launches on the same
+    inputs (22 steps per group) give identical results, within the
+    oracle's bound."""
+    monkeypatch.setenv("NESO_AMD_W4_TILE_GEMM", "7")
+    x, codes, scales = I.qmatmul_inputs(64, 11008, 1000, seed=7)
+    words = Q.pack_int4(codes.numpy())
+    xd, wd, sd = x.to(DEV), torch.as_tensor(words).to(DEV), scales.to(DEV)
+    ys = [neso_amd.w4a16_linear(xd, wd, sd, group_size=32, zero_point=8) for _ in range(5)]
+    torch.cuda.synchronize()
+    assert all(torch.equal(ys[0], y) for y in ys[1:])
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy())
+    assert Q.rel_err(ys[0].float().cpu().numpy(), ref) <= 2e-3
+
+
+@pytest.mark.parametrize("kgroups", ["2", "3", "4", "5", "6"])
 def test_tile_sync_identical(gpu, monkeypatch, kgroups):
     """Per-group arrival counters and workgroup barriers order the same
     LDS traffic, so the two syncs give bit-identical results."""
