@@ -1236,13 +1236,18 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
                                        : 6;
 
   // The skinny kernels: X in LDS up to M = 16 (group 32, K <= 4096), the
-  // split-K skinny kernel otherwise up to M = 16, and up to M = 32 when the
-  // tile GEMM is off or its offsets would pass 2^31 bytes.
+  // split-K skinny kernel otherwise up to M = 16 (past that K only where
+  // the 32 x 32 tile grid would not fit on the CUs), and up to M = 32 when
+  // the tile GEMM is off or its offsets would pass 2^31 bytes.
   // NESO_AMD_W4_SKINNY_MAX_M (at most 64) forces them up to that M.
   const char* skinny_env = getenv("NESO_AMD_W4_SKINNY_MAX_M");
   const int skinny_max_m = skinny_env ? atoi(skinny_env) : 32;
+  // Up to M = 16 past the X-in-LDS kernel's K the 32 x 32 tile GEMM beats
+  // the split-K skinny kernel when its grid fits (K = 11008 N = 4096:
+  // M = 4 20.8, M = 16 22.1 us against 23.9 and 27.3).
+  const bool tile_ok = tile_fits && tile_mode != 0;
   const bool skinny_default =
-      a.M <= 16 || !tile_fits || tile_mode == 0;
+      a.M <= 16 ? !(tile_ok && a.K > w4a16_skinny_lds_max_k() && tiles_of(32, 32) <= cus) : !tile_ok;
   if (a.M <= 16 && a.M <= skinny_max_m && a.group == 32 && a.K % 128 == 0 &&
       a.K <= w4a16_skinny_lds_max_k()) {
     // X in LDS, one persistent workgroup per CU, 8 waves splitting K

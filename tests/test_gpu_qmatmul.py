@@ -170,6 +170,35 @@ def test_route_thresholds(gpu, monkeypatch, env, m, n, kernel, targs):
     assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
 
 
+@pytest.mark.parametrize("env,m,n,kernel", [
+    ({}, 16, 4096, "w4a16_tile_gemm_kernel"),
+    ({}, 1, 1000, "w4a16_tile_gemm_kernel"),
+    ({}, 3, 1000, "w4a16_tile_gemm_kernel"),
+    ({}, 16, 11008, "w4a16_skinny_kernel"),
+    ({"NESO_AMD_W4_SKINNY_MAX_M": "16"}, 16, 4096, "w4a16_skinny_kernel"),
+    ({"NESO_AMD_W4_TILE_GEMM": "0"}, 8, 1000, "w4a16_skinny_kernel"),
+])
+def test_long_k_small_m_route(gpu, monkeypatch, env, m, n, kernel):
+    """Up to M = 16 with K past the X-in-LDS kernel's limit (and the
+    GEMV's, for M = 1): the 32 x 32 tile GEMM where its grid fits on a
+    256-CU part, the split-K skinny kernel where it does not, when forced,
+    or with the tile GEMM off."""
+    for key, val in env.items():
+        monkeypatch.setenv(key, val)
+    k = 11008
+    x, codes, scales = I.qmatmul_inputs(m, k, n, seed=m + n)
+    words = Q.pack_int4(codes.numpy())
+    xd, wd, sd = x.to(DEV), torch.as_tensor(words).to(DEV), scales.to(DEV)
+    yd = torch.empty(m, n, dtype=torch.float16, device=DEV)
+    plan = neso_amd.launch_plan("w4a16_matmul", xd, wd, sd, yd, m, n, k, k, n, 32, 8, cu_count=256)
+    assert [p["device_kernel"] for p in plan] == [kernel], plan
+    if kernel == "w4a16_tile_gemm_kernel":
+        assert plan[0]["template_args"] == [8, 1, 1], plan
+    y = gpu_w4(x, words, scales)
+    ref = Q.w4a16_matmul(x.numpy(), words, scales.numpy(), dtype=np.float64)
+    assert Q.rel_err(y.float().numpy(), ref) <= 2e-3
+
+
 @pytest.mark.parametrize("m,targs", [(17, [4, 2, 1]), (32, [4, 2, 1]), (33, [4, 2, 2]), (64, [4, 2, 2]),
                                     (65, [4, 2, 4])])
 def test_small_tile_route(gpu, m, targs):
