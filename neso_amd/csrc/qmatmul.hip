@@ -556,7 +556,8 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
 }
 
 // ---------------------------------------------------------------------------
-// Tile GEMM (M > 16; the launcher picks the tile shape by M).
+// Tile GEMM (M > 16, and smaller M past the skinny kernels' K; the
+// launcher picks the finest tile whose grid fits on the CUs).
 //
 // A workgroup computes a 32 MI (m) x 32 WN (n) tile of Y with KG K-groups of
 // WN waves; group g takes the contiguous range of K-steps [g T, (g + 1) T)
@@ -581,7 +582,9 @@ __global__ __launch_bounds__(WM * WN * kWave) void w4a16_gemm_kernel(W4Args a) {
 // the earlier form, which dequantised W into LDS too.  LDS is
 // double-buffered per group; X loads run two steps ahead of their store, W
 // loads two steps ahead of their use; the next step's X stores are issued
-// among the current step's MFMAs.  One barrier per step.
+// among the current step's MFMAs.  One sync per step: a workgroup barrier,
+// a per-group LDS arrival counter, or for one-wave groups a wave-level
+// fence (step_sync below).
 constexpr int kTT = 128, kTK = 64, kTLD = kTK + 8;
 
 // K-groups per workgroup, waves (32-column strips) per group, 32-row MFMA
