@@ -1072,7 +1072,7 @@ constexpr char kManifest[] = R"JSON({
       "WN",
       "MI"
      ],
-     "when": "M > 16, and M <= 16 past the X-in-LDS kernel's K where the 32 x 32 grid fits on the CUs: 32 MI x 32 WN tiles, each wave a 32 MI x 32 column strip with its weights dequantised once into MFMA registers and X through LDS, KG K-groups of WN waves per workgroup; the finest of 32 x 32 (MI = 1, WN = 1, KG = 8), 32 x 64 (MI = 1), 64 x 64 (MI = 2) and 128 x 64 (MI = 4) tiles (WN = 2, KG = 4) whose cdiv(M, 32 MI) * cdiv(N, 32 WN) <= cus; when none fits: M >= 129 (NESO_AMD_W4_WIDE_TILE_MIN_M overrides): WN = 4, MI = 4, KG = 2 while cdiv(M, 128) * cdiv(N, 128) <= cus, else 1; 65 <= M <= 128: WN = 2, MI = 4, KG = 2; 33 <= M <= 64: WN = 2, MI = 2, KG = 4; 17 <= M <= 32: WN = 2, MI = 1, KG = 4; KG > 1 steps sync per K-group through LDS arrival counters when MI = 4 and cdiv(cdiv(K, 64), KG) >= 16, or cdiv(cdiv(K, 64), KG) >= 32 (NESO_AMD_W4_TILE_SYNC overrides), else through workgroup barriers; WN = 1 groups (one wave) sync through a wave-level fence only",
+     "when": "M > 16, and M <= 16 past the X-in-LDS kernel's K where the 32 x 32 grid fits on the CUs: 32 MI x 32 WN tiles, each wave a 32 MI x 32 column strip with its weights dequantised once into MFMA registers and X through LDS, KG K-groups of WN waves per workgroup; the finest of 32 x 32 (MI = 1, WN = 1, KG = 8), 32 x 64 (MI = 1), 64 x 64 (MI = 2) and 128 x 64 (MI = 4) tiles (WN = 2, KG = 4) whose cdiv(M, 32 MI) * cdiv(N, 32 WN) <= cus; when none fits: M >= 65 (NESO_AMD_W4_WIDE_TILE_MIN_M overrides): WN = 4, MI = 4, KG = 2 while cdiv(M, 128) * cdiv(N, 128) <= cus, else KG = 1 from M = 129 and WN = 2, MI = 4, KG = 2 below; 33 <= M <= 64: WN = 2, MI = 2, KG = 4; 17 <= M <= 32: WN = 2, MI = 1, KG = 4; KG > 1 steps sync per K-group through LDS arrival counters when MI = 4 and cdiv(cdiv(K, 64), KG) >= 16, or cdiv(cdiv(K, 64), KG) >= 32 (NESO_AMD_W4_TILE_SYNC overrides), else through workgroup barriers; WN = 1 groups (one wave) sync through a wave-level fence only",
      "threadgroup_size": "64 * WN * KG",
      "num_warps": "WN * KG",
      "grid": [

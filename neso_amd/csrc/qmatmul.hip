@@ -1208,8 +1208,10 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
   //   two workgroups per CU beyond (M = 144 39.2 us against 54.6 for the
   //   128 x 64 kernel; M = 160 36.5 against 49.3 for 128 x 64 tiles in two
   //   rounds);
-  // * 65 <= M <= 128: 128 x 64 tiles with two K-groups (N = 32768 M = 64
-  //   59.9 against 66.8 with four);
+  // * 65 <= M <= 128: the same 128 x 128 tiles with two K-groups while
+  //   they fit (N = 32768 M = 128 52.2 us, N = 24576 M = 100 44.1, against
+  //   61.5 and 52.4 for 128 x 64 tiles with two K-groups), else those
+  //   128 x 64 tiles;
   // * 33 <= M <= 64: 64 x 64 tiles (N = 32768 M = 64 42.8 against 55.6);
   // * 17 <= M <= 32: 32 x 64 tiles (N = 32768 M = 32 34.4 against 53.6).
   // From M = 17 the tile GEMM is ahead of the split-K skinny kernel on
@@ -1218,12 +1220,12 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
   // NESO_AMD_W4_TILE_GEMM = 0 turns the tile GEMM off; 1 / 2: 128 x 128
   // tiles with one / two K-groups; 3 / 4: 128 x 64 with two / four; 5:
   // 64 x 64 with four; 6: 32 x 64 with four; 7: 32 x 32 with eight.
-  // NESO_AMD_W4_WIDE_TILE_MIN_M moves the 128 / 129 boundary of the forms
-  // taken when no fine tile fits.
+  // NESO_AMD_W4_WIDE_TILE_MIN_M (65 by default) is the smallest M for which
+  // those 128 x 128 tiles are taken when no fine tile fits.
   const char* tile_env = getenv("NESO_AMD_W4_TILE_GEMM");
   const int tile_mode = tile_env ? atoi(tile_env) : -1;
   const char* wide_env = getenv("NESO_AMD_W4_WIDE_TILE_MIN_M");
-  const int wide_min_m = wide_env ? atoi(wide_env) : 129;
+  const int wide_min_m = wide_env ? atoi(wide_env) : 65;
   const int cus = device_cu_count();
   auto tiles_of = [&](int tm, int tn) { return ((a.M + tm - 1) / tm) * ((a.N + tn - 1) / tn); };
   const int fine = tiles_of(32, 32) <= cus    ? 7
@@ -1233,8 +1235,9 @@ hipError_t launch_w4a16(const W4Args& a, hipStream_t s) {
                                               : 0;
   const int mode = tile_mode >= 0      ? tile_mode
                    : fine              ? fine
-                   : a.M >= wide_min_m ? (tiles_of(128, 128) <= cus ? 2 : 1)
-                   : a.M > 64          ? 3
+                   : a.M >= wide_min_m && (a.M > 128 || tiles_of(128, 128) <= cus)
+                       ? (tiles_of(128, 128) <= cus ? 2 : 1)
+                   : a.M > 64 ? 3
                    : a.M > 32          ? 5
                                        : 6;
 

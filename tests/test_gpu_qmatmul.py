@@ -144,14 +144,17 @@ def test_small_m_both_regimes(gpu, monkeypatch, gemv_max_m, m, n, k):
     ({}, 160, 11008, "w4a16_tile_gemm_kernel", [2, 4, 4]),
     ({}, 1024, 4096, "w4a16_tile_gemm_kernel", [2, 4, 4]),
     ({}, 1200, 4096, "w4a16_tile_gemm_kernel", [1, 4, 4]),
+    ({}, 128, 32768, "w4a16_tile_gemm_kernel", [2, 4, 4]),
+    ({}, 100, 40960, "w4a16_tile_gemm_kernel", [2, 2, 4]),
+    ({"NESO_AMD_W4_WIDE_TILE_MIN_M": "129"}, 128, 32768, "w4a16_tile_gemm_kernel", [2, 2, 4]),
 ])
 def test_route_thresholds(gpu, monkeypatch, env, m, n, kernel, targs):
     """The kernels on each side of the skinny / tile GEMM threshold (M = 16
     / 17) and of the tile GEMM's tile shapes, for a 256-CU part: the finest
     of 32 x 32, 32 x 64, 64 x 64 and 128 x 64 tiles whose grid fits on the
-    CUs, else 128 x 128 from M = 129 (two K-groups while those tiles fit,
-    one beyond), 128 x 64 with two K-groups from M = 65, 64 x 64 from
-    M = 33; the NESO_AMD_W4_SKINNY_MAX_M, NESO_AMD_W4_TILE_GEMM and
+    CUs, else 128 x 128 from M = 65 while those tiles fit (from M = 129
+    with one K-group beyond), 128 x 64 with two K-groups for M = 65..128,
+    64 x 64 from M = 33; the NESO_AMD_W4_SKINNY_MAX_M, NESO_AMD_W4_TILE_GEMM and
     NESO_AMD_W4_WIDE_TILE_MIN_M overrides, and the skinny and 128 x 64
     kernels with the tile GEMM turned off."""
     for key, val in env.items():
